@@ -1,0 +1,138 @@
+/*
+ * llmserve_hip.h - C ABI of the MI355X (gfx950) quantized decode path.
+ *
+ * Every entry point takes plain device pointers, int64 sizes and a HIP stream passed as
+ * `void*` (NULL = the default stream). Work is enqueued on that stream and the call returns
+ * without synchronising. A nonzero status means nothing was launched (LLMSERVE_ERR_INVALID:
+ * an argument check failed, the same checks the reference makes with TORCH_CHECK) or the
+ * launch failed (LLMSERVE_ERR_HIP). `llmserve_last_error()` returns the calling thread's
+ * message for the last failure.
+ *
+ * The reference binds its CPU kernels through pybind11 (kernels/__init__.py:19-72 of
+ * Buland-Choudhary/llm-serving-engine, src/llmserve/); each function below names the
+ * reference interface it replaces. Tensors are row-major and contiguous. Device pointers for
+ * vector loads must be 16-byte aligned; the library checks and falls back to a scalar-load
+ * kernel where a shape or pointer does not allow them.
+ */
+#ifndef LLMSERVE_HIP_H
+#define LLMSERVE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLMSERVE_OK 0
+#define LLMSERVE_ERR_INVALID 1
+#define LLMSERVE_ERR_HIP 2
+
+/* Largest number of activation rows a GEMV call accepts. Replaces the reference's
+ * TORCH_CHECK(M <= 64) in int8_gemv.cpp:22 and int8_gemv.cpp:64. */
+#define LLMSERVE_GEMV_MAX_ROWS 64
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* llmserve_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int llmserve_abi_version(void);
+
+/* ---- quantize + pack (load time) ------------------------------------------------------ */
+
+/*
+ * Symmetric per-output-channel int8 (Int8Linear.__init__, quant.py:41-43):
+ *   scale[n] = max(amax_k |w[n,k]| / 127, 1e-8)
+ *   q[n,k]   = clamp(round_half_even(w[n,k] / scale[n]), -127, 127)
+ * w fp32 [N,K] -> q int8 [N,K], scale fp32 [N]. IEEE division, no contraction: bit-exact
+ * with the reference's torch CPU ops.
+ */
+int llmserve_int8_quantize(const float* w, int8_t* q, float* scale, int64_t N, int64_t K,
+                           void* stream);
+
+/*
+ * Asymmetric group-wise int4 with optional AWQ fold and nibble packing
+ * (Int4Linear.__init__ quant.py:94-121, _int4_quantize quant.py:82-90):
+ *   w'       = act_scale ? w * act_scale[None,:] : w
+ *   per group of `group_size` input channels: mn, mx of w'
+ *   scale    = max((mx - mn) / 15, 1e-8);  q = clamp(round_half_even((w' - mn) / scale), 0, 15)
+ *   zero     = mn + 8 * scale               (kernel convention w = (q - 8) * scale + zero)
+ *   nibbles[n, j] = q[n, 2j] | q[n, 2j+1] << 4
+ *   inv_act_scale[k] = 1 / act_scale[k]     (written when both pointers are non-NULL)
+ * w fp32 [N,K] -> nibbles uint8 [N,K/2], g_scale/g_zero fp32 [N,K/group_size].
+ * Requires K % group_size == 0 and group_size even (the reference raises ValueError /
+ * TORCH_CHECK otherwise, quant.py:100-101, int8_gemv.cpp:63).
+ */
+int llmserve_int4_quantize(const float* w, const float* act_scale /* nullable [K] */,
+                           uint8_t* nibbles, float* g_scale, float* g_zero,
+                           float* inv_act_scale /* nullable [K] */, int64_t N, int64_t K,
+                           int64_t group_size, void* stream);
+
+/*
+ * int8 KV-cache quantize + scatter (QuantizedKV.quantize/write, attention.py:153-162, with
+ * the key smoothing division of attention.py:243-245 fused when `smooth` is non-NULL):
+ *   x'          = smooth ? x / smooth[h, :] : x
+ *   s           = max(amax_d |x'[t,h,d]|, 1e-8) / 127
+ *   data[slot]  = clamp(round_half_even(x' / s), -127, 127);  scale[slot, h] = s
+ * x fp32 [T,Hk,D], slots int64 [T] -> data int8 [num_slots,Hk,D], scale fp32 [num_slots,Hk].
+ * Slots outside [0, num_slots) are skipped (torch.index_copy_ raises for them; the host
+ * wrappers check before calling). Duplicate slots race, as index_copy_ leaves them undefined.
+ */
+int llmserve_kv_quantize_write(const float* x, const int64_t* slots, const float* smooth,
+                               int8_t* data, float* scale, int64_t T, int64_t Hk, int64_t D,
+                               int64_t num_slots, void* stream);
+
+/* ---- weight-only quantized linears ------------------------------------------------------ */
+
+/*
+ * int8 weight-only GEMV for decode (replaces int8_linear, int8_gemv.cpp:13-46):
+ *   y[m,n] = scale[n] * sum_k x[m,k] * q[n,k]      (fp32 accumulate)
+ * x fp32 [M,K], q int8 [N,K], scale fp32 [N] -> y fp32 [M,N]; 1 <= M <= 64.
+ */
+int llmserve_int8_linear(const float* x, const int8_t* q, const float* scale, float* y,
+                         int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * int4 weight-only GEMV for decode (replaces int4_linear, int8_gemv.cpp:53-107, and fuses
+ * the AWQ activation pre-scale x * inv_act_scale of Int4Linear.forward, quant.py:137-138):
+ *   y[m,n] = sum_g s[n,g] * sum_{k in g} x'[m,k] q[n,k] + (z[n,g] - 8 s[n,g]) * sum_{k in g} x'[m,k]
+ *   x' = inv_act_scale ? x * inv_act_scale[None,:] : x
+ * x fp32 [M,K], nibbles uint8 [N,K/2], g_scale/g_zero fp32 [N,K/group] -> y fp32 [M,N].
+ */
+int llmserve_int4_linear(const float* x, const float* inv_act_scale /* nullable [K] */,
+                         const uint8_t* nibbles, const float* g_scale, const float* g_zero,
+                         float* y, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                         void* stream);
+
+/* ---- int8-KV paged decode attention ------------------------------------------------------ */
+
+/*
+ * Split-context paged decode over an int8 KV cache (replaces paged_attention_decode_int8 ->
+ * pa2::decode<int8_t>, paged_attention.cpp:141-346 and :361-376). For each sequence b, kv
+ * head h and the G = Hq/Hk query heads sharing it:
+ *   s_t   = scale * k_scale[slot_t,h] * (q'_g . k_cache[slot_t,h,:])
+ *   out_g = sum_t softmax(s)_t * v_scale[slot_t,h] * v_cache[slot_t,h,:]
+ *   q'    = q_mult ? q * q_mult : q            (key smoothing, attention.py:243-244)
+ *   slot_t = block_tables[b, t / block_size] * block_size + t % block_size
+ * q fp32 [B,Hq,D]; k/v_cache int8 [num_slots,Hk,D]; k/v_scale fp32 [num_slots,Hk];
+ * block_tables int64 [B,max_blocks]; context_lens int64 [B] -> out fp32 [B,Hq,D].
+ * partition_size: tokens per split-context partition (rounded up to a block multiple);
+ * 0 picks one for the GPU. Block ids outside [0, num_slots/block_size) contribute nothing;
+ * context lengths are clamped to max_blocks*block_size. A zero context yields NaN, as the
+ * reference's 0 * (1/0) does. `workspace` holds the per-partition (max, sum, acc) partials:
+ * at least llmserve_paged_attention_workspace_bytes(...) bytes (may be NULL when that is 0).
+ */
+int64_t llmserve_paged_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hk, int64_t D,
+                                                 int64_t max_blocks, int64_t block_size,
+                                                 int64_t partition_size);
+int llmserve_paged_attention_decode_int8(
+    const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
+    const float* v_scale, const int64_t* block_tables, const int64_t* context_lens, float* out,
+    int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots, int64_t max_blocks,
+    int64_t block_size, float scale, int64_t partition_size, const float* q_mult /* nullable */,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLMSERVE_HIP_H */

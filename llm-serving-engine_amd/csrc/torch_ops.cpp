@@ -1,0 +1,235 @@
+// Thin PyTorch binding of the C ABI (include/llmserve_hip.h) as torch.ops.llmserve_hip.*.
+//
+// Each op keeps the reference's Python-visible signature (int8_gemv.cpp:109-112,
+// paged_attention.cpp:386-399 of the reference) and argument checks, takes ROCm tensors,
+// allocates its outputs and workspaces with PyTorch's caching allocator and enqueues the
+// kernels on the current HIP stream of the input's device without synchronising.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "llmserve_hip.h"
+
+namespace {
+
+void* stream_of(const at::Tensor& t) {
+  return static_cast<void*>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
+}
+
+void check_status(int rc) {
+  TORCH_CHECK(rc == LLMSERVE_OK, llmserve_last_error());
+}
+
+void check_device(const at::Tensor& ref, std::initializer_list<const at::Tensor*> ts,
+                  const char* what) {
+  TORCH_CHECK(ref.is_cuda(), what, ": tensors must be on a ROCm device (got ", ref.device(), ")");
+  for (const at::Tensor* t : ts)
+    TORCH_CHECK(t->device() == ref.device(), what, ": all tensors must be on ", ref.device());
+}
+
+template <typename T>
+const T* opt_ptr(const std::optional<at::Tensor>& t) {
+  return t.has_value() ? t->data_ptr<T>() : nullptr;
+}
+
+// ---- quantize + pack ---------------------------------------------------------------------
+
+std::tuple<at::Tensor, at::Tensor> int8_quantize(const at::Tensor& w) {
+  TORCH_CHECK(w.dim() == 2 && w.scalar_type() == at::kFloat && w.is_contiguous(),
+              "int8_quantize: weight must be a contiguous float32 [out, in] tensor");
+  check_device(w, {}, "int8_quantize");
+  const c10::DeviceGuard guard(w.device());
+  const int64_t N = w.size(0), K = w.size(1);
+  auto q = at::empty({N, K}, w.options().dtype(at::kChar));
+  auto s = at::empty({N}, w.options());
+  check_status(llmserve_int8_quantize(w.data_ptr<float>(), q.data_ptr<int8_t>(), s.data_ptr<float>(),
+                                      N, K, stream_of(w)));
+  return {q, s};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> int4_quantize(
+    const at::Tensor& w, int64_t group_size, const std::optional<at::Tensor>& act_scale) {
+  TORCH_CHECK(w.dim() == 2 && w.scalar_type() == at::kFloat && w.is_contiguous(),
+              "int4_quantize: weight must be a contiguous float32 [out, in] tensor");
+  check_device(w, {}, "int4_quantize");
+  const int64_t N = w.size(0), K = w.size(1);
+  if (act_scale.has_value()) {
+    check_device(w, {&*act_scale}, "int4_quantize");
+    TORCH_CHECK(act_scale->scalar_type() == at::kFloat && act_scale->is_contiguous() &&
+                    act_scale->numel() == K,
+                "int4_quantize: act_scale must be a contiguous float32 [in] tensor");
+  }
+  TORCH_CHECK(group_size > 0 && K % group_size == 0, "in_features ", K,
+              " not divisible by group ", group_size);
+  const c10::DeviceGuard guard(w.device());
+  auto nib = at::empty({N, K / 2}, w.options().dtype(at::kByte));
+  auto gs = at::empty({N, K / group_size}, w.options());
+  auto gz = at::empty({N, K / group_size}, w.options());
+  auto inv = at::empty({act_scale.has_value() ? K : 0}, w.options());
+  check_status(llmserve_int4_quantize(w.data_ptr<float>(), opt_ptr<float>(act_scale),
+                                      nib.data_ptr<uint8_t>(), gs.data_ptr<float>(),
+                                      gz.data_ptr<float>(),
+                                      act_scale.has_value() ? inv.data_ptr<float>() : nullptr, N,
+                                      K, group_size, stream_of(w)));
+  return {nib, gs, gz, inv};
+}
+
+void kv_quantize_write(const at::Tensor& x, const at::Tensor& slots, at::Tensor& data,
+                       at::Tensor& scale, const std::optional<at::Tensor>& smooth) {
+  TORCH_CHECK(x.dim() == 3 && x.scalar_type() == at::kFloat && x.is_contiguous(),
+              "kv_quantize_write: x must be a contiguous float32 [T, Hk, D] tensor");
+  TORCH_CHECK(slots.dim() == 1 && slots.scalar_type() == at::kLong && slots.is_contiguous() &&
+                  slots.size(0) == x.size(0),
+              "kv_quantize_write: slots must be a contiguous int64 [T] tensor");
+  TORCH_CHECK(data.dim() == 3 && data.scalar_type() == at::kChar && data.is_contiguous() &&
+                  data.size(1) == x.size(1) && data.size(2) == x.size(2),
+              "kv_quantize_write: data must be a contiguous int8 [slots, Hk, D] tensor");
+  TORCH_CHECK(scale.dim() == 2 && scale.scalar_type() == at::kFloat && scale.is_contiguous() &&
+                  scale.size(0) == data.size(0) && scale.size(1) == x.size(1),
+              "kv_quantize_write: scale must be a contiguous float32 [slots, Hk] tensor");
+  check_device(x, {&slots, &data, &scale}, "kv_quantize_write");
+  if (smooth.has_value()) {
+    check_device(x, {&*smooth}, "kv_quantize_write");
+    TORCH_CHECK(smooth->scalar_type() == at::kFloat && smooth->is_contiguous() &&
+                    smooth->numel() == x.size(1) * x.size(2),
+                "kv_quantize_write: smooth must be a contiguous float32 [Hk, D] tensor");
+  }
+  const c10::DeviceGuard guard(x.device());
+  check_status(llmserve_kv_quantize_write(x.data_ptr<float>(), slots.data_ptr<int64_t>(),
+                                          opt_ptr<float>(smooth), data.data_ptr<int8_t>(),
+                                          scale.data_ptr<float>(), x.size(0), x.size(1),
+                                          x.size(2), data.size(0), stream_of(x)));
+}
+
+// ---- linears -------------------------------------------------------------------------------
+
+at::Tensor int8_linear(const at::Tensor& x, const at::Tensor& qweight, const at::Tensor& scale) {
+  TORCH_CHECK(x.scalar_type() == at::kFloat && qweight.scalar_type() == at::kChar &&
+                  scale.scalar_type() == at::kFloat,
+              "int8_linear: dtypes");
+  TORCH_CHECK(x.is_contiguous() && qweight.is_contiguous() && scale.is_contiguous(),
+              "int8_linear: contiguous inputs");
+  TORCH_CHECK(x.dim() == 2 && qweight.dim() == 2, "int8_linear: 2-D x and qweight");
+  check_device(x, {&qweight, &scale}, "int8_linear");
+  const int64_t M = x.size(0), K = x.size(1), N = qweight.size(0);
+  TORCH_CHECK(qweight.size(1) == K, "int8_linear: K mismatch");
+  TORCH_CHECK(scale.numel() == N, "int8_linear: scale must have one entry per output channel");
+  TORCH_CHECK(M <= LLMSERVE_GEMV_MAX_ROWS, "int8_linear: meant for small batches (M <= 64)");
+  const c10::DeviceGuard guard(x.device());
+  auto y = at::empty({M, N}, x.options());
+  check_status(llmserve_int8_linear(x.data_ptr<float>(), qweight.data_ptr<int8_t>(),
+                                    scale.data_ptr<float>(), y.data_ptr<float>(), M, N, K,
+                                    stream_of(x)));
+  return y;
+}
+
+at::Tensor int4_linear(const at::Tensor& x, const at::Tensor& nibbles, const at::Tensor& scale,
+                       const at::Tensor& zero, int64_t group_size,
+                       const std::optional<at::Tensor>& inv_act_scale) {
+  TORCH_CHECK(x.scalar_type() == at::kFloat && nibbles.scalar_type() == at::kByte, "int4: dtypes");
+  TORCH_CHECK(scale.scalar_type() == at::kFloat && zero.scalar_type() == at::kFloat, "int4: dtypes");
+  TORCH_CHECK(x.is_contiguous() && nibbles.is_contiguous() && scale.is_contiguous() &&
+                  zero.is_contiguous(),
+              "int4: contiguous inputs");
+  TORCH_CHECK(x.dim() == 2 && nibbles.dim() == 2, "int4: 2-D x and nibbles");
+  check_device(x, {&nibbles, &scale, &zero}, "int4_linear");
+  const int64_t M = x.size(0), K = x.size(1), N = nibbles.size(0);
+  TORCH_CHECK(group_size > 0, "int4: shapes");
+  const int64_t G = K / group_size;
+  TORCH_CHECK(nibbles.size(1) * 2 == K && G * group_size == K && group_size % 2 == 0, "int4: shapes");
+  TORCH_CHECK(scale.numel() == N * G && zero.numel() == N * G, "int4: scale/zero must be [N, G]");
+  TORCH_CHECK(M <= LLMSERVE_GEMV_MAX_ROWS, "int4_linear: meant for small batches (M <= 64)");
+  if (inv_act_scale.has_value()) {
+    check_device(x, {&*inv_act_scale}, "int4_linear");
+    TORCH_CHECK(inv_act_scale->scalar_type() == at::kFloat && inv_act_scale->is_contiguous() &&
+                    inv_act_scale->numel() == K,
+                "int4_linear: inv_act_scale must be a contiguous float32 [K] tensor");
+  }
+  const c10::DeviceGuard guard(x.device());
+  auto y = at::empty({M, N}, x.options());
+  check_status(llmserve_int4_linear(x.data_ptr<float>(), opt_ptr<float>(inv_act_scale),
+                                    nibbles.data_ptr<uint8_t>(), scale.data_ptr<float>(),
+                                    zero.data_ptr<float>(), y.data_ptr<float>(), M, N, K,
+                                    group_size, stream_of(x)));
+  return y;
+}
+
+// ---- int8-KV paged decode -------------------------------------------------------------------
+
+at::Tensor paged_attention_decode_int8(const at::Tensor& q, const at::Tensor& k_cache,
+                                       const at::Tensor& v_cache, const at::Tensor& k_scale,
+                                       const at::Tensor& v_scale, const at::Tensor& block_tables,
+                                       const at::Tensor& context_lens, int64_t block_size,
+                                       double scale, int64_t partition_size,
+                                       const std::optional<at::Tensor>& q_mult) {
+  TORCH_CHECK(k_cache.scalar_type() == at::kChar && v_cache.scalar_type() == at::kChar,
+              "paged_attention_decode_int8: int8 cache");
+  TORCH_CHECK(k_scale.scalar_type() == at::kFloat && v_scale.scalar_type() == at::kFloat &&
+                  k_scale.is_contiguous() && v_scale.is_contiguous(),
+              "paged_attention_decode_int8: float32 contiguous scales [num_slots, Hk]");
+  TORCH_CHECK(q.scalar_type() == at::kFloat, "paged_attention: q must be float32");
+  TORCH_CHECK(block_tables.scalar_type() == at::kLong && context_lens.scalar_type() == at::kLong,
+              "paged_attention: int64 block tables / context lens");
+  TORCH_CHECK(q.is_contiguous() && k_cache.is_contiguous() && v_cache.is_contiguous() &&
+                  block_tables.is_contiguous() && context_lens.is_contiguous(),
+              "paged_attention: inputs must be contiguous");
+  TORCH_CHECK(q.dim() == 3 && k_cache.dim() == 3 && v_cache.sizes() == k_cache.sizes(),
+              "paged_attention: q [B, Hq, D], caches [num_slots, Hk, D]");
+  TORCH_CHECK(block_tables.dim() == 2 && context_lens.dim() == 1 &&
+                  block_tables.size(0) == q.size(0) && context_lens.size(0) == q.size(0),
+              "paged_attention: block_tables [B, max_blocks], context_lens [B]");
+  check_device(q, {&k_cache, &v_cache, &k_scale, &v_scale, &block_tables, &context_lens},
+               "paged_attention_decode_int8");
+  const int64_t B = q.size(0), Hq = q.size(1), D = q.size(2);
+  const int64_t num_slots = k_cache.size(0), Hk = k_cache.size(1);
+  TORCH_CHECK(k_cache.size(2) == D, "paged_attention: head_dim mismatch");
+  TORCH_CHECK(k_scale.numel() == num_slots * Hk && v_scale.numel() == num_slots * Hk,
+              "paged_attention_decode_int8: float32 contiguous scales [num_slots, Hk]");
+  if (q_mult.has_value()) {
+    check_device(q, {&*q_mult}, "paged_attention_decode_int8");
+    TORCH_CHECK(q_mult->scalar_type() == at::kFloat && q_mult->is_contiguous() &&
+                    q_mult->numel() == Hq * D,
+                "paged_attention_decode_int8: q_mult must be a contiguous float32 [Hq, D] tensor");
+  }
+  const c10::DeviceGuard guard(q.device());
+  auto out = at::empty_like(q);
+  if (B == 0) return out;
+  const int64_t max_blocks = block_tables.size(1);
+  const int64_t ws_bytes = llmserve_paged_attention_workspace_bytes(B, Hq, Hk, D, max_blocks,
+                                                                    block_size, partition_size);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes / 4}, q.options());
+  check_status(llmserve_paged_attention_decode_int8(
+      q.data_ptr<float>(), k_cache.data_ptr<int8_t>(), v_cache.data_ptr<int8_t>(),
+      k_scale.data_ptr<float>(), v_scale.data_ptr<float>(), block_tables.data_ptr<int64_t>(),
+      context_lens.data_ptr<int64_t>(), out.data_ptr<float>(), B, Hq, Hk, D, num_slots,
+      max_blocks, block_size, static_cast<float>(scale), partition_size, opt_ptr<float>(q_mult),
+      ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q)));
+  return out;
+}
+
+}  // namespace
+
+TORCH_LIBRARY(llmserve_hip, m) {
+  m.def("int8_quantize(Tensor w) -> (Tensor, Tensor)");
+  m.def("int4_quantize(Tensor w, int group_size, Tensor? act_scale=None)"
+        " -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("kv_quantize_write(Tensor x, Tensor slots, Tensor(a!) data, Tensor(b!) scale,"
+        " Tensor? smooth=None) -> ()");
+  m.def("int8_linear(Tensor x, Tensor qweight, Tensor scale) -> Tensor");
+  m.def("int4_linear(Tensor x, Tensor nibbles, Tensor scale, Tensor zero, int group_size,"
+        " Tensor? inv_act_scale=None) -> Tensor");
+  m.def("paged_attention_decode_int8(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale,"
+        " Tensor v_scale, Tensor block_tables, Tensor context_lens, int block_size, float scale,"
+        " int partition_size=0, Tensor? q_mult=None) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
+  m.impl("int8_quantize", &int8_quantize);
+  m.impl("int4_quantize", &int4_quantize);
+  m.impl("kv_quantize_write", &kv_quantize_write);
+  m.impl("int8_linear", &int8_linear);
+  m.impl("int4_linear", &int4_linear);
+  m.impl("paged_attention_decode_int8", &paged_attention_decode_int8);
+}

@@ -1,0 +1,79 @@
+"""Loading of the in-tree gfx950 libraries.
+
+``ops()`` registers ``torch.ops.llmserve_hip.*`` (``libllmserve_torch.so``) and ``capi()``
+returns a ctypes handle on the C ABI of ``include/llmserve_hip.h`` (``libllmserve_hip.so``).
+Both raise ``NativeLibraryMissing`` when the libraries were not built: the quantized path
+has no CPU or PyTorch substitute, so a missing build must fail loudly rather than run
+something else.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+from pathlib import Path
+
+LIB_DIR = Path(__file__).resolve().parent / "_lib"
+HIP_LIB = LIB_DIR / "libllmserve_hip.so"
+TORCH_LIB = LIB_DIR / "libllmserve_torch.so"
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def _require(path: Path) -> Path:
+    if not path.is_file():
+        raise NativeLibraryMissing(
+            f"{path.name} is not built; run `python llm-serving-engine_amd/build.py` "
+            "(or __graft_entry__.build()) first"
+        )
+    return path
+
+
+@functools.cache
+def ops():
+    """The ``torch.ops.llmserve_hip`` namespace (loads the op library once)."""
+    import torch
+
+    torch.ops.load_library(str(_require(TORCH_LIB)))
+    return torch.ops.llmserve_hip
+
+
+# C ABI signatures, in the order of include/llmserve_hip.h.
+_P, _I64, _I32, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+C_SIGNATURES: dict[str, tuple[object, list]] = {
+    "llmserve_last_error": (ctypes.c_char_p, []),
+    "llmserve_abi_version": (_I32, []),
+    "llmserve_int8_quantize": (_I32, [_P, _P, _P, _I64, _I64, _P]),
+    "llmserve_int4_quantize": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "llmserve_kv_quantize_write": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "llmserve_int8_linear": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "llmserve_int4_linear": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "llmserve_paged_attention_workspace_bytes": (_I64, [_I64] * 7),
+    "llmserve_paged_attention_decode_int8": (
+        _I32,
+        [_P] * 8 + [_I64] * 7 + [_F32, _I64, _P, _P, _I64, _P],
+    ),
+}
+
+
+@functools.cache
+def capi() -> ctypes.CDLL:
+    """ctypes handle on libllmserve_hip.so with argument/return types set.
+
+    In a process that uses torch, import torch first so that the library binds to the HIP
+    runtime torch already loaded (both carry the SONAME libamdhip64.so.7).
+    """
+    lib = ctypes.CDLL(str(_require(HIP_LIB)))
+    for name, (res, args) in C_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def check(rc: int) -> None:
+    """Raises RuntimeError with the library's message for a nonzero C ABI status."""
+    if rc != 0:
+        raise RuntimeError(capi().llmserve_last_error().decode())

@@ -1,0 +1,51 @@
+"""Native kernel loaders (reference: src/llmserve/kernels/__init__.py:19-72).
+
+The reference JIT-compiles three CPU extensions and returns ``None`` when a build fails, so
+that callers fall back to PyTorch. Here the kernels are prebuilt gfx950 HIP code and there is
+no fallback: a missing library raises ``NativeLibraryMissing`` (a RuntimeError). The returned
+objects expose the reference's function names and signatures:
+
+* ``load_int8_gemv()``: ``int8_linear(x, qweight, scale)`` and
+  ``int4_linear(x, nibbles, scale, zero, group_size, inv_act_scale=None)``
+  (int8_gemv.cpp:109-112; ``inv_act_scale`` fuses Int4Linear's AWQ pre-scale);
+* ``load_paged_attention()``: ``paged_attention_decode_int8(q, k_cache, v_cache, k_scale,
+  v_scale, block_tables, context_lens, block_size, scale, partition_size=0, q_mult=None)``
+  (paged_attention.cpp:386-399; ``q_mult`` fuses the key-smoothing multiply of q).
+
+The fp32-KV decode variants (``paged_attention_decode``, ``paged_attention_decode_v1``,
+``set_simd``) and ``load_fused_ops`` are outside the quantized path and not provided.
+"""
+
+from __future__ import annotations
+
+import functools
+from types import SimpleNamespace
+
+from llmserve._native import NativeLibraryMissing, ops
+
+__all__ = ["NativeLibraryMissing", "load_int8_gemv", "load_paged_attention", "load_quant"]
+
+
+@functools.cache
+def load_int8_gemv() -> SimpleNamespace:
+    """Weight-only int8 / int4 small-batch matmuls (HIP, gfx950)."""
+    o = ops()
+    return SimpleNamespace(int8_linear=o.int8_linear, int4_linear=o.int4_linear)
+
+
+@functools.cache
+def load_paged_attention() -> SimpleNamespace:
+    """int8-KV paged decode attention (HIP, gfx950)."""
+    o = ops()
+    return SimpleNamespace(paged_attention_decode_int8=o.paged_attention_decode_int8)
+
+
+@functools.cache
+def load_quant() -> SimpleNamespace:
+    """Load-time quantizers and the int8 KV-cache write (HIP, gfx950)."""
+    o = ops()
+    return SimpleNamespace(
+        int8_quantize=o.int8_quantize,
+        int4_quantize=o.int4_quantize,
+        kv_quantize_write=o.kv_quantize_write,
+    )

@@ -1,0 +1,66 @@
+"""ORACLE (test infrastructure only) — float64 references of the path's mathematics.
+
+These fix what the kernels must compute independently of any summation order:
+  * weight-only linears: y = x @ W_deq^T with W_deq the float32 dequantized weight;
+  * paged decode: softmax(scale * q . k_deq) @ v_deq over each sequence's context, slots
+    from the block table.
+Pinned by tests/test_oracle_math.py with brute-force loops on tiny inputs, torch SDPA and
+closed forms (uniform attention, one-token contexts).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import quant as oq
+
+
+def linear_f64(x: np.ndarray, w_deq: np.ndarray) -> np.ndarray:
+    """y[m, n] = sum_k x[m, k] w[n, k] in float64."""
+    return np.asarray(x, np.float64) @ np.asarray(w_deq, np.float64).T
+
+
+def int8_linear_f64(x, q, scale):
+    return linear_f64(x, oq.int8_dequantize(q, scale))
+
+
+def int4_linear_f64(x, nib, g_scale, g_zero, group_size, inv_act_scale=None):
+    """Int4Linear.forward: x * inv_act_scale (float32), then x @ dequantize()^T."""
+    x = np.asarray(x, np.float32)
+    if inv_act_scale is not None:
+        x = (x * inv_act_scale[None, :]).astype(np.float32)
+    return linear_f64(x, oq.int4_dequantize(nib, g_scale, g_zero, group_size))
+
+
+def context_slots(table: np.ndarray, ctx: int, block_size: int) -> np.ndarray:
+    t = np.arange(ctx)
+    return table[t // block_size].astype(np.int64) * block_size + t % block_size
+
+
+def paged_decode_f64(q, k_deq, v_deq, block_tables, context_lens, block_size, scale):
+    """out[b, hq] = softmax_t(scale * q[b, hq] . k[slot_t, hq // G]) @ v[slot_t, hq // G].
+
+    q [B, Hq, D]; k_deq / v_deq [num_slots, Hk, D] (dequantized caches); returns float64.
+    """
+    q = np.asarray(q, np.float64)
+    B, Hq, D = q.shape
+    Hk = k_deq.shape[1]
+    G = Hq // Hk
+    out = np.zeros((B, Hq, D))
+    for b in range(B):
+        ctx = int(context_lens[b])
+        slots = context_slots(np.asarray(block_tables[b]), ctx, block_size)
+        kb = np.asarray(k_deq[slots], np.float64)  # [ctx, Hk, D]
+        vb = np.asarray(v_deq[slots], np.float64)
+        for hq in range(Hq):
+            h = hq // G
+            s = scale * (kb[:, h, :] @ q[b, hq])
+            s = s - s.max()
+            p = np.exp(s)
+            out[b, hq] = (p @ vb[:, h, :]) / p.sum()
+    return out
+
+
+def kv_dequantize(data: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """QuantizedKV.rows (reference attention.py:164-166): data * scale[..., None] in float32."""
+    return (data.astype(np.float32) * scale[..., None]).astype(np.float32)

@@ -1,0 +1,93 @@
+"""The C ABI library without a GPU: it loads, exports every function include/llmserve_hip.h
+declares, and its argument checks (the reference's TORCH_CHECKs) reject bad calls before
+anything is launched."""
+
+from __future__ import annotations
+
+import re
+
+import pytest
+
+from conftest import REPO
+
+HEADER = REPO / "include" / "llmserve_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"\b(llmserve_\w+)\s*\(", text)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from llmserve._native import capi
+
+    return capi()
+
+
+def test_every_declared_symbol_is_exported_and_typed(lib):
+    from llmserve._native import C_SIGNATURES
+
+    names = declared_functions()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in C_SIGNATURES, f"{n} has no ctypes signature"
+    assert set(C_SIGNATURES) == set(names)
+    assert lib.llmserve_abi_version() == 1
+
+
+def _err(lib) -> str:
+    return lib.llmserve_last_error().decode()
+
+
+def test_gemv_argument_checks(lib):
+    assert lib.llmserve_int8_linear(None, None, None, None, 65, 8, 16, None) == 1
+    assert "M <= 64" in _err(lib)
+    assert lib.llmserve_int8_linear(None, None, None, None, 0, 8, 16, None) == 0  # empty: no launch
+    assert lib.llmserve_int8_linear(None, None, None, None, 2, 8, 16, None) == 1
+    assert "null pointer" in _err(lib)
+    assert lib.llmserve_int4_linear(None, None, None, None, None, None, 1, 8, 100, 64, None) == 1
+    assert "int4: shapes" in _err(lib)
+    assert lib.llmserve_int4_linear(None, None, None, None, None, None, 1, 8, 96, 3, None) == 1
+
+
+def test_quantizer_argument_checks(lib):
+    assert lib.llmserve_int4_quantize(None, None, None, None, None, None, 4, 100, 64, None) == 1
+    assert "not divisible by group" in _err(lib)
+    assert lib.llmserve_int4_quantize(None, None, None, None, None, None, 4, 99, 33, None) == 1
+    assert lib.llmserve_int8_quantize(None, None, None, 0, 16, None) == 0
+    assert lib.llmserve_kv_quantize_write(None, None, None, None, None, 0, 2, 32, 64, None) == 0
+
+
+def test_paged_attention_argument_checks(lib):
+    f = lib.llmserve_paged_attention_decode_int8
+    args = [None] * 8
+    assert f(*args, 2, 6, 4, 32, 64, 4, 4, 0.1, 0, None, None, 0, None) == 1
+    assert "multiple of Hk" in _err(lib)
+    assert f(*args, 0, 8, 4, 32, 64, 4, 4, 0.1, 0, None, None, 0, None) == 0  # B == 0
+    assert f(*args, 2, 8, 4, 48, 64, 4, 4, 0.1, 0, None, None, 0, None) == 1
+    assert "head_dim" in _err(lib)
+    assert f(*args, 2, 72, 4, 32, 64, 4, 4, 0.1, 0, None, None, 0, None) == 1
+    assert "at most 8" in _err(lib)
+
+
+def test_paged_attention_workspace_size(lib):
+    ws = lib.llmserve_paged_attention_workspace_bytes
+    # one partition -> no workspace
+    assert ws(4, 16, 8, 128, 4, 16, 10_000) == 0
+    # forced 32-token partitions over a 256-token bound: NP = 8
+    assert ws(2, 16, 8, 128, 16, 16, 32) == 2 * 16 * 8 * (128 + 2) * 4
+    assert ws(0, 16, 8, 128, 16, 16, 32) == 0
+
+
+def test_single_hip_runtime_with_torch():
+    """The library binds to the HIP runtime torch loaded (both are libamdhip64.so.7)."""
+    import torch  # noqa: F401
+
+    from llmserve._native import capi, ops
+
+    ops()
+    capi()
+    maps = {line.split()[-1] for line in open("/proc/self/maps") if "libamdhip64" in line}
+    assert len(maps) == 1, maps

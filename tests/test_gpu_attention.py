@@ -1,0 +1,232 @@
+"""HIP int8-KV paged decode through the C ABI and the drop-in attention module.
+
+Tolerance: max-abs <= 1e-5 * max|out| and rel-L2 <= 1e-5 against the float64 attention over
+the dequantized cache (the reference's strongest pin, tests/test_attention.py:146-152, is
+1e-5), and against the reference kernel's own outputs (committed goldens) and the C
+restatement. At the BASELINE size (config 4) the C restatement is the checker, plus
+size-independent properties: partition-size invariance and relabelling of physical blocks.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import capi_util as cu
+from conftest import GOLDEN
+from oracle import cpu as ocpu
+from oracle import math_ref as mr
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def kg():
+    return dict(np.load(GOLDEN / "kernels_golden.npz"))
+
+
+def _golden_case(kg, name):
+    bs, sc = kg[f"{name}_meta"]
+    arrays = [kg[f"{name}_{k}"] for k in ("q", "kq", "vq", "ks", "vs", "bt", "cl")]
+    return arrays, int(bs), float(sc)
+
+
+@pytest.mark.parametrize("name,parts", [("pa_small", [0, 4, 8, 10000]), ("pa_d128", [0, 32, 64]),
+                                        ("pa_g1", [0, 16])])
+def test_reference_goldens(gpu, kg, name, parts):
+    arrays, bs, sc = _golden_case(kg, name)
+    q, kq, vq, ks, vs, bt, cl = arrays
+    ref64 = mr.paged_decode_f64(q, mr.kv_dequantize(kq, ks), mr.kv_dequantize(vq, vs), bt, cl, bs, sc)
+    dq = [cu.dev(a) for a in arrays]
+    for p in parts:
+        out = cu.paged_decode_int8(*dq, bs, sc, p)
+        cu.assert_rel_close(out, kg[f"{name}_out_p{p}"], 2 * TOL, f"{name} p={p} vs reference")
+        cu.assert_rel_close(out, ref64, TOL, f"{name} p={p} vs f64")
+
+
+def make_case(seed, B, Hq, Hk, D, bs, ctx_lo, ctx_hi, outlier=True, slack_blocks=3):
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(ctx_lo, ctx_hi + 1, B)
+    nblk = [-(-int(c) // bs) for c in ctx]
+    total = sum(nblk) + slack_blocks
+    perm = rng.permutation(total)
+    width = max(nblk)
+    bt = np.zeros((B, width), np.int64)
+    used = 0
+    for b, n in enumerate(nblk):
+        bt[b, :n] = perm[used:used + n]
+        used += n
+    k = rng.standard_normal((total * bs, Hk, D), dtype=F32)
+    if outlier:
+        k[..., 3] *= 40
+        k[..., D // 2 + 1] *= 25
+    v = rng.standard_normal((total * bs, Hk, D), dtype=F32)
+    sm = np.maximum(np.abs(k).max(0), F32(1e-5)).astype(F32)
+    sm = (sm / sm.mean(-1, keepdims=True)).astype(F32)
+    kq, ks = oq.kv_quantize(oq.kv_smooth(k, sm))
+    vq, vs = oq.kv_quantize(v)
+    q = rng.standard_normal((B, Hq, D)).astype(F32)
+    q_mult = np.repeat(sm, Hq // Hk, axis=0).astype(F32)
+    return dict(q=q, kq=kq, vq=vq, ks=ks, vs=vs, bt=bt, cl=ctx.astype(np.int64), q_mult=q_mult)
+
+
+@pytest.mark.parametrize("Hq,Hk,D,bs", [(16, 8, 128, 16), (8, 2, 32, 4), (9, 3, 64, 16),
+                                        (4, 4, 16, 8), (8, 1, 256, 16), (32, 4, 128, 32)])
+def test_geometries_vs_f64(gpu, Hq, Hk, D, bs):
+    c = make_case(Hq * 31 + D, 5, Hq, Hk, D, bs, 1, 300)
+    ref = mr.paged_decode_f64(oq.q_smooth(c["q"], c["q_mult"]), mr.kv_dequantize(c["kq"], c["ks"]),
+                              mr.kv_dequantize(c["vq"], c["vs"]), c["bt"], c["cl"], bs, D ** -0.5)
+    args = [cu.dev(c[k]) for k in ("q", "kq", "vq", "ks", "vs", "bt", "cl")]
+    for p in (0, bs, 64, 100000):
+        out = cu.paged_decode_int8(*args, bs, D ** -0.5, p, cu.dev(c["q_mult"]))
+        cu.assert_rel_close(out, ref, TOL, f"H{Hq}/{Hk} D{D} bs{bs} p{p}")
+
+
+def test_baseline_config4_size(gpu):
+    """16q/8kv heads, D=128, block 16, batch 32, ctx ~ U[512, 8192],
+    permuted blocks, outlier key channels with smoothing. Checked against the C restatement;
+    partition sizes agree and relabelling the physical blocks changes nothing."""
+    c = make_case(2024, 32, 16, 8, 128, 16, 512, 8192)
+    args = [cu.dev(c[k]) for k in ("q", "kq", "vq", "ks", "vs", "bt", "cl")]
+    qm = cu.dev(c["q_mult"])
+    sc = 128 ** -0.5
+    out = cu.paged_decode_int8(*args, 16, sc, 0, qm)
+    ref = ocpu.paged_decode_int8(c["q"], c["kq"], c["vq"], c["ks"], c["vs"], c["bt"], c["cl"], 16,
+                                 sc, 0, c["q_mult"])
+    cu.assert_rel_close(out, ref, 2 * TOL, "config 4 vs C restatement")
+    out2 = cu.paged_decode_int8(*args, 16, sc, 1024, qm)
+    cu.assert_rel_close(out2, out, 2 * TOL, "partition 1024 vs auto")
+    # relabel physical blocks: move every block to a new id
+    nb = c["kq"].shape[0] // 16
+    relabel = np.random.default_rng(1).permutation(nb)
+    inv = np.argsort(relabel)
+    kq2 = c["kq"].reshape(nb, 16, 8, 128)[inv].reshape(c["kq"].shape)
+    vq2 = c["vq"].reshape(nb, 16, 8, 128)[inv].reshape(c["vq"].shape)
+    ks2 = c["ks"].reshape(nb, 16, 8)[inv].reshape(c["ks"].shape)
+    vs2 = c["vs"].reshape(nb, 16, 8)[inv].reshape(c["vs"].shape)
+    bt2 = relabel[c["bt"]]
+    args2 = [cu.dev(a) for a in (c["q"], kq2, vq2, ks2, vs2, bt2, c["cl"])]
+    out3 = cu.paged_decode_int8(*args2, 16, sc, 0, qm)
+    assert torch.equal(out3, out)
+
+
+def test_edge_contexts(gpu):
+    """ctx = 1 returns the token's value row; ctx = 0 gives NaN (the reference's 0 * (1/0))."""
+    c = make_case(5, 3, 4, 2, 32, 4, 9, 9, outlier=False)
+    c["cl"][:] = [1, 0, 9]
+    args = [cu.dev(c[k]) for k in ("q", "kq", "vq", "ks", "vs", "bt", "cl")]
+    for p in (0, 4):
+        out = cu.paged_decode_int8(*args, 4, 0.2, p).cpu().numpy()
+        slot = c["bt"][0, 0] * 4
+        vrow = mr.kv_dequantize(c["vq"][slot], c["vs"][slot])
+        np.testing.assert_allclose(out[0], np.repeat(vrow, 2, axis=0), rtol=1e-6, atol=1e-6)
+        assert np.isnan(out[1]).all()
+        assert np.isfinite(out[2]).all()
+
+
+def test_invalid_block_ids_are_skipped(gpu):
+    c = make_case(6, 2, 8, 2, 32, 4, 12, 12, outlier=False)
+    bt = c["bt"].copy()
+    bt[0, 1] = 10**9  # out of range: those 4 tokens contribute nothing
+    args = [cu.dev(a) for a in (c["q"], c["kq"], c["vq"], c["ks"], c["vs"], bt, c["cl"])]
+    out = cu.paged_decode_int8(*args, 4, 0.2).cpu().numpy()
+    keep = np.array([0, 2])
+    bt_ok = c["bt"][:1, keep]
+    ref = mr.paged_decode_f64(c["q"][:1], mr.kv_dequantize(c["kq"], c["ks"]),
+                              mr.kv_dequantize(c["vq"], c["vs"]), bt_ok, np.array([8]), 4, 0.2)
+    cu.assert_rel_close(out[:1], ref, TOL)
+
+
+# ---- drop-in module tests (mirroring the reference's tests/test_attention.py) --------------
+
+def _int8_caches(kc, vc):
+    from llmserve.attention import QuantizedKV
+
+    kq, vq = QuantizedKV(*kc.shape, device=kc.device), QuantizedKV(*vc.shape, device=vc.device)
+    all_slots = torch.arange(kc.shape[0], device=kc.device)
+    kq.write(all_slots, kc)
+    vq.write(all_slots, vc)
+    return kq, vq
+
+
+def test_quantized_kv_roundtrip_error_is_bounded(gpu):
+    from llmserve.attention import QuantizedKV
+
+    x = torch.randn(64, 2, 32, device="cuda")
+    c = QuantizedKV(64, 2, 32, device="cuda")
+    c.write(torch.arange(64, device="cuda"), x)
+    err = (c.rows(torch.arange(64, device="cuda")) - x).abs()
+    assert (err <= c.scale[..., None] / 2 + 1e-6).all()
+    q, s = QuantizedKV.quantize(x)
+    assert torch.equal(q, c.data) and torch.equal(s, c.scale)
+
+
+@pytest.mark.parametrize("q_lens,ctx_lens", [([1, 1, 1], [5, 40, 17]), ([6, 1, 1], [6, 23, 9])])
+def test_int8_kv_attention_close_to_fp32(gpu, q_lens, ctx_lens):
+    from llmserve.attention import AttentionMetadata, QuantizedKV, paged_attention
+
+    g = torch.Generator().manual_seed(4)
+    hq, hk, d, bs = 8, 2, 32, 4
+    kc = torch.randn(64 * bs, hk, d, generator=g).cuda()
+    vc = torch.randn(64 * bs, hk, d, generator=g).cuda()
+    tables, used = [], 0
+    for c in ctx_lens:
+        n = -(-c // bs)
+        tables.append(list(range(used, used + n)))
+        used += n
+    T = sum(q_lens)
+    q, k, v = (torch.randn(T, h, d, generator=g).cuda() for h in (hq, hk, hk))
+    ref_meta = AttentionMetadata.build(q_lens, ctx_lens, tables, bs, device="cuda", backend="torch")
+    ref = paged_attention(q, k, v, kc.clone(), vc.clone(), ref_meta, d**-0.5)
+    meta = AttentionMetadata.build(q_lens, ctx_lens, tables, bs, device="cuda", backend="hip")
+    kq, vq = _int8_caches(kc, vc)
+    out = paged_attention(q, k, v, kq, vq, meta, d**-0.5)
+    rel = (out - ref).norm() / ref.norm()
+    assert rel < 0.02, rel
+    # the int8 kernel equals attention over the dequantized cache (same math)
+    all_slots = torch.arange(kc.shape[0], device="cuda")
+    kd, vd = kq.rows(all_slots), vq.rows(all_slots)
+    kr, vr = ((lambda t: t[0].float() * t[1][..., None])(QuantizedKV.quantize(x)) for x in (k, v))
+    deq = paged_attention(q, kr, vr, kd, vd, ref_meta, d**-0.5)
+    torch.testing.assert_close(out, deq, atol=1e-5, rtol=1e-5)
+
+
+def test_k_smoothing_reduces_int8_error_with_outlier_channels(gpu):
+    from llmserve.attention import AttentionMetadata, QuantizedKV, paged_attention
+
+    g = torch.Generator().manual_seed(5)
+    hq, hk, d, bs = 8, 2, 32, 4
+    n = 40 * bs
+    kc = torch.randn(n, hk, d, generator=g)
+    kc[..., 3] *= 40.0
+    kc[..., 17] *= 25.0
+    kc = kc.cuda()
+    vc = torch.randn(n, hk, d, generator=g).cuda()
+    ctx = [37, 60, 11]
+    tables, used = [], 0
+    for c in ctx:
+        m = -(-c // bs)
+        tables.append(list(range(used, used + m)))
+        used += m
+    q = (torch.randn(len(ctx), hq, d, generator=g) * 0.2).cuda()
+    k, v = torch.randn(len(ctx), hk, d, generator=g).cuda(), torch.randn(len(ctx), hk, d, generator=g).cuda()
+    ref_meta = AttentionMetadata.build([1] * 3, ctx, tables, bs, device="cuda", backend="torch")
+    ref = paged_attention(q, k, v, kc.clone(), vc.clone(), ref_meta, d**-0.5)
+    meta = AttentionMetadata.build([1] * 3, ctx, tables, bs, device="cuda", backend="hip")
+
+    def run(smooth):
+        kq, vq = QuantizedKV(n, hk, d, device="cuda"), QuantizedKV(n, hk, d, device="cuda")
+        if smooth is not None:
+            kq.set_smoothing(smooth, hq)
+        kq.write(torch.arange(n, device="cuda"), kc / (smooth if smooth is not None else 1.0))
+        vq.write(torch.arange(n, device="cuda"), vc)
+        out = paged_attention(q, k, v, kq, vq, meta, d**-0.5)
+        return ((out - ref).norm() / ref.norm()).item()
+
+    s = kc.abs().amax(0).sqrt()
+    s = s / s.mean(-1, keepdim=True)
+    assert run(s) < 0.5 * run(None)

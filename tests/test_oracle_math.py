@@ -1,0 +1,70 @@
+"""Pins of the float64 references (oracle/math_ref.py), CPU only: brute-force loops, torch
+SDPA in float64 and closed forms."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import math_ref as mr
+from oracle import quant as oq
+
+
+def test_linear_brute_force():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((3, 7)).astype(np.float32)
+    q, s = oq.int8_quantize(rng.standard_normal((5, 7)).astype(np.float32))
+    y = mr.int8_linear_f64(x, q, s)
+    for m in range(3):
+        for n in range(5):
+            # the dequantized weight is the float32 product q * scale (quant.py:79)
+            w = [float(np.float32(q[n, k]) * s[n]) for k in range(7)]
+            assert abs(y[m, n] - sum(float(x[m, k]) * w[k] for k in range(7))) < 1e-9
+
+
+def test_int4_awq_prescale_applied_once():
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((4, 64)) * 0.02).astype(np.float32)
+    act = np.abs(rng.standard_normal(64)).astype(np.float32) + 0.5
+    nib, gs, gz, inv = oq.int4_quantize_pack(w, 32, act)
+    x = rng.standard_normal((2, 64)).astype(np.float32)
+    y = mr.int4_linear_f64(x, nib, gs, gz, 32, inv)
+    # (x / s) @ Q(W s)^T ~= x @ W^T within int4 rounding of the scaled weight
+    deq = oq.int4_dequantize(nib, gs, gz, 32) * inv[None, :]
+    np.testing.assert_allclose(y, x.astype(np.float64) @ deq.T.astype(np.float64), rtol=1e-5, atol=1e-6)
+
+
+def _paged_case(seed, B=3, Hq=4, Hk=2, D=16, bs=4, nblk=16):
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((nblk * bs, Hk, D)).astype(np.float32)
+    v = rng.standard_normal((nblk * bs, Hk, D)).astype(np.float32)
+    bt = rng.permutation(nblk)[: B * 4].reshape(B, 4).astype(np.int64)
+    cl = np.array([13, 1, 16], np.int64)[:B]
+    q = rng.standard_normal((B, Hq, D)).astype(np.float32)
+    return q, k, v, bt, cl, bs
+
+
+def test_paged_decode_matches_sdpa():
+    q, k, v, bt, cl, bs = _paged_case(0)
+    out = mr.paged_decode_f64(q, k, v, bt, cl, bs, 0.3)
+    G = q.shape[1] // k.shape[1]
+    for b in range(q.shape[0]):
+        slots = mr.context_slots(bt[b], int(cl[b]), bs)
+        kb = torch.from_numpy(k[slots]).double().repeat_interleave(G, 1).transpose(0, 1)
+        vb = torch.from_numpy(v[slots]).double().repeat_interleave(G, 1).transpose(0, 1)
+        qb = torch.from_numpy(q[b]).double()[:, None, :]
+        ref = torch.nn.functional.scaled_dot_product_attention(qb, kb, vb, scale=0.3)[:, 0]
+        np.testing.assert_allclose(out[b], ref.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_paged_decode_closed_forms():
+    q, k, v, bt, cl, bs = _paged_case(1)
+    # one-token context: the output is that token's value row
+    out = mr.paged_decode_f64(q, k, v, bt, cl, bs, 0.3)
+    s0 = bt[1, 0] * bs
+    np.testing.assert_allclose(out[1], np.repeat(v[s0], 2, axis=0), rtol=0, atol=1e-12)
+    # identical keys: uniform weights -> mean of the value rows
+    k_same = np.broadcast_to(k[:1], k.shape).copy()
+    out = mr.paged_decode_f64(q, k_same, v, bt, cl, bs, 0.3)
+    slots = mr.context_slots(bt[0], int(cl[0]), bs)
+    np.testing.assert_allclose(out[0], np.repeat(v[slots].astype(np.float64).mean(0), 2, axis=0), atol=1e-12)
