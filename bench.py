@@ -1,0 +1,374 @@
+"""Benchmark of the quantized decode path on one MI355X (BASELINE config 2 as the headline).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+One step = one decode token (M = 1) through the weight-only int4 (group 128, AWQ-scaled)
+linears of all 28 Qwen3-0.6B layers: fused qkv 1024->4096, o 2048->1024, gate_up 1024->6144,
+down 3072->1024 — 112 GEMV launches with distinct weights, replayed from a HIP graph. Four
+distinct copies of the model's quantized linears (4 x 250 MB) rotate between steps, so the
+weights stream from HBM and not from the 256 MB Infinity Cache. Inputs are resident in HBM
+before the timed region; weights are random N(0, 0.02), activations N(0, 1) with 1% of the
+input channels x20, AWQ scales from the reference's grid search on 512 such rows.
+
+`value` = algorithmic bytes per step (packed weights + group scales/zeros + inv_act_scale +
+x + y) x steps / wall time of the K timed steps. `roofline` is for the dominant kernel (the
+gate_up GEMV): its algorithmic bytes per launch over its average launch duration, measured
+here with HIP events on the stream it runs on. `cpu_baseline` times the reference's own CPU
+kernels (oracle/_ref, built from the reference sources) — or the oracle's C restatement where
+that build is absent — on the host cores, on the same quantized weights, for about 10 s.
+Extra fields report M = 4 / 16 steps and configs 1 (int8 GEMV) and 4 (int8-KV decode).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO, REPO / "llm-serving-engine_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0
+LAYERS = 28
+SHAPES = {"qkv": (4096, 1024), "o": (1024, 2048), "gate_up": (6144, 1024), "down": (1024, 3072)}
+GROUP = 128
+COPIES = 4
+METRIC = "quantized GEMV GB/s & % HBM peak (Qwen3-0.6B shapes); quantized decode tok/s"
+
+
+def int4_bytes(N: int, K: int, M: int) -> int:
+    """Algorithmic bytes of one int4 GEMV: nibbles + fp32 scale/zero per group +
+    inv_act_scale + x + y."""
+    return N * K // 2 + 8 * N * (K // GROUP) + 4 * K + 4 * M * K + 4 * M * N
+
+
+def int8_bytes(N: int, K: int, M: int) -> int:
+    return N * K + 4 * N + 4 * M * K + 4 * M * N
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_weights(torch, dev, seed: int = 0):
+    """COPIES x LAYERS x 4 int4 AWQ linears, quantized on the GPU."""
+    from llmserve.kernels import load_quant
+    from llmserve.quant import _search_awq_scale
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    calib = {}
+    for name, (N, K) in SHAPES.items():
+        x = torch.randn(512, K, device=dev, generator=g)
+        outl = torch.randperm(K, device=dev, generator=g)[: K // 100]
+        x[:, outl] *= 20.0
+        calib[name] = x
+    model = []
+    for c in range(COPIES):
+        layers = []
+        for layer in range(LAYERS):
+            lin = {}
+            for name, (N, K) in SHAPES.items():
+                w = torch.randn(N, K, device=dev, generator=g) * 0.02
+                s = _search_awq_scale(w, calib[name], GROUP)
+                lin[name] = load_quant().int4_quantize(w, GROUP, s)
+                del w
+            layers.append(lin)
+        model.append(layers)
+        log(f"[bench] quantized copy {c + 1}/{COPIES}")
+    return model, calib
+
+
+def make_inputs(torch, dev, calib, M: int):
+    return {name: calib[name][:M].contiguous() for name in SHAPES}
+
+
+def capture_steps(torch, model, xs, gemv):
+    """One HIP graph per weight copy, each holding the 112 launches of one step."""
+    graphs, outs = [], []
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm the op (allocator) outside capture
+        for name in SHAPES:
+            nib, gs, gz, inv = model[0][0][name]
+            gemv.int4_linear(xs[name], nib, gs, gz, GROUP, inv)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for layers in model:
+        g = torch.cuda.CUDAGraph()
+        ys = []
+        with torch.cuda.graph(g):
+            for lin in layers:
+                for name in SHAPES:
+                    nib, gs, gz, inv = lin[name]
+                    ys.append(gemv.int4_linear(xs[name], nib, gs, gz, GROUP, inv))
+        graphs.append(g)
+        outs.append(ys)
+    torch.cuda.synchronize()
+    return graphs, outs
+
+
+def time_graphs(torch, graphs, steps: int, warmup: int) -> tuple[float, float]:
+    """(wall seconds, GPU event seconds) for `steps` replays after `warmup`."""
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return t1 - t0, e0.elapsed_time(e1) / 1e3
+
+
+def kernel_avg_us(torch, launch, n: int) -> float:
+    """Average duration of single launches, each bracketed by HIP events on the current
+    stream (the stream the op launches on)."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n)]
+    for i in range(3):
+        launch(i)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        launch(i)
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / n * 1e3
+
+
+def read_traffic(kernel: str) -> dict | None:
+    """HBM bytes per launch from the committed PMC summary (profiles/roofline_traffic.md):
+    a markdown table row `| kernel | fetch_bytes | write_bytes | ... |`."""
+    p = REPO / "profiles" / "roofline_traffic.md"
+    if not p.is_file():
+        return None
+    for line in p.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[0] == kernel:
+            try:
+                return {"fetch": float(cells[1]), "write": float(cells[2])}
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(torch, model, calib, budget_s: float = 10.0) -> dict:
+    """The reference's CPU int4 kernel (Int4Linear.forward's small-batch path: x * inv then
+    int4_linear) over one copy of the 112 linears, M = 1, for about `budget_s` seconds."""
+    import numpy as np
+
+    from oracle import cpu as ocpu
+
+    host = [{n: tuple(t.cpu() for t in lin[n]) for n in SHAPES} for lin in model[0]]
+    xs = {n: calib[n][:1].cpu().contiguous() for n in SHAPES}
+    kind, fn = "port", None
+    try:
+        if ocpu.ref_available():
+            mod = ocpu.ref_module("llmserve_int8_gemv")
+            kind = "reference"
+
+            def fn(x, nib, gs, gz, inv):
+                return mod.int4_linear((x * inv).contiguous(), nib, gs, gz, GROUP)
+    except Exception as e:  # pragma: no cover - depends on the box
+        log(f"[bench] reference CPU kernels unavailable ({e}); timing the C restatement")
+    if fn is None:
+        def fn(x, nib, gs, gz, inv):
+            return ocpu.int4_linear(x.numpy(), nib.numpy(), gs.numpy(), gz.numpy(), GROUP,
+                                    inv.numpy())
+    step_bytes = LAYERS * sum(int4_bytes(N, K, 1) for N, K in SHAPES.values())
+
+    def step():
+        for lin in host:
+            for n in SHAPES:
+                nib, gs, gz, inv = lin[n]
+                fn(xs[n], nib, gs, gz, inv)
+
+    step()  # warm-up
+    steps, t0 = 0, time.perf_counter()
+    best = float("inf")
+    while time.perf_counter() - t0 < budget_s:
+        t = time.perf_counter()
+        step()
+        best = min(best, time.perf_counter() - t)
+        steps += 1
+    elapsed = time.perf_counter() - t0
+    threads = torch.get_num_threads() if kind == "reference" else ocpu.get_threads()
+    return {
+        "value": round(step_bytes * steps / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"{steps} steps x 112 int4 g128 GEMVs (M=1, all 28 Qwen3-0.6B layers, one "
+                   f"250 MB weight copy), {elapsed:.1f} s; best step {best * 1e3:.1f} ms; host "
+                   f"{os.cpu_count()} logical CPUs, ISA {ocpu.host_isa()}"),
+    }
+
+
+def extra_configs(torch, dev) -> dict:
+    """Kernel-level GB/s for BASELINE configs 1 (int8 GEMV) and 4 (int8-KV paged decode)."""
+    import numpy as np
+
+    from llmserve.kernels import load_int8_gemv, load_paged_attention, load_quant
+
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(1)
+    N, K = 6144, 1024
+    qs = [load_quant().int8_quantize(torch.randn(N, K, device=dev, generator=g) * 0.02)
+          for _ in range(160)]  # 1 GB of int8 weights
+    x = torch.randn(1, K, device=dev, generator=g)
+    gemv = load_int8_gemv()
+    us = kernel_avg_us(torch, lambda i: gemv.int8_linear(x, *qs[i % len(qs)]), 200)
+    b = int8_bytes(N, K, 1)
+    out["c1_int8_gemv"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                           "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}
+    del qs
+    # config 4
+    rng = np.random.default_rng(2024)
+    B, Hq, Hk, D, bs = 32, 16, 8, 128, 16
+    ctx = rng.integers(512, 8193, B)
+    nblk = -(-ctx // bs)
+    total = int(nblk.sum())
+    width = int(nblk.max())
+    copies = []
+    for c in range(4):  # 4 x ~300 MB of cache
+        perm = rng.permutation(total)
+        bt = np.zeros((B, width), np.int64)
+        used = 0
+        for i, n in enumerate(nblk):
+            bt[i, :n] = perm[used:used + n]
+            used += n
+        kq = torch.randint(-127, 128, (total * bs, Hk, D), dtype=torch.int8, device=dev)
+        vq = torch.randint(-127, 128, (total * bs, Hk, D), dtype=torch.int8, device=dev)
+        ks = torch.rand(total * bs, Hk, device=dev) * 0.05
+        vs = torch.rand(total * bs, Hk, device=dev) * 0.05
+        copies.append((kq, vq, ks, vs, torch.from_numpy(bt).to(dev)))
+    q = torch.randn(B, Hq, D, device=dev)
+    cl = torch.from_numpy(ctx.astype(np.int64)).to(dev)
+    qm = torch.rand(Hq, D, device=dev) + 0.5
+    pa = load_paged_attention()
+
+    def launch(i):
+        kq, vq, ks, vs, bt = copies[i % len(copies)]
+        pa.paged_attention_decode_int8(q, kq, vq, ks, vs, bt, cl, bs, D ** -0.5, 0, qm)
+
+    us = kernel_avg_us(torch, launch, 40)
+    b = int(ctx.sum()) * Hk * (2 * D + 8) + 8 * B * Hq * D + 8 * int(nblk.sum()) + 4 * Hq * D
+    out["c4_int8kv_paged_decode"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                                     "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 1 and 4")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run --gpus 1)",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    from llmserve.kernels import load_int8_gemv
+
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    log("[bench] quantizing 4 copies of the Qwen3-0.6B linears (int4 g128 AWQ)")
+    model, calib = build_weights(torch, dev)
+    gemv = load_int8_gemv()
+
+    by_rows = {}
+    headline = None
+    for M in (1, 4, 16):
+        xs = make_inputs(torch, dev, calib, M)
+        graphs, _ = capture_steps(torch, model, xs, gemv)
+        steps = args.steps if M == 1 else max(20, args.steps // 4)
+        wall, gpu = time_graphs(torch, graphs, steps, args.warmup)
+        step_bytes = LAYERS * sum(int4_bytes(N, K, M) for N, K in SHAPES.values())
+        gbs = step_bytes * steps / wall / 1e9
+        by_rows[str(M)] = {"GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                           "ms_per_step": round(wall / steps * 1e3, 4),
+                           "gpu_ms_per_step": round(gpu / steps * 1e3, 4), "bytes": step_bytes}
+        if M == 1:
+            headline = (gbs, wall / steps * 1e3, steps, step_bytes)
+        del graphs
+        log(f"[bench] M={M}: {by_rows[str(M)]}")
+
+    # dominant kernel: the gate_up GEMV at M = 1
+    N, K = SHAPES["gate_up"]
+    xs = make_inputs(torch, dev, calib, 1)
+    order = [(c, l) for l in range(LAYERS) for c in range(COPIES)]
+
+    def gate_up(i):
+        c, l = order[i % len(order)]
+        nib, gs, gz, inv = model[c][l]["gate_up"]
+        gemv.int4_linear(xs["gate_up"], nib, gs, gz, GROUP, inv)
+
+    avg_us = kernel_avg_us(torch, gate_up, 224)
+    kb = int4_bytes(N, K, 1)
+    achieved = kb / avg_us / 1e3
+    traffic = read_traffic("int4_gemv_fast gate_up M=1")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": None if traffic is None else int(traffic["fetch"] + traffic["write"]),
+                "kernel": "int4_gemv_fast<1,8,4> (gate_up 1024->6144, M=1)",
+                "bytes_per_launch": kb, "avg_launch_us": round(avg_us, 3)}
+    log(f"[bench] roofline: {roofline}")
+
+    extra = {} if args.no_extra else extra_configs(torch, dev)
+    if extra:
+        log(f"[bench] extra: {extra}")
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline (about 10 s)")
+        cpu = cpu_baseline(torch, model, calib)
+        log(f"[bench] cpu: {cpu}")
+
+    gbs, ms, steps, step_bytes = headline
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": ("config 2: int4 g128 AWQ weight-only GEMV through all 28 Qwen3-0.6B "
+                         "layers (qkv 1024->4096, o 2048->1024, gate_up 1024->6144, down "
+                         "3072->1024), M=1, 4 rotating weight copies, HIP graph per step"),
+            "model_shapes": "Qwen3-0.6B",
+            "group_size": GROUP,
+            "rows": 1,
+            "bytes_per_step": step_bytes,
+            "parallelism": "single GPU",
+        },
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "by_rows": by_rows,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

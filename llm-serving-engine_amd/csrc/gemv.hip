@@ -1,61 +1,49 @@
-// Weight-only int8 / int4 GEMV for decode (M <= 16 per launch; the host loops over row tiles
-// up to the 64-row limit).
+// Weight-only int8 / int4 GEMV for decode (M <= 16 activation rows per launch; the host
+// loops over row tiles up to the 64-row limit).
 //
-// Decode is HBM-bound: each weight byte is read once, dequantized in registers and used for
-// all M activation rows. Layout of the work:
-//  * a 256-thread workgroup = 4 wavefronts; wavefront w owns R consecutive output rows;
-//  * a row is streamed in segments of 64*V bytes: lane l loads bytes [l*V, l*V+V) of each
-//    segment with one V-byte (dwordx4 / dwordx2 / dword) load, so every wave-level load is
-//    one fully coalesced 64*V-byte run;
-//  * the activations x (M x K fp32) are either staged once per workgroup in LDS (the int4
-//    AWQ pre-scale x * inv_act_scale is applied while staging) or read directly from the
-//    L1/L2-resident copy;
-//  * each lane keeps R x MT partial sums; a butterfly over the 64 lanes (DPP/permute
-//    shuffles) finishes the K reduction.
+// Decode is bound by HBM and, at the Qwen3-0.6B layer sizes (1-6 MB per matrix), by the
+// latency of one kernel: a plain read of 4 MB takes ~2.3 us on MI355X (a null kernel ~1.6 us),
+// and it is fastest with many small wavefronts that each issue one 16-byte load per lane.
+// The kernels are laid out for that:
+//  * every lane loads 16 weight bytes per load (global_load_dwordx4, non-temporal): 16 int8
+//    or 32 int4 input channels;
+//  * LPR lanes (16, 32 or 64) cover LPR*16 bytes of one output row; a wavefront holds
+//    64/LPR row slots, so one wave-level load reads 64/LPR consecutive rows = 1 KB of
+//    contiguous weights when a row is LPR*16 bytes long;
+//  * a wavefront owns R such row groups; a 256-thread workgroup is 4 wavefronts;
+//  * the activations x (M x K fp32, a few KB) are staged once per workgroup in LDS (the
+//    int4 AWQ pre-scale x * inv_act_scale is applied while staging) or, for M <= 2, read
+//    directly from L1/L2; every row slot of the wave reuses the same x slice;
+//  * partial sums are finished with xor-shuffles over the LPR lanes of a row.
 // The int4 path uses the reference's group decomposition
-//   y = sum_g s * sum_{k in g} x q + (z - 8 s) * sum_{k in g} x   (int8_gemv.cpp:48-52)
-// evaluated per lane slice (2V input channels, always inside one group).
-// Shapes that do not meet the fast path's divisibility/alignment go to a generic kernel
-// with scalar loads.
+//   y = sum_g s * sum_{k in g} x q + (z - 8 s) * sum_{k in g} x     (int8_gemv.cpp:48-52)
+// per 32-channel lane slice, which always lies inside one quantization group (group % 32 == 0).
+// Shapes the fast path cannot tile go to a generic kernel with scalar loads.
 #include "common.h"
 
 namespace {
 
 using lsh::kWave;
 constexpr int kWaves = 4;
+constexpr int kLdsBudget = 64 * 1024;  // bytes of staged x per workgroup
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-template <int V>
-struct Vec;
-template <>
-struct Vec<16> {
-  using T = u32x4;
-  static constexpr int kWords = 4;
-};
-template <>
-struct Vec<8> {
-  using T = u32x2;
-  static constexpr int kWords = 2;
-};
-template <>
-struct Vec<4> {
-  using T = uint32_t;
-  static constexpr int kWords = 1;
+struct GemvArgs {
+  const float* x;      // [M, K]
+  const float* inv;    // [K] int4 AWQ pre-scale, or null
+  const uint8_t* w;    // int8 [N, K] or nibbles [N, K/2]
+  const float* s;      // int8: scale [N]; int4: g_scale [N, G]
+  const float* z;      // int4: g_zero [N, G]
+  float* y;            // [M, N]
+  int M, N, K, group, KC;
 };
 
-__device__ __forceinline__ uint32_t word(const u32x4& v, int i) { return v[i]; }
-__device__ __forceinline__ uint32_t word(const u32x2& v, int i) { return v[i]; }
-__device__ __forceinline__ uint32_t word(const uint32_t& v, int) { return v; }
-
-// Streaming (non-temporal) load of one lane's V weight bytes: weights are read once per call.
-template <int V>
-__device__ __forceinline__ typename Vec<V>::T load_vec(const uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const typename Vec<V>::T*>(p));
+__device__ __forceinline__ u32x4 load16(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
-// Nibbles of byte b of word u: channel 2b (low) and 2b+1 (high) of the word's 8 channels.
+// Channels 2b (low nibble) and 2b+1 (high nibble) of byte b, for the 4 bytes of u.
 __device__ __forceinline__ void unpack_nibbles(uint32_t u, float (&q)[8]) {
   const uint32_t lo = u & 0x0f0f0f0fu, hi = (u >> 4) & 0x0f0f0f0fu;
 #pragma unroll
@@ -65,14 +53,9 @@ __device__ __forceinline__ void unpack_nibbles(uint32_t u, float (&q)[8]) {
   }
 }
 
-// Sums acc[i] over the wave and stores lane-0's totals through `store(i, value)`.
-template <int NV, typename F>
-__device__ __forceinline__ void wave_reduce_store(float (&acc)[NV], int lane, F store) {
+__device__ __forceinline__ void unpack_int8(uint32_t u, float (&q)[4]) {
 #pragma unroll
-  for (int i = 0; i < NV; ++i) acc[i] = lsh::wave_sum_from<1>(acc[i]);
-#pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (lane == (i & (kWave - 1))) store(i, acc[i]);
+  for (int b = 0; b < 4; ++b) q[b] = static_cast<float>(static_cast<int8_t>((u >> (8 * b)) & 0xffu));
 }
 
 // Stages x[0:M, c0:c0+width] (times inv[k] when given) into LDS as fp32 rows of stride KC
@@ -100,14 +83,13 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x,
   }
 }
 
-// With XLDS, xs holds the staged chunk [MT][KC] starting at channel c0.
+// NX consecutive activations of row m from channel k: from the staged chunk (XLDS; the
+// chunk starts at channel c0, row stride KC) or from global memory.
 template <int NX, bool XLDS>
-__device__ __forceinline__ void read_x(float (&xv)[NX], const float* xs,
-                                       const float* __restrict__ x,
-                                       const float* __restrict__ inv, int m, int M, int K, int k,
-                                       int c0, int KC) {
+__device__ __forceinline__ void read_x(float (&xv)[NX], const float* xs, const GemvArgs& a, int m,
+                                       int k, int c0) {
   if (XLDS) {
-    const float4* p = reinterpret_cast<const float4*>(xs + m * KC + (k - c0));
+    const float4* p = reinterpret_cast<const float4*>(xs + m * a.KC + (k - c0));
 #pragma unroll
     for (int i = 0; i < NX / 4; ++i) {
       const float4 v = p[i];
@@ -117,13 +99,13 @@ __device__ __forceinline__ void read_x(float (&xv)[NX], const float* xs,
       xv[4 * i + 3] = v.w;
     }
   } else {
-    if (m >= M) {
+    if (m >= a.M) {
 #pragma unroll
       for (int i = 0; i < NX; ++i) xv[i] = 0.f;
       return;
     }
-    const float4* p = reinterpret_cast<const float4*>(x + static_cast<int64_t>(m) * K + k);
-    const float4* s = inv ? reinterpret_cast<const float4*>(inv + k) : nullptr;
+    const float4* p = reinterpret_cast<const float4*>(a.x + static_cast<int64_t>(m) * a.K + k);
+    const float4* s = a.inv ? reinterpret_cast<const float4*>(a.inv + k) : nullptr;
 #pragma unroll
     for (int i = 0; i < NX / 4; ++i) {
       float4 v = p[i];
@@ -142,215 +124,135 @@ __device__ __forceinline__ void read_x(float (&xv)[NX], const float* xs,
   }
 }
 
-// ---------------------------------------------------------------------------------------
-// int8: y[m, n] = scale[n] * sum_k x[m, k] q[n, k]
-// ---------------------------------------------------------------------------------------
-template <int MT, int V, int R, bool XLDS>
-__global__ __launch_bounds__(256) void int8_gemv_fast(const float* __restrict__ x,
-                                                      const int8_t* __restrict__ q,
-                                                      const float* __restrict__ scale,
-                                                      float* __restrict__ y, int M, int N,
-                                                      int K, int KC) {
+// The fast GEMV. INT4 selects the nibble format. Requires: K a multiple of the segment
+// (LPR * CPL channels), 16-byte aligned rows, and for int4 group % 32 == 0.
+template <int MT, int LPR, int R, bool XLDS, bool INT4>
+__global__ __launch_bounds__(256) void gemv_fast(GemvArgs a) {
   extern __shared__ float xs[];
-  using VT = typename Vec<V>::T;
-  constexpr int W = Vec<V>::kWords;
-  constexpr int SEG = kWave * V;  // input channels per segment
+  constexpr int RPW = kWave / LPR;         // row slots per wavefront
+  constexpr int CPL = INT4 ? 32 : 16;      // input channels per lane per 16-byte load
+  constexpr int SEGK = LPR * CPL;          // input channels per row segment
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int row0 = (blockIdx.x * kWaves + wave) * R;
-  const int nseg = K / SEG;
-  const int spc = KC / SEG;  // segments per staged x chunk
-  const uint8_t* qb = reinterpret_cast<const uint8_t*>(q);
+  const int rs = lane / LPR, li = lane % LPR;
+  const int row0 = (blockIdx.x * kWaves + wave) * R * RPW + rs;  // row of group r: row0 + r*RPW
+  const int RB = INT4 ? a.K / 2 : a.K;
+  const int nseg = a.K / SEGK;
+  const int spc = a.KC / SEGK;  // segments per staged chunk
+  const int G = INT4 ? a.K / a.group : 1;
 
-  VT w[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-    w[r] = (row0 + r < N) ? load_vec<V>(qb + static_cast<int64_t>(row0 + r) * K + lane * V)
-                          : VT{};
-  float acc[R * MT];
-#pragma unroll
-  for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
-
-  int c0 = 0;
-  for (int j = 0; j < nseg; ++j) {
-    VT wn[R];
-    if (j + 1 < nseg) {
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        wn[r] = (row0 + r < N) ? load_vec<V>(qb + static_cast<int64_t>(row0 + r) * K +
-                                             (j + 1) * SEG + lane * V)
-                               : VT{};
-    }
-    if (XLDS && j % spc == 0) {
-      c0 = j * SEG;
-      if (j) __syncthreads();
-      stage_x<MT>(xs, x, nullptr, M, K, c0, min(KC, K - c0), KC);
-      __syncthreads();
-    }
-    float wf[R][V];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        const uint32_t u = word(w[r], i);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          wf[r][4 * i + b] = static_cast<float>(static_cast<int8_t>((u >> (8 * b)) & 0xffu));
-      }
-    const int k0 = j * SEG + lane * V;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      float xv[V];
-      read_x<V, XLDS>(xv, xs, x, nullptr, m, M, K, k0, c0, KC);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float a = acc[r * MT + m];
-#pragma unroll
-        for (int i = 0; i < V; ++i) a += xv[i] * wf[r][i];
-        acc[r * MT + m] = a;
-      }
-    }
-    if (j + 1 < nseg) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) w[r] = wn[r];
-    }
-  }
-  wave_reduce_store<R * MT>(acc, lane, [&](int i, float v) {
-    const int r = i / MT, m = i % MT;
-    if (m < M && row0 + r < N) y[static_cast<int64_t>(m) * N + row0 + r] = v * scale[row0 + r];
-  });
-}
-
-// Any shape / alignment: one wave per output row, lanes stride over k with byte loads.
-template <int MT>
-__global__ __launch_bounds__(256) void int8_gemv_generic(const float* __restrict__ x,
-                                                         const int8_t* __restrict__ q,
-                                                         const float* __restrict__ scale,
-                                                         float* __restrict__ y, int M, int N,
-                                                         int K) {
-  const int lane = threadIdx.x % kWave;
-  const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
-  if (row >= N) return;
-  float acc[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) acc[m] = 0.f;
-  const int8_t* qr = q + static_cast<int64_t>(row) * K;
-  for (int k = lane; k < K; k += kWave) {
-    const float wv = static_cast<float>(qr[k]);
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-      if (m < M) acc[m] += x[static_cast<int64_t>(m) * K + k] * wv;
-  }
-  wave_reduce_store<MT>(acc, lane, [&](int m, float v) {
-    if (m < M) y[static_cast<int64_t>(m) * N + row] = v * scale[row];
-  });
-}
-
-// ---------------------------------------------------------------------------------------
-// int4: nibble byte j of a row holds q[2j] (low) and q[2j+1] (high); w = (q - 8) s + z.
-// ---------------------------------------------------------------------------------------
-template <int MT, int V, int R, bool XLDS>
-__global__ __launch_bounds__(256) void int4_gemv_fast(
-    const float* __restrict__ x, const float* __restrict__ inv, const uint8_t* __restrict__ nib,
-    const float* __restrict__ gs, const float* __restrict__ gz, float* __restrict__ y, int M,
-    int N, int K, int group, int KC) {
-  extern __shared__ float xs[];
-  using VT = typename Vec<V>::T;
-  constexpr int W = Vec<V>::kWords;
-  constexpr int KL = 2 * V;         // input channels per lane slice
-  constexpr int SEG = kWave * KL;   // input channels per segment
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int row0 = (blockIdx.x * kWaves + wave) * R;
-  const int RB = K / 2;  // bytes per row
-  const int G = K / group;
-  const int nseg = K / SEG;
-  const int spc = KC / SEG;
-
-  VT w[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-    w[r] = (row0 + r < N) ? load_vec<V>(nib + static_cast<int64_t>(row0 + r) * RB + lane * V)
-                          : VT{};
-  float acc[R * MT];
-#pragma unroll
-  for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
-
-  int c0 = 0;
-  for (int j = 0; j < nseg; ++j) {
-    VT wn[R];
-    if (j + 1 < nseg) {
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        wn[r] = (row0 + r < N) ? load_vec<V>(nib + static_cast<int64_t>(row0 + r) * RB +
-                                             (j + 1) * kWave * V + lane * V)
-                               : VT{};
-    }
-    if (XLDS && j % spc == 0) {
-      c0 = j * SEG;
-      if (j) __syncthreads();
-      stage_x<MT>(xs, x, inv, M, K, c0, min(KC, K - c0), KC);
-      __syncthreads();
-    }
-    const int k0 = j * SEG + lane * KL;
-    const int g = k0 / group;
-    float s[R], c[R];
+  auto load_seg = [&](int j, u32x4 (&w)[R]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int rr = min(row0 + r, N - 1);
-      s[r] = gs[static_cast<int64_t>(rr) * G + g];
-      c[r] = gz[static_cast<int64_t>(rr) * G + g] - 8.f * s[r];
+      const int row = row0 + r * RPW;
+      w[r] = row < a.N ? load16(a.w + static_cast<int64_t>(row) * RB + j * LPR * 16 + li * 16)
+                       : u32x4{0u, 0u, 0u, 0u};
     }
-    if constexpr (MT <= 2) {
-      // x slice read once per m; nibbles unpacked per (m, row).
+  };
+
+  u32x4 w[R];
+  load_seg(0, w);
+  float acc[R][MT];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
+
+  int c0 = 0;
+  for (int j = 0; j < nseg; ++j) {
+    u32x4 wn[R];
+    if (j + 1 < nseg) load_seg(j + 1, wn);
+    const int k0 = j * SEGK + li * CPL;
+    float sc[R], zc[R];
+    if constexpr (INT4) {
+      const int g = k0 / a.group;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r * RPW, a.N - 1);
+        sc[r] = a.s[static_cast<int64_t>(row) * G + g];
+        zc[r] = a.z[static_cast<int64_t>(row) * G + g] - 8.f * sc[r];
+      }
+    }
+    if (XLDS && j % spc == 0) {
+      c0 = j * SEGK;
+      if (j) __syncthreads();
+      stage_x<MT>(xs, a.x, INT4 ? a.inv : nullptr, a.M, a.K, c0, min(a.KC, a.K - c0), a.KC);
+      __syncthreads();
+    }
+    if constexpr (!INT4) {
+      float wf[R][16];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float t[4];
+          unpack_int8(w[r][i], t);
+#pragma unroll
+          for (int b = 0; b < 4; ++b) wf[r][4 * i + b] = t[b];
+        }
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        float xv[KL];
-        read_x<KL, XLDS>(xv, xs, x, inv, m, M, K, k0, c0, KC);
+        float xv[16];
+        read_x<16, XLDS>(xv, xs, a, m, k0, c0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float t = acc[r][m];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) t += xv[i] * wf[r][i];
+          acc[r][m] = t;
+        }
+      }
+    } else if constexpr (MT <= 2) {
+      // x slice read once per m; nibbles unpacked per (m, row)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        float xv[32];
+        read_x<32, XLDS>(xv, xs, a, m, k0, c0);
         float xsum = 0.f;
 #pragma unroll
-        for (int i = 0; i < KL; ++i) xsum += xv[i];
+        for (int i = 0; i < 32; ++i) xsum += xv[i];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           float d = 0.f;
 #pragma unroll
-          for (int i = 0; i < W; ++i) {
+          for (int i = 0; i < 4; ++i) {
             float qf[8];
-            unpack_nibbles(word(w[r], i), qf);
+            unpack_nibbles(w[r][i], qf);
 #pragma unroll
             for (int e = 0; e < 8; ++e) d += xv[8 * i + e] * qf[e];
           }
-          acc[r * MT + m] += s[r] * d + c[r] * xsum;
+          acc[r][m] += sc[r] * d + zc[r] * xsum;
         }
       }
     } else {
-      // nibbles unpacked once per row; x slice re-read per row (LDS / L1).
+      // nibbles unpacked once per row; x slice re-read from LDS per row
       float xsum[MT];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        float xv[KL];
-        read_x<KL, XLDS>(xv, xs, x, inv, m, M, K, k0, c0, KC);
+        float xv[32];
+        read_x<32, XLDS>(xv, xs, a, m, k0, c0);
         float t = 0.f;
 #pragma unroll
-        for (int i = 0; i < KL; ++i) t += xv[i];
+        for (int i = 0; i < 32; ++i) t += xv[i];
         xsum[m] = t;
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        float qf[KL];
+        float qf[32];
 #pragma unroll
-        for (int i = 0; i < W; ++i) {
+        for (int i = 0; i < 4; ++i) {
           float t[8];
-          unpack_nibbles(word(w[r], i), t);
+          unpack_nibbles(w[r][i], t);
 #pragma unroll
           for (int e = 0; e < 8; ++e) qf[8 * i + e] = t[e];
         }
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          float xv[KL];
-          read_x<KL, XLDS>(xv, xs, x, inv, m, M, K, k0, c0, KC);
+          float xv[32];
+          read_x<32, XLDS>(xv, xs, a, m, k0, c0);
           float d = 0.f;
 #pragma unroll
-          for (int i = 0; i < KL; ++i) d += xv[i] * qf[i];
-          acc[r * MT + m] += s[r] * d + c[r] * xsum[m];
+          for (int i = 0; i < 32; ++i) d += xv[i] * qf[i];
+          acc[r][m] += sc[r] * d + zc[r] * xsum[m];
         }
       }
     }
@@ -359,182 +261,155 @@ __global__ __launch_bounds__(256) void int4_gemv_fast(
       for (int r = 0; r < R; ++r) w[r] = wn[r];
     }
   }
-  wave_reduce_store<R * MT>(acc, lane, [&](int i, float v) {
-    const int r = i / MT, m = i % MT;
-    if (m < M && row0 + r < N) y[static_cast<int64_t>(m) * N + row0 + r] = v;
-  });
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r * RPW;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float v = lsh::group_sum<LPR>(acc[r][m]);
+      if (li == 0 && m < a.M && row < a.N)
+        a.y[static_cast<int64_t>(m) * a.N + row] = INT4 ? v : v * a.s[row];
+    }
+  }
 }
 
-template <int MT>
-__global__ __launch_bounds__(256) void int4_gemv_generic(
-    const float* __restrict__ x, const float* __restrict__ inv, const uint8_t* __restrict__ nib,
-    const float* __restrict__ gs, const float* __restrict__ gz, float* __restrict__ y, int M,
-    int N, int K, int group) {
+// Any shape / alignment: one wavefront per output row, lanes stride over k with byte loads.
+template <int MT, bool INT4>
+__global__ __launch_bounds__(256) void gemv_generic(GemvArgs a) {
   const int lane = threadIdx.x % kWave;
   const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
-  if (row >= N) return;
-  const int G = K / group;
+  if (row >= a.N) return;  // whole wave; no barriers in this kernel
+  const int G = INT4 ? a.K / a.group : 1;
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = 0.f;
-  const uint8_t* qr = nib + static_cast<int64_t>(row) * (K / 2);
-  for (int k = lane; k < K; k += kWave) {
-    const uint8_t b = qr[k / 2];
-    const float qv = static_cast<float>((k & 1) ? (b >> 4) : (b & 0xf));
-    const int g = k / group;
-    const float s = gs[static_cast<int64_t>(row) * G + g];
-    const float c = gz[static_cast<int64_t>(row) * G + g] - 8.f * s;
+  for (int k = lane; k < a.K; k += kWave) {
+    float wv, s = 1.f, c = 0.f;
+    if constexpr (INT4) {
+      const uint8_t b = a.w[static_cast<int64_t>(row) * (a.K / 2) + k / 2];
+      wv = static_cast<float>((k & 1) ? (b >> 4) : (b & 0xf));
+      const int g = k / a.group;
+      s = a.s[static_cast<int64_t>(row) * G + g];
+      c = a.z[static_cast<int64_t>(row) * G + g] - 8.f * s;
+    } else {
+      wv = static_cast<float>(reinterpret_cast<const int8_t*>(a.w)[static_cast<int64_t>(row) * a.K + k]);
+    }
 #pragma unroll
     for (int m = 0; m < MT; ++m)
-      if (m < M) {
-        float xv = x[static_cast<int64_t>(m) * K + k];
-        if (inv) xv = __fmul_rn(xv, inv[k]);
-        acc[m] += s * (xv * qv) + c * xv;
+      if (m < a.M) {
+        float xv = a.x[static_cast<int64_t>(m) * a.K + k];
+        if (INT4 && a.inv) xv = __fmul_rn(xv, a.inv[k]);
+        acc[m] += INT4 ? s * (xv * wv) + c * xv : xv * wv;
       }
   }
-  wave_reduce_store<MT>(acc, lane, [&](int m, float v) {
-    if (m < M) y[static_cast<int64_t>(m) * N + row] = v;
-  });
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const float v = lsh::wave_sum_from<1>(acc[m]);
+    if (lane == 0 && m < a.M) a.y[static_cast<int64_t>(m) * a.N + row] = INT4 ? v : v * a.s[row];
+  }
 }
 
 // ---------------------------------------------------------------------------------------
 // Launch selection
 // ---------------------------------------------------------------------------------------
-constexpr int kLdsBudget = 64 * 1024;  // bytes of staged x per workgroup
+struct Config {
+  int lpr;     // lanes per row: 16, 32, 64 (0 = generic kernel)
+  int rows;    // R: row groups per wavefront
+  bool xlds;   // stage x in LDS
+};
 
 int pick_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
-// Rows per wave: spread small matrices over more waves, amortise x reads on large ones.
-int pick_rows(int N, int MT) {
-  if (MT >= 8) return 2;
-  if (N >= 4 * 256 * kWaves) return 4;
-  if (N >= 2 * 256 * kWaves) return 2;
-  return 1;
-}
-
-// Widest lane vector (16/8/4 bytes) whose segment tiles a row exactly and whose staged x
-// segment (MT rows x seg_channels) fits the LDS budget; 0 = generic kernel.
-int pick_vec(int64_t row_bytes, int channels_per_byte, int MT) {
-  for (int v : {16, 8, 4}) {
-    const int64_t seg_channels = static_cast<int64_t>(kWave) * v * channels_per_byte;
-    if (row_bytes % (kWave * v) == 0 && MT * seg_channels * 4 <= kLdsBudget) return v;
+// Fast-path tiling for a (bits, MT, N, K, group) problem; lpr = 0 when it cannot tile.
+Config choose(bool int4, int MT, int N, int K, int group, bool aligned) {
+  Config c{0, 1, true};
+  if (!aligned || (int4 && group % 32 != 0)) return c;
+  const int cpl = int4 ? 32 : 16;
+  const int row_bytes = int4 ? K / 2 : K;
+  for (int lpr : {64, 32, 16}) {
+    if (row_bytes % (lpr * 16) != 0) continue;
+    if (MT * lpr * cpl * 4 > kLdsBudget) continue;  // one staged segment must fit
+    c.lpr = lpr;
+    break;
   }
-  return 0;
+  if (c.lpr == 0) return c;
+  // R = 2 only when there are wavefronts to spare (~4 per SIMD)
+  const int rpw = kWave / c.lpr;
+  const int waves = (N + rpw - 1) / rpw;
+  c.rows = (MT <= 2 && waves >= 2 * 4096) ? 2 : 1;
+  c.xlds = MT > 2 || (static_cast<int64_t>(MT) * K * 4 <= kLdsBudget);
+  return c;
 }
 
-// Staged chunk: as many whole segments as fit the budget.
-int pick_chunk(int K, int seg, int MT) {
-  const int max_segs = kLdsBudget / (MT * seg * 4);
-  const int segs = K / seg;
-  return seg * (segs < max_segs ? segs : max_segs);
+int pick_chunk(int K, int segk, int MT) {
+  const int max_segs = kLdsBudget / (MT * segk * 4);
+  const int segs = K / segk;
+  return segk * (segs < max_segs ? segs : max_segs);
 }
 
-struct Int8Args {
-  const float* x;
-  const int8_t* q;
-  const float* s;
-  float* y;
-  int M, N, K;
-};
-
-template <int MT, int V, int R>
-void launch_int8(const Int8Args& a, hipStream_t st) {
-  const int KC = pick_chunk(a.K, kWave * V, MT);
-  const int rows_per_block = kWaves * R;
-  hipLaunchKernelGGL((int8_gemv_fast<MT, V, R, true>), dim3((a.N + rows_per_block - 1) / rows_per_block),
-                     dim3(kWaves * kWave), MT * KC * sizeof(float), st, a.x, a.q, a.s, a.y, a.M,
-                     a.N, a.K, KC);
+template <int MT, int LPR, int R, bool XLDS, bool INT4>
+void launch_fast(GemvArgs a, hipStream_t st) {
+  constexpr int SEGK = LPR * (INT4 ? 32 : 16);
+  constexpr int rows_per_block = kWaves * R * (kWave / LPR);
+  a.KC = XLDS ? pick_chunk(a.K, SEGK, MT) : SEGK;
+  const size_t lds = XLDS ? static_cast<size_t>(MT) * a.KC * sizeof(float) : 0;
+  hipLaunchKernelGGL((gemv_fast<MT, LPR, R, XLDS, INT4>),
+                     dim3((a.N + rows_per_block - 1) / rows_per_block), dim3(kWaves * kWave), lds, st,
+                     a);
 }
 
-template <int MT, int V>
-void launch_int8_r(int R, const Int8Args& a, hipStream_t st) {
-  if constexpr (MT >= 8) {  // 4 rows x 8+ activation rows would not fit the register file
-    if (R >= 2)
-      launch_int8<MT, V, 2>(a, st);
-    else
-      launch_int8<MT, V, 1>(a, st);
+template <int MT, int LPR, bool INT4>
+void launch_lpr(const Config& c, const GemvArgs& a, hipStream_t st) {
+  if constexpr (MT > 2) {  // x always staged; one row group (register budget)
+    launch_fast<MT, LPR, 1, true, INT4>(a, st);
   } else {
-    if (R == 4)
-      launch_int8<MT, V, 4>(a, st);
-    else if (R == 2)
-      launch_int8<MT, V, 2>(a, st);
-    else
-      launch_int8<MT, V, 1>(a, st);
+    if (c.rows == 2) {
+      if (c.xlds)
+        launch_fast<MT, LPR, 2, true, INT4>(a, st);
+      else
+        launch_fast<MT, LPR, 2, false, INT4>(a, st);
+    } else {
+      if (c.xlds)
+        launch_fast<MT, LPR, 1, true, INT4>(a, st);
+      else
+        launch_fast<MT, LPR, 1, false, INT4>(a, st);
+    }
   }
 }
 
-template <int MT>
-void dispatch_int8(bool fast_ok, const Int8Args& a, hipStream_t st) {
-  const int V = fast_ok ? pick_vec(a.K, 1, MT) : 0;
-  if (V == 0) {
-    hipLaunchKernelGGL(int8_gemv_generic<MT>, dim3((a.N + kWaves - 1) / kWaves),
-                       dim3(kWaves * kWave), 0, st, a.x, a.q, a.s, a.y, a.M, a.N, a.K);
-    return;
-  }
-  const int R = pick_rows(a.N, MT);
-  if (V == 16)
-    launch_int8_r<MT, 16>(R, a, st);
-  else if (V == 8)
-    launch_int8_r<MT, 8>(R, a, st);
-  else
-    launch_int8_r<MT, 4>(R, a, st);
-}
-
-struct Int4Args {
-  const float* x;
-  const float* inv;
-  const uint8_t* nib;
-  const float* gs;
-  const float* gz;
-  float* y;
-  int M, N, K, group;
-};
-
-template <int MT, int V, int R>
-void launch_int4(const Int4Args& a, hipStream_t st) {
-  const int KC = pick_chunk(a.K, 2 * kWave * V, MT);
-  const int rows_per_block = kWaves * R;
-  hipLaunchKernelGGL((int4_gemv_fast<MT, V, R, true>), dim3((a.N + rows_per_block - 1) / rows_per_block),
-                     dim3(kWaves * kWave), MT * KC * sizeof(float), st, a.x, a.inv, a.nib, a.gs,
-                     a.gz, a.y, a.M, a.N, a.K, a.group, KC);
-}
-
-template <int MT, int V>
-void launch_int4_r(int R, const Int4Args& a, hipStream_t st) {
-  if constexpr (MT >= 8) {  // 4 rows x 8+ activation rows would not fit the register file
-    if (R >= 2)
-      launch_int4<MT, V, 2>(a, st);
-    else
-      launch_int4<MT, V, 1>(a, st);
-  } else {
-    if (R == 4)
-      launch_int4<MT, V, 4>(a, st);
-    else if (R == 2)
-      launch_int4<MT, V, 2>(a, st);
-    else
-      launch_int4<MT, V, 1>(a, st);
+template <int MT, bool INT4>
+void launch_mt(const Config& c, const GemvArgs& a, hipStream_t st) {
+  switch (c.lpr) {
+    case 64: launch_lpr<MT, 64, INT4>(c, a, st); break;
+    case 32: launch_lpr<MT, 32, INT4>(c, a, st); break;
+    case 16: launch_lpr<MT, 16, INT4>(c, a, st); break;
+    default:
+      hipLaunchKernelGGL((gemv_generic<MT, INT4>), dim3((a.N + kWaves - 1) / kWaves),
+                         dim3(kWaves * kWave), 0, st, a);
   }
 }
 
-template <int MT>
-void dispatch_int4(bool fast_ok, const Int4Args& a, hipStream_t st) {
-  int V = fast_ok ? pick_vec(a.K / 2, 2, MT) : 0;
-  // a lane slice (2V channels) must stay inside one quantization group
-  while (V && a.group % (2 * V) != 0) V = (V == 4) ? 0 : V / 2;
-  if (V && (a.K / 2) % (kWave * V) != 0) V = 0;
-  if (V == 0) {
-    hipLaunchKernelGGL(int4_gemv_generic<MT>, dim3((a.N + kWaves - 1) / kWaves),
-                       dim3(kWaves * kWave), 0, st, a.x, a.inv, a.nib, a.gs, a.gz, a.y, a.M, a.N,
-                       a.K, a.group);
-    return;
+template <bool INT4>
+int run_gemv(GemvArgs a, bool aligned, hipStream_t st, const char* what) {
+  const int M = a.M;
+  for (int m0 = 0; m0 < M; m0 += 16) {
+    GemvArgs t = a;
+    t.M = M - m0 < 16 ? M - m0 : 16;
+    t.x = a.x + static_cast<int64_t>(m0) * a.K;
+    t.y = a.y + static_cast<int64_t>(m0) * a.N;
+    const int MT = pick_mt(t.M);
+    const Config c = choose(INT4, MT, a.N, a.K, a.group, aligned);
+    switch (MT) {
+      case 1: launch_mt<1, INT4>(c, t, st); break;
+      case 2: launch_mt<2, INT4>(c, t, st); break;
+      case 4: launch_mt<4, INT4>(c, t, st); break;
+      case 8: launch_mt<8, INT4>(c, t, st); break;
+      default: launch_mt<16, INT4>(c, t, st); break;
+    }
+    const int rc = lsh::launch_status(what);
+    if (rc) return rc;
   }
-  const int R = pick_rows(a.N, MT);
-  if (V == 16)
-    launch_int4_r<MT, 16>(R, a, st);
-  else if (V == 8)
-    launch_int4_r<MT, 8>(R, a, st);
-  else
-    launch_int4_r<MT, 4>(R, a, st);
+  return LLMSERVE_OK;
 }
 
 }  // namespace
@@ -548,22 +423,10 @@ extern "C" int llmserve_int8_linear(const float* x, const int8_t* q, const float
             "int8_linear: shape too large");
   if (M == 0 || N == 0) return LLMSERVE_OK;
   LSH_CHECK(x && q && scale && y, "int8_linear: null pointer");
-  hipStream_t st = lsh::as_stream(stream);
-  const bool fast_ok = lsh::aligned16(x) && lsh::aligned16(q) && K % 16 == 0;
-  for (int64_t m0 = 0; m0 < M; m0 += 16) {
-    const int mt = static_cast<int>(M - m0 < 16 ? M - m0 : 16);
-    const Int8Args a{x + m0 * K, q, scale, y + m0 * N, mt, static_cast<int>(N), static_cast<int>(K)};
-    switch (pick_mt(mt)) {
-      case 1: dispatch_int8<1>(fast_ok, a, st); break;
-      case 2: dispatch_int8<2>(fast_ok, a, st); break;
-      case 4: dispatch_int8<4>(fast_ok, a, st); break;
-      case 8: dispatch_int8<8>(fast_ok, a, st); break;
-      default: dispatch_int8<16>(fast_ok, a, st); break;
-    }
-    const int rc = lsh::launch_status("int8_linear");
-    if (rc) return rc;
-  }
-  return LLMSERVE_OK;
+  GemvArgs a{x, nullptr, reinterpret_cast<const uint8_t*>(q), scale, nullptr, y,
+             static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), 1, 0};
+  const bool aligned = lsh::aligned16(x) && lsh::aligned16(q) && K % 16 == 0;
+  return run_gemv<false>(a, aligned, lsh::as_stream(stream), "int8_linear");
 }
 
 extern "C" int llmserve_int4_linear(const float* x, const float* inv_act_scale,
@@ -577,22 +440,9 @@ extern "C" int llmserve_int4_linear(const float* x, const float* inv_act_scale,
             "int4_linear: shape too large");
   if (M == 0 || N == 0) return LLMSERVE_OK;
   LSH_CHECK(x && nibbles && g_scale && g_zero && y, "int4_linear: null pointer");
-  hipStream_t st = lsh::as_stream(stream);
-  const bool fast_ok = lsh::aligned16(x) && lsh::aligned16(nibbles) && K % 32 == 0 &&
+  GemvArgs a{x, inv_act_scale, nibbles, g_scale, g_zero, y, static_cast<int>(M),
+             static_cast<int>(N), static_cast<int>(K), static_cast<int>(group_size), 0};
+  const bool aligned = lsh::aligned16(x) && lsh::aligned16(nibbles) && K % 32 == 0 &&
                        (inv_act_scale == nullptr || lsh::aligned16(inv_act_scale));
-  for (int64_t m0 = 0; m0 < M; m0 += 16) {
-    const int mt = static_cast<int>(M - m0 < 16 ? M - m0 : 16);
-    const Int4Args a{x + m0 * K, inv_act_scale, nibbles, g_scale, g_zero, y + m0 * N, mt,
-                     static_cast<int>(N), static_cast<int>(K), static_cast<int>(group_size)};
-    switch (pick_mt(mt)) {
-      case 1: dispatch_int4<1>(fast_ok, a, st); break;
-      case 2: dispatch_int4<2>(fast_ok, a, st); break;
-      case 4: dispatch_int4<4>(fast_ok, a, st); break;
-      case 8: dispatch_int4<8>(fast_ok, a, st); break;
-      default: dispatch_int4<16>(fast_ok, a, st); break;
-    }
-    const int rc = lsh::launch_status("int4_linear");
-    if (rc) return rc;
-  }
-  return LLMSERVE_OK;
+  return run_gemv<true>(a, aligned, lsh::as_stream(stream), "int4_linear");
 }
