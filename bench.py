@@ -8,12 +8,15 @@ down 3072->1024 — 112 GEMV launches with distinct weights, replayed from a HIP
 distinct copies of the model's quantized linears (4 x 250 MB) rotate between steps, so the
 weights stream from HBM and not from the 256 MB Infinity Cache. Inputs are resident in HBM
 before the timed region; weights are random N(0, 0.02), activations N(0, 1) with 1% of the
-input channels x20, AWQ scales from the reference's grid search on 512 such rows.
+input channels x20; each layer shape's AWQ scale comes from the reference's grid search
+(quant.py:154-170) on 512 such rows and that shape's first weight.
 
 `value` = algorithmic bytes per step (packed weights + group scales/zeros + inv_act_scale +
 x + y) x steps / wall time of the K timed steps. `roofline` is for the dominant kernel (the
 gate_up GEMV): its algorithmic bytes per launch over its average launch duration, measured
-here with HIP events on the stream it runs on. `cpu_baseline` times the reference's own CPU
+here with HIP events that the kernel's own dispatch records (hipExtLaunchKernelGGL, via
+llmserve_time_next_call) on the stream it runs on — the interval a kernel-trace profiler
+reports. `cpu_baseline` times the reference's own CPU
 kernels (oracle/_ref, built from the reference sources) — or the oracle's C restatement where
 that build is absent — on the host cores, on the same quantized weights, for about 10 s.
 Extra fields report M = 4 / 16 steps and configs 1 (int8 GEMV) and 4 (int8-KV decode).
@@ -56,17 +59,20 @@ def log(msg: str) -> None:
 
 
 def build_weights(torch, dev, seed: int = 0):
-    """COPIES x LAYERS x 4 int4 AWQ linears, quantized on the GPU."""
+    """COPIES x LAYERS x 4 int4 AWQ linears, quantized on the GPU. The AWQ scale of each
+    layer shape comes from the reference's grid search on that shape's first weight and the
+    calibration rows (reused by the other layers of the shape)."""
     from llmserve.kernels import load_quant
     from llmserve.quant import _search_awq_scale
 
     g = torch.Generator(device=dev).manual_seed(seed)
-    calib = {}
+    calib, scales = {}, {}
     for name, (N, K) in SHAPES.items():
         x = torch.randn(512, K, device=dev, generator=g)
         outl = torch.randperm(K, device=dev, generator=g)[: K // 100]
         x[:, outl] *= 20.0
         calib[name] = x
+        scales[name] = _search_awq_scale(torch.randn(N, K, device=dev, generator=g) * 0.02, x, GROUP)
     model = []
     for c in range(COPIES):
         layers = []
@@ -74,12 +80,11 @@ def build_weights(torch, dev, seed: int = 0):
             lin = {}
             for name, (N, K) in SHAPES.items():
                 w = torch.randn(N, K, device=dev, generator=g) * 0.02
-                s = _search_awq_scale(w, calib[name], GROUP)
-                lin[name] = load_quant().int4_quantize(w, GROUP, s)
+                lin[name] = load_quant().int4_quantize(w, GROUP, scales[name])
                 del w
             layers.append(lin)
         model.append(layers)
-        log(f"[bench] quantized copy {c + 1}/{COPIES}")
+    log(f"[bench] quantized {COPIES} copies x {LAYERS} layers x {len(SHAPES)} linears")
     return model, calib
 
 
@@ -130,19 +135,19 @@ def time_graphs(torch, graphs, steps: int, warmup: int) -> tuple[float, float]:
 
 
 def kernel_avg_us(torch, launch, n: int) -> float:
-    """Average duration of single launches, each bracketed by HIP events on the current
-    stream (the stream the op launches on)."""
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(n)]
+    """Average kernel-execution time of `launch(i)` calls, each timed by HIP events that the
+    kernel's own dispatch records (llmserve_time_next_call), on the stream it runs on."""
+    from llmserve._native import KernelTimer
+
+    timer = KernelTimer(n)
     for i in range(3):
         launch(i)
     torch.cuda.synchronize()
-    for i, (a, b) in enumerate(evs):
-        a.record()
+    for i in range(n):
+        timer.arm(i)
         launch(i)
-        b.record()
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in evs) / n * 1e3
+    return sum(timer.elapsed_ms(i) for i in range(n)) / n * 1e3
 
 
 def read_traffic(kernel: str) -> dict | None:
@@ -319,11 +324,11 @@ def main() -> int:
     avg_us = kernel_avg_us(torch, gate_up, 224)
     kb = int4_bytes(N, K, 1)
     achieved = kb / avg_us / 1e3
-    traffic = read_traffic("int4_gemv_fast gate_up M=1")
+    traffic = read_traffic("gemv_fast int4 gate_up M=1")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None if traffic is None else int(traffic["fetch"] + traffic["write"]),
-                "kernel": "int4_gemv_fast<1,8,4> (gate_up 1024->6144, M=1)",
+                "kernel": "gemv_fast int4 (gate_up 1024->6144, M=1)",
                 "bytes_per_launch": kb, "avg_launch_us": round(avg_us, 3)}
     log(f"[bench] roofline: {roofline}")
 

@@ -37,6 +37,15 @@ const char* llmserve_last_error(void);
 /* ABI version of this library (bumped on any signature change). */
 int llmserve_abi_version(void);
 
+/*
+ * Measurement hook (no counterpart in the reference): arms two hipEvent_t for the calling
+ * thread's next kernel-launching call. Its first kernel records `start_event` when the
+ * dispatch starts and its last kernel records `stop_event` when it completes
+ * (hipExtLaunchKernelGGL), so hipEventElapsedTime gives the kernels' own execution time,
+ * the interval a kernel-trace profiler reports. Either event may be NULL.
+ */
+int llmserve_time_next_call(void* start_event, void* stop_event);
+
 /* ---- quantize + pack (load time) ------------------------------------------------------ */
 
 /*

@@ -2,6 +2,7 @@
 // wavefront (64-lane) reductions.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -20,29 +21,86 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Checks the status of the launch just enqueued.
 int launch_status(const char* what);
 
+// Events armed by llmserve_time_next_call() for the calling thread.
+struct TimingEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+TimingEvents& timing_events();
+
+// Enqueues `kernel`. When events are armed, the first launch of the call records the start
+// event at its dispatch start and the launch marked `last` records the stop event at its
+// completion (hipExtLaunchKernelGGL: the kernel's own execution interval).
+template <typename F, typename... Args>
+void launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, bool last, Args... args) {
+  TimingEvents& t = timing_events();
+  if (t.start == nullptr && t.stop == nullptr) {
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+    return;
+  }
+  hipEvent_t start = t.start, stop = last ? t.stop : nullptr;
+  t.start = nullptr;
+  if (last) t.stop = nullptr;
+  hipExtLaunchKernelGGL(kernel, grid, block, static_cast<std::uint32_t>(lds), st, start, stop, 0u,
+                        args...);
+}
+
 constexpr int kWave = 64;
 
-// Butterfly sum / max over the lanes whose index differs only in the bits of [lo, 64):
-// lane groups of size `lo` stay separate. All lanes get the result.
-template <int LO = 1>
-__device__ __forceinline__ float wave_sum_from(float v) {
-#pragma unroll
-  for (int o = 32; o >= LO; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+// ---- cross-lane reductions --------------------------------------------------------------
+// Within a row of 16 lanes: DPP (quad_perm, row_half_mirror, row_mirror, row_ror), which the
+// compiler fuses into the VALU op. Across rows (xor 16 / 32) the steps use ds_bpermute
+// (__shfl_xor); the hot loops only reduce within rows, the crossings run once per row or
+// partition at the end. (gfx950's v_permlane16/32_swap builtins would avoid the LDS
+// crossbar, but this compiler returns the same register for both of their results.)
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
-template <int LO = 1>
-__device__ __forceinline__ float wave_max_from(float v) {
-#pragma unroll
-  for (int o = 32; o >= LO; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+constexpr int kQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+constexpr int kRowRor4 = 0x124;
+constexpr int kRowRor8 = 0x128;
 
-// Sum over the `W` consecutive lanes of each group of W (W a power of two <= 64).
+// Sum over each aligned group of W consecutive lanes (W a power of two <= 64); every lane
+// of the group gets the sum.
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = W / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  if constexpr (W >= 2) v += dpp<kQuadXor1>(v);
+  if constexpr (W >= 4) v += dpp<kQuadXor2>(v);
+  if constexpr (W >= 8) v += dpp<kRowHalfMirror>(v);
+  if constexpr (W >= 16) v += dpp<kRowMirror>(v);
+  if constexpr (W >= 32) v += __shfl_xor(v, 16, kWave);
+  if constexpr (W >= 64) v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+// Sum / max over the lanes that share lane % LO (LO a power of two <= 64): the "columns"
+// of a wave laid out as rows of LO lanes. Every lane gets its column's result.
+template <int LO>
+__device__ __forceinline__ float wave_sum_from(float v) {
+  if constexpr (LO <= 1) v += dpp<kQuadXor1>(v);
+  if constexpr (LO <= 2) v += dpp<kQuadXor2>(v);
+  if constexpr (LO <= 4) v += dpp<kRowRor4>(v);
+  if constexpr (LO <= 8) v += dpp<kRowRor8>(v);
+  if constexpr (LO <= 16) v += __shfl_xor(v, 16, kWave);
+  if constexpr (LO <= 32) v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+template <int LO>
+__device__ __forceinline__ float wave_max_from(float v) {
+  if constexpr (LO <= 1) v = fmaxf(v, dpp<kQuadXor1>(v));
+  if constexpr (LO <= 2) v = fmaxf(v, dpp<kQuadXor2>(v));
+  if constexpr (LO <= 4) v = fmaxf(v, dpp<kRowRor4>(v));
+  if constexpr (LO <= 8) v = fmaxf(v, dpp<kRowRor8>(v));
+  if constexpr (LO <= 16) v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  if constexpr (LO <= 32) v = fmaxf(v, __shfl_xor(v, 32, kWave));
   return v;
 }
 

@@ -6,6 +6,7 @@
 
 namespace {
 thread_local char g_msg[512] = "";
+thread_local lsh::TimingEvents g_timing;
 }
 
 namespace lsh {
@@ -16,6 +17,8 @@ void set_error(const char* fmt, ...) {
   vsnprintf(g_msg, sizeof(g_msg), fmt, ap);
   va_end(ap);
 }
+
+TimingEvents& timing_events() { return g_timing; }
 
 int launch_status(const char* what) {
   const hipError_t e = hipGetLastError();
@@ -31,3 +34,9 @@ int launch_status(const char* what) {
 extern "C" const char* llmserve_last_error(void) { return g_msg; }
 
 extern "C" int llmserve_abi_version(void) { return 1; }
+
+extern "C" int llmserve_time_next_call(void* start_event, void* stop_event) {
+  g_timing.start = static_cast<hipEvent_t>(start_event);
+  g_timing.stop = static_cast<hipEvent_t>(stop_event);
+  return LLMSERVE_OK;
+}

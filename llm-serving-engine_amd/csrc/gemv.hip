@@ -348,44 +348,43 @@ int pick_chunk(int K, int segk, int MT) {
 }
 
 template <int MT, int LPR, int R, bool XLDS, bool INT4>
-void launch_fast(GemvArgs a, hipStream_t st) {
+void launch_fast(GemvArgs a, hipStream_t st, bool last) {
   constexpr int SEGK = LPR * (INT4 ? 32 : 16);
   constexpr int rows_per_block = kWaves * R * (kWave / LPR);
   a.KC = XLDS ? pick_chunk(a.K, SEGK, MT) : SEGK;
   const size_t lds = XLDS ? static_cast<size_t>(MT) * a.KC * sizeof(float) : 0;
-  hipLaunchKernelGGL((gemv_fast<MT, LPR, R, XLDS, INT4>),
-                     dim3((a.N + rows_per_block - 1) / rows_per_block), dim3(kWaves * kWave), lds, st,
-                     a);
+  lsh::launch(gemv_fast<MT, LPR, R, XLDS, INT4>, dim3((a.N + rows_per_block - 1) / rows_per_block),
+              dim3(kWaves * kWave), lds, st, last, a);
 }
 
 template <int MT, int LPR, bool INT4>
-void launch_lpr(const Config& c, const GemvArgs& a, hipStream_t st) {
+void launch_lpr(const Config& c, const GemvArgs& a, hipStream_t st, bool last) {
   if constexpr (MT > 2) {  // x always staged; one row group (register budget)
-    launch_fast<MT, LPR, 1, true, INT4>(a, st);
+    launch_fast<MT, LPR, 1, true, INT4>(a, st, last);
   } else {
     if (c.rows == 2) {
       if (c.xlds)
-        launch_fast<MT, LPR, 2, true, INT4>(a, st);
+        launch_fast<MT, LPR, 2, true, INT4>(a, st, last);
       else
-        launch_fast<MT, LPR, 2, false, INT4>(a, st);
+        launch_fast<MT, LPR, 2, false, INT4>(a, st, last);
     } else {
       if (c.xlds)
-        launch_fast<MT, LPR, 1, true, INT4>(a, st);
+        launch_fast<MT, LPR, 1, true, INT4>(a, st, last);
       else
-        launch_fast<MT, LPR, 1, false, INT4>(a, st);
+        launch_fast<MT, LPR, 1, false, INT4>(a, st, last);
     }
   }
 }
 
 template <int MT, bool INT4>
-void launch_mt(const Config& c, const GemvArgs& a, hipStream_t st) {
+void launch_mt(const Config& c, const GemvArgs& a, hipStream_t st, bool last) {
   switch (c.lpr) {
-    case 64: launch_lpr<MT, 64, INT4>(c, a, st); break;
-    case 32: launch_lpr<MT, 32, INT4>(c, a, st); break;
-    case 16: launch_lpr<MT, 16, INT4>(c, a, st); break;
+    case 64: launch_lpr<MT, 64, INT4>(c, a, st, last); break;
+    case 32: launch_lpr<MT, 32, INT4>(c, a, st, last); break;
+    case 16: launch_lpr<MT, 16, INT4>(c, a, st, last); break;
     default:
-      hipLaunchKernelGGL((gemv_generic<MT, INT4>), dim3((a.N + kWaves - 1) / kWaves),
-                         dim3(kWaves * kWave), 0, st, a);
+      lsh::launch(gemv_generic<MT, INT4>, dim3((a.N + kWaves - 1) / kWaves), dim3(kWaves * kWave),
+                  0, st, last, a);
   }
 }
 
@@ -399,12 +398,13 @@ int run_gemv(GemvArgs a, bool aligned, hipStream_t st, const char* what) {
     t.y = a.y + static_cast<int64_t>(m0) * a.N;
     const int MT = pick_mt(t.M);
     const Config c = choose(INT4, MT, a.N, a.K, a.group, aligned);
+    const bool last = m0 + 16 >= M;
     switch (MT) {
-      case 1: launch_mt<1, INT4>(c, t, st); break;
-      case 2: launch_mt<2, INT4>(c, t, st); break;
-      case 4: launch_mt<4, INT4>(c, t, st); break;
-      case 8: launch_mt<8, INT4>(c, t, st); break;
-      default: launch_mt<16, INT4>(c, t, st); break;
+      case 1: launch_mt<1, INT4>(c, t, st, last); break;
+      case 2: launch_mt<2, INT4>(c, t, st, last); break;
+      case 4: launch_mt<4, INT4>(c, t, st, last); break;
+      case 8: launch_mt<8, INT4>(c, t, st, last); break;
+      default: launch_mt<16, INT4>(c, t, st, last); break;
     }
     const int rc = lsh::launch_status(what);
     if (rc) return rc;

@@ -45,6 +45,7 @@ _P, _I64, _I32, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_f
 C_SIGNATURES: dict[str, tuple[object, list]] = {
     "llmserve_last_error": (ctypes.c_char_p, []),
     "llmserve_abi_version": (_I32, []),
+    "llmserve_time_next_call": (_I32, [_P, _P]),
     "llmserve_int8_quantize": (_I32, [_P, _P, _P, _I64, _I64, _P]),
     "llmserve_int4_quantize": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "llmserve_kv_quantize_write": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
@@ -77,3 +78,54 @@ def check(rc: int) -> None:
     """Raises RuntimeError with the library's message for a nonzero C ABI status."""
     if rc != 0:
         raise RuntimeError(capi().llmserve_last_error().decode())
+
+
+@functools.cache
+def _hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime already loaded in this process (torch's; SONAME libamdhip64.so.7)."""
+    import torch  # noqa: F401  (makes sure torch's runtime is the one bound)
+
+    lib = ctypes.CDLL("libamdhip64.so.7")
+    lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    lib.hipEventCreate.restype = ctypes.c_int
+    lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), _P, _P]
+    lib.hipEventElapsedTime.restype = ctypes.c_int
+    lib.hipEventSynchronize.argtypes = [_P]
+    lib.hipEventSynchronize.restype = ctypes.c_int
+    lib.hipEventDestroy.argtypes = [_P]
+    lib.hipEventDestroy.restype = ctypes.c_int
+    return lib
+
+
+class KernelTimer:
+    """Kernel-execution time of single library calls: ``arm(i)`` makes the next call on this
+    thread record event pair i around its kernels (llmserve_time_next_call), ``elapsed_ms(i)``
+    reads it after the call."""
+
+    def __init__(self, n: int) -> None:
+        hip = _hip_runtime()
+        self._ev = []
+        for _ in range(2 * n):
+            e = ctypes.c_void_p()
+            if hip.hipEventCreate(ctypes.byref(e)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            self._ev.append(e)
+
+    def arm(self, i: int) -> None:
+        check(capi().llmserve_time_next_call(self._ev[2 * i], self._ev[2 * i + 1]))
+
+    def elapsed_ms(self, i: int) -> float:
+        hip = _hip_runtime()
+        hip.hipEventSynchronize(self._ev[2 * i + 1])
+        ms = ctypes.c_float()
+        if hip.hipEventElapsedTime(ctypes.byref(ms), self._ev[2 * i], self._ev[2 * i + 1]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def __del__(self) -> None:
+        try:
+            hip = _hip_runtime()
+            for e in self._ev:
+                hip.hipEventDestroy(e)
+        except Exception:
+            pass
