@@ -124,11 +124,14 @@ int llmserve_int4_linear(const float* x, const float* inv_act_scale /* nullable 
  *   slot_t = block_tables[b, t / block_size] * block_size + t % block_size
  * q fp32 [B,Hq,D]; k/v_cache int8 [num_slots,Hk,D]; k/v_scale fp32 [num_slots,Hk];
  * block_tables int64 [B,max_blocks]; context_lens int64 [B] -> out fp32 [B,Hq,D].
- * partition_size: tokens per split-context partition (rounded up to a block multiple);
- * 0 picks one for the GPU. Block ids outside [0, num_slots/block_size) contribute nothing;
+ * The context is split, as the reference's partitions are, into work ranges whose partial
+ * (max, sum, acc) are merged: partition_size = tokens per range; 0 splits the whole batch
+ * evenly over the GPU's resident workgroups (the same number of cache rows for each, whatever
+ * the context lengths). Block ids outside [0, num_slots/block_size) contribute nothing;
  * context lengths are clamped to max_blocks*block_size. A zero context yields NaN, as the
- * reference's 0 * (1/0) does. `workspace` holds the per-partition (max, sum, acc) partials:
- * at least llmserve_paged_attention_workspace_bytes(...) bytes (may be NULL when that is 0).
+ * reference's 0 * (1/0) does. `workspace` holds the partials: at least
+ * llmserve_paged_attention_workspace_bytes(...) bytes (non-zero whenever B > 0; the size of
+ * the balanced split depends on the current device).
  */
 int64_t llmserve_paged_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hk, int64_t D,
                                                  int64_t max_blocks, int64_t block_size,

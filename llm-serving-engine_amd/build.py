@@ -36,7 +36,7 @@ ARCH = "gfx950"
 
 HIP_FLAGS = [
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     f"--offload-arch={ARCH}",
     "-fhip-fp32-correctly-rounded-divide-sqrt",

@@ -80,6 +80,17 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Max over each aligned group of W consecutive lanes (W a power of two <= 16: DPP only).
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+  static_assert(W <= 16, "group_max: DPP rows of 16 lanes");
+  if constexpr (W >= 2) v = fmaxf(v, dpp<kQuadXor1>(v));
+  if constexpr (W >= 4) v = fmaxf(v, dpp<kQuadXor2>(v));
+  if constexpr (W >= 8) v = fmaxf(v, dpp<kRowHalfMirror>(v));
+  if constexpr (W >= 16) v = fmaxf(v, dpp<kRowMirror>(v));
+  return v;
+}
+
 // Sum / max over the lanes that share lane % LO (LO a power of two <= 64): the "columns"
 // of a wave laid out as rows of LO lanes. Every lane gets its column's result.
 template <int LO>

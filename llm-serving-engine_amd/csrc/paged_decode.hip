@@ -1,42 +1,67 @@
-// int8-KV paged decode attention (split context + online softmax) and the partition merge.
+// int8-KV paged decode attention: the context split evenly over the GPU's wavefronts, an
+// online softmax per wavefront, and a merge of the sequences that were split.
 //
-// Work item = one wavefront per (sequence b, kv head h, context partition p); a 256-thread
-// workgroup holds the wavefronts of 4 consecutive kv heads of the same (b, p), so one
-// workgroup streams 4 x 128 B of every cache slot it touches.
+// Work line: the kv heads form NHG groups of HB heads (HB = the largest divisor of Hk up to
+// 8). The (sequence b, head group hg, token t) triples, t fastest, laid end to end make a line
+// of T = NHG * sum_b ctx_b. The line is cut into ranges of Q tokens (Q = ceil(T / W) over the
+// W resident workgroups, so every SIMD streams the same number of cache rows whatever the
+// context lengths; or a caller-fixed Q). A workgroup holds HB wavefronts, one per kv head of
+// the group, which run the same tokens: together they read whole HB * D-byte pieces of every
+// slot row (all of it when HB = Hk), so the cache streams in long contiguous runs. A workgroup
+// runs its range as segments, one per (b, hg) the range touches. A segment that covers its
+// whole (b, hg) writes the output rows; the others write a partial (running max, sum, acc) per
+// head to slot ((b * NHG + hg) + j) * HB + head-in-group (j = range index; distinct for
+// distinct segments since the ranges of one (b, hg) have consecutive j and the next (b, hg)
+// starts at a j no smaller than the last one of this (b, hg)). The merge kernel combines the
+// partials of every split (b, hg).
 //
 // Lane layout inside a wavefront (D = head dim, LPR = D / 16 lanes per token row):
 //   lane = r * LPR + seg : row slot r of the RPW = 64 / LPR tokens of one step, dims
 //                          [16 seg, 16 seg + 16) of that token.
-// Each lane loads 16 bytes of the token's K row and 16 bytes of its V row per step (one
-// dwordx4 each, non-temporal: the wave reads RPW whole rows). Every row slot runs its own
-// online softmax over the tokens it sees (t = r, r + RPW, ...), so a step needs no
+// Step k covers tokens [k RPW, (k + 1) RPW) of the sequence; each lane loads 16 bytes of its
+// token's K row and 16 bytes of its V row (one dwordx4 each, non-temporal) and the row's two
+// scales. When the block size is a multiple of RPW a step lies inside one cache block, its
+// block id is wave-uniform (read from the lane holding it) and the slot arithmetic is
+// scalar; otherwise each lane fetches its own block id with a lane shuffle.
+// Every row slot runs its own online softmax over the tokens it sees, so a step needs no
 // cross-row communication:
 //   * q.k: 16-dim partial dot per query head, summed over the LPR lanes of the row with DPP;
-//   * the running max is raised only when a score exceeds it by more than kLazy (the
-//     exponentials stay <= e^kLazy); the rescale of (sum, acc) then runs under a
-//     wave-uniform branch, so most steps skip it;
+//     q is pre-scaled by scale * log2(e), so scores are in log2 units and p = exp2(s - m);
+//   * the running max is raised only when a score exceeds it by more than kLazy2 (p stays
+//     <= e^8); the rescale of (sum, acc) then runs under a wave-uniform branch;
 //   * acc += (p * v_scale) * v_int8 in the lane's 16 dims.
 // Up to four steps of K/V loads are kept in flight (a ring of registers, refilled as each
-// step is consumed), and the partition's block ids (<= 64 blocks) sit one per lane, read with a
-// lane shuffle. At the end the RPW row-slot states are merged (DPP / permlane swaps), then
-// written as the output (one partition) or as a partial for the merge kernel.
-// Scores follow the reference's order of operations: s = (scale * k_scale) * (q . k_int8),
-// acc += (p * v_scale) * v_int8 (paged_attention.cpp:301-355).
+// step is consumed). Block ids are read in windows of 64 (one per lane). At the end the RPW
+// row-slot states are merged with DPP / lane shuffles.
+// The scores are the reference's s = (scale * k_scale) * (q . k_int8) and the values
+// acc += (p * v_scale) * v_int8 (paged_attention.cpp:301-355), up to the order of the
+// float operations (scale folded into q; exp2 of log2-unit scores).
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
 
 using lsh::kWave;
-constexpr int kWavesPerBlock = 4;
+constexpr int kMaxHeadsPerBlock = 8;  // wavefronts of a decode workgroup (HB <= 8)
+constexpr int kMergeWaves = 4;        // wavefronts of a merge workgroup
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kNegBig = -1e30f;  // the reference's initial running max
-constexpr float kLazy = 8.0f;       // headroom of the lazy running max (natural-log units)
-constexpr int kMaxPartBlocks = 64;  // block ids of one partition held one per lane
+constexpr float kNegBig = -1e30f;        // the reference's initial running max
+constexpr float kLazy2 = 8.0f * kLog2e;  // lazy running-max headroom (log2 units: e^8)
+constexpr int kWin = 64;                 // block ids of a window, one per lane
 // steps of K/V loads in flight per wavefront (fewer for wide GQA groups: register budget)
 template <int G>
 constexpr int ring_depth() { return G <= 2 ? 4 : (G <= 4 ? 3 : 2); }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kNT = 2;  // buffer-load cache policy: non-temporal (streamed once)
+
+// Raw buffer resource over `bytes` bytes at p (loads past the end return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
 
 __device__ __forceinline__ void unpack_i8x16(const u32x4& w, float (&f)[16]) {
 #pragma unroll
@@ -56,82 +81,107 @@ struct DecodeArgs {
   const int64_t* cl;
   const float* q_mult;
   float* out;
-  float* part_ml;   // [B, Hk, NP, G, 2]  (max, sum)
-  float* part_acc;  // [B, Hk, NP, G, D]
+  float* part_ml;   // [slots, G, 2]  (running max in log2 units, sum)
+  float* part_acc;  // [slots, G, D]
   int64_t num_slots;
-  int B, Hq, Hk, max_blocks, bs, bs_shift, P, NP;  // bs_shift = log2(bs), or -1
-  float scale;
+  int64_t range;  // token-heads per work range; 0: ceil(T / W)
+  int B, Hq, Hk, max_blocks, bs, bs_shift;  // bs_shift = log2(bs), or -1
+  int HB, NHG;  // kv heads per workgroup, head groups (Hk = HB * NHG)
+  int W;        // decode workgroups (all resident)
+  float qscale;                                 // scale * log2(e)
 };
+
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Context length of sequence b, clamped to [0, max_blocks * block_size].
+__device__ __forceinline__ int64_t seq_ctx(const DecodeArgs& a, int b) {
+  const int64_t cap = static_cast<int64_t>(a.max_blocks) * a.bs;
+  const int64_t c = a.cl[b];
+  return c < 0 ? 0 : (c > cap ? cap : c);
+}
+
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+  return v;
+}
+
+// Sum of the contexts of sequences [0, bend) (wave-uniform).
+__device__ int64_t tokens_before(const DecodeArgs& a, int bend) {
+  const int lane = threadIdx.x % kWave;
+  int64_t s = 0;
+  for (int b0 = 0; b0 < bend; b0 += kWave) {
+    const int b = b0 + lane;
+    s += wave_sum_i64(b < bend ? seq_ctx(a, b) : 0);
+  }
+  return uniform64(s);
+}
+
+// Work-range geometry shared by the decode and merge kernels.
+struct Ranges {
+  int64_t T, Q, R;  // token-heads, token-heads per range, ranges
+};
+
+__device__ __forceinline__ Ranges work_ranges(const DecodeArgs& a) {
+  Ranges g;
+  g.T = tokens_before(a, a.B) * a.NHG;
+  g.Q = a.range > 0 ? a.range : (g.T + a.W - 1) / a.W;
+  if (g.Q < 1) g.Q = 1;
+  g.R = (g.T + g.Q - 1) / g.Q;
+  return g;
+}
+
+// The sequence whose line part [NHG * pre, NHG * (pre + ctx)) holds line index g (g < T).
+struct SeqPos {
+  int b;
+  int64_t pre, ctx;
+};
+
+__device__ SeqPos locate(const DecodeArgs& a, int64_t g) {
+  const int lane = threadIdx.x % kWave;
+  int64_t base = 0;
+  for (int b0 = 0; b0 < a.B; b0 += kWave) {
+    const int b = b0 + lane;
+    const int64_t c = b < a.B ? seq_ctx(a, b) : 0;
+    int64_t incl = c;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int64_t u = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += u;
+    }
+    const uint64_t hit = __ballot(b < a.B && (base + incl) * a.NHG > g);
+    if (hit != 0) {
+      const int i = __builtin_ctzll(hit);
+      const int64_t ci = __shfl(c, i, kWave), ii = __shfl(incl, i, kWave);
+      return {b0 + i, uniform64(base + ii - ci), uniform64(ci)};
+    }
+    base += __shfl(incl, kWave - 1, kWave);
+  }
+  return {a.B, uniform64(base), 0};
+}
 
 // One token step of one lane: its 16 K and V bytes and the row's two scales.
 struct Tok {
   u32x4 k, v;
   float ks, vs;
-  bool valid;
+  bool valid;  // this lane's token is in the segment and its block id is inside the cache
 };
 
-// One work item: sequence b, kv head h, context partition p, on one wavefront.
-template <int D, int G>
-__device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, int p) {
+// Runs tokens [t0, t1) of (b, h) and writes the output rows (whole) or partial `slot`.
+template <int D, int G, bool kScalarBlk>
+__device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h, int t0, int t1,
+                                               bool whole, int64_t slot) {
   constexpr int LPR = D / 16;       // lanes per token row
   constexpr int RPW = kWave / LPR;  // row slots per wavefront
   constexpr int kRing = ring_depth<G>();
   const int lane = threadIdx.x % kWave;
   const int r = lane / LPR, seg = lane % LPR;
-
-  int64_t ctx = a.cl[b];
-  const int64_t cap = static_cast<int64_t>(a.max_blocks) * a.bs;
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-  const int t0 = p * a.P;
-  const int t1 = static_cast<int>(ctx < t0 + a.P ? ctx : t0 + a.P);
-  const int64_t pidx = (static_cast<int64_t>(b) * a.Hk + h) * a.NP + p;
-
-  if (t0 >= t1) {  // partition past this sequence's end (or an empty context)
-    if (a.NP > 1) {
-      if (lane < G) {
-        a.part_ml[(pidx * G + lane) * 2] = kNegBig;
-        a.part_ml[(pidx * G + lane) * 2 + 1] = 0.f;
-      }
-    } else if (r == 0) {  // ctx == 0: the reference yields 0 * (1 / 0)
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          a.out[(static_cast<int64_t>(b) * a.Hq + h * G + g) * D + seg * 16 + i] = __builtin_nanf("");
-    }
-    return;
-  }
-
-  // block ids of this partition, one per lane (-1: outside the cache)
-  const int blk0 = t0 / a.bs;  // t0 is a block multiple
-  const int nblk = (t1 - t0 + a.bs - 1) / a.bs;
-  int my_blk = -1;
-  if (lane < nblk) {
-    const int64_t id = a.bt[static_cast<int64_t>(b) * a.max_blocks + blk0 + lane];
-    my_blk = (id >= 0 && id < a.num_slots / a.bs) ? static_cast<int>(id) : -1;
-  }
-
-  const int64_t row_stride = static_cast<int64_t>(a.Hk) * D;  // bytes between slots
-  const int64_t head_off = static_cast<int64_t>(h) * D + seg * 16;
-  // Issues the loads of token t into o. A lane without a token (t >= t1 or a block id
-  // outside the cache) reads slot 0 instead — the same 16 bytes for every such lane, one
-  // cached line — and o.valid masks it. The loads are unconditional on purpose: with a
-  // predicated load the compiler folds the consumer's byte unpacking into the load's block
-  // and waits for the data right there, which serialises the ring of in-flight steps.
-  auto fetch = [&](int t, Tok& o) {
-    // every lane takes part in the shuffle (a lane's block id is read even when that lane
-    // has no token of its own in this step)
-    const int rel = t < t1 ? t - t0 : 0;
-    int id = __shfl(my_blk, a.bs_shift >= 0 ? rel >> a.bs_shift : rel / a.bs, kWave);
-    if (t >= t1) id = -1;
-    o.valid = id >= 0;
-    const int off = a.bs_shift >= 0 ? t & (a.bs - 1) : t % a.bs;
-    const int64_t slot = o.valid ? static_cast<int64_t>(id) * a.bs + off : 0;
-    o.k = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.kc + slot * row_stride + head_off));
-    o.v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vc + slot * row_stride + head_off));
-    o.ks = a.ks[slot * a.Hk + h];
-    o.vs = a.vs[slot * a.Hk + h];
-  };
+  const int bs = a.bs;
 
   float qv[G][16];
 #pragma unroll
@@ -150,41 +200,91 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, i
         v.z = __fmul_rn(v.z, s.z);
         v.w = __fmul_rn(v.w, s.w);
       }
-      qv[g][4 * i] = v.x;
-      qv[g][4 * i + 1] = v.y;
-      qv[g][4 * i + 2] = v.z;
-      qv[g][4 * i + 3] = v.w;
+      qv[g][4 * i] = v.x * a.qscale;
+      qv[g][4 * i + 1] = v.y * a.qscale;
+      qv[g][4 * i + 2] = v.z * a.qscale;
+      qv[g][4 * i + 3] = v.w * a.qscale;
     }
   }
 
-  // q and the block ids are in registers before any K/V load is issued: otherwise the
-  // loop header, which merges this entry path with its back edge, would wait for all
-  // outstanding loads (vmcnt counts in issue order) on every iteration.
-  __builtin_amdgcn_s_waitcnt(0);
-
-  Tok ring[kRing];
-#pragma unroll
-  for (int u = 0; u < kRing; ++u) fetch(t0 + u * RPW + r, ring[u]);
-
-  float m[G], l[G], acc[G][16];
+  float m[G], mt[G], l[G], acc[G][16];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = kNegBig;
+    mt[g] = kNegBig;  // m + kLazy2 (kNegBig absorbs the headroom)
     l[g] = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[g][i] = 0.f;
   }
 
-  // Whole rounds of kRing steps; steps past t1 are fully masked (no loads, p = 0).
-  for (int tb = t0; tb < t1; tb += kRing * RPW) {
-#pragma unroll
-    for (int u = 0; u < kRing; ++u) {
-      const int tcur = tb + u * RPW;
-      Tok& c = ring[u];
-      // Consume the ring entry here and not earlier: an opaque use stops the compiler from
-      // folding the unpacking into the loop latch, where it would wait for loads issued
-      // only this round (vmcnt counts in issue order).
-      asm volatile("" : "+v"(c.k), "+v"(c.v), "+v"(c.ks), "+v"(c.vs));
+  const int64_t row_stride = static_cast<int64_t>(a.Hk) * D;  // bytes between slots
+  // Per-lane offsets inside a step: row slot r, head h, dims of segment seg.
+  const uint32_t kv_lane = static_cast<uint32_t>(r * row_stride + h * D + seg * 16);
+  const uint32_t sc_lane = static_cast<uint32_t>((r * a.Hk + h) * sizeof(float));
+  const int64_t head_off = static_cast<int64_t>(h) * D + seg * 16;
+  const uint32_t step_bytes = static_cast<uint32_t>(RPW * row_stride);
+  const uint32_t sc_bytes = static_cast<uint32_t>(RPW * a.Hk * sizeof(float));
+
+  for (int wb = t0 / bs; static_cast<int64_t>(wb) * bs < t1; wb += kWin) {
+    const int ws = t0 > wb * bs ? t0 : wb * bs;
+    const int we =
+        static_cast<int64_t>(t1) < static_cast<int64_t>(wb + kWin) * bs ? t1 : (wb + kWin) * bs;
+    int my_blk = -1;  // block id of window block `lane` (-1: outside the cache)
+    {
+      const int nwin = (we - wb * bs + bs - 1) / bs;
+      if (lane < nwin) {
+        const int64_t id = a.bt[static_cast<int64_t>(b) * a.max_blocks + wb + lane];
+        my_blk = (id >= 0 && id < a.num_slots / bs) ? static_cast<int>(id) : -1;
+      }
+    }
+    // q and the block ids are in registers before any K/V load is issued: otherwise the
+    // loop header, which merges this entry path with its back edge, would wait for all
+    // outstanding loads (vmcnt counts in issue order) on every iteration.
+    __builtin_amdgcn_s_waitcnt(0);
+
+    // Issues the loads of step k into o. Steps past the window read slot rows of block 0
+    // (in bounds, masked). The loads are unconditional on purpose: with a predicated load
+    // the compiler folds the consumer's byte unpacking into the load's block and waits for
+    // the data right there, which serialises the ring of in-flight steps.
+    auto fetch = [&](int k, Tok& o) {
+      const int tk = k * RPW;
+      const int t = tk + r;
+      if constexpr (kScalarBlk) {
+        // the step's rows are slots sb .. sb + RPW - 1 of one block: buffer loads from a
+        // scalar base, each lane at its own 32-bit offset
+        const int bi = (tk >> a.bs_shift) - wb;  // wave-uniform
+        const int id = bi < kWin ? __builtin_amdgcn_readlane(my_blk, bi) : -1;
+        o.valid = id >= 0 && t >= ws && t < we;
+        const int64_t sb = static_cast<int64_t>(id >= 0 ? id : 0) * bs + (tk & (bs - 1));
+        o.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rsrc(a.kc + sb * row_stride, step_bytes), kv_lane, 0, kNT));
+        o.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rsrc(a.vc + sb * row_stride, step_bytes), kv_lane, 0, kNT));
+        o.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             rsrc(a.ks + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
+        o.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             rsrc(a.vs + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
+      } else {
+        // every lane takes part in the shuffle (a lane's block id is read even when that
+        // lane has no token of its own in this step)
+        const int tt = t < we ? t : ws;
+        const int bi = (a.bs_shift >= 0 ? tt >> a.bs_shift : tt / bs) - wb;
+        const int id = __shfl(my_blk, bi, kWave);
+        o.valid = id >= 0 && t >= ws && t < we;
+        const int off = a.bs_shift >= 0 ? t & (bs - 1) : t % bs;
+        const int64_t sl = o.valid ? static_cast<int64_t>(id) * bs + off : 0;
+        o.k = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(a.kc + sl * row_stride + head_off));
+        o.v = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(a.vc + sl * row_stride + head_off));
+        o.ks = a.ks[sl * a.Hk + h];
+        o.vs = a.vs[sl * a.Hk + h];
+      }
+    };
+
+    // One step. A row outside the segment or the cache gets the score -inf (p = 0, and it
+    // never raises the max) and the value scale 0 (its bytes, whatever they hold, add 0).
+    auto consume = [&](const Tok& c) {
       float kf[16];
       unpack_i8x16(c.k, kf);
       float s[G];
@@ -195,15 +295,16 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, i
 #pragma unroll
         for (int i = 0; i < 16; ++i) d += qv[g][i] * kf[i];
         d = lsh::group_sum<LPR>(d);
-        s[g] = c.valid ? (a.scale * c.ks) * d : kNegBig;
-        raise |= s[g] > m[g] + kLazy;
+        s[g] = c.valid ? c.ks * d : -__builtin_inff();
+        raise |= s[g] > mt[g];
       }
       if (__builtin_amdgcn_ballot_w64(raise)) {  // rare: the running max moves
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const bool up = s[g] > m[g] + kLazy;
-          const float alpha = up ? __builtin_amdgcn_exp2f((m[g] - s[g]) * kLog2e) : 1.f;
+          const bool up = s[g] > mt[g];
+          const float alpha = up ? __builtin_amdgcn_exp2f(m[g] - s[g]) : 1.f;
           m[g] = up ? s[g] : m[g];
+          mt[g] = m[g] + kLazy2;
           l[g] *= alpha;
 #pragma unroll
           for (int i = 0; i < 16; ++i) acc[g][i] *= alpha;
@@ -211,15 +312,33 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, i
       }
       float vf[16];
       unpack_i8x16(c.v, vf);
+      const float vsc = c.valid ? c.vs : 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float pr = c.valid ? __builtin_amdgcn_exp2f((s[g] - m[g]) * kLog2e) : 0.f;
+        const float pr = __builtin_amdgcn_exp2f(s[g] - m[g]);
         l[g] += pr;
-        const float pv = c.valid ? pr * c.vs : 0.f;
+        const float pv = pr * vsc;
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[g][i] += pv * vf[i];
       }
-      fetch(tcur + kRing * RPW + r, c);
+    };
+
+    const int k0 = ws / RPW, k1 = (we + RPW - 1) / RPW;
+    Tok ring[kRing];
+#pragma unroll
+    for (int u = 0; u < kRing; ++u) fetch(k0 + u, ring[u]);
+    // Whole rounds of kRing steps; steps past the window are fully masked.
+    for (int k = k0; k < k1; k += kRing) {
+#pragma unroll
+      for (int u = 0; u < kRing; ++u) {
+        Tok& c = ring[u];
+        // Consume the ring entry here and not earlier: an opaque use stops the compiler from
+        // folding the unpacking into the loop latch, where it would wait for loads issued
+        // only this round (vmcnt counts in issue order).
+        asm volatile("" : "+v"(c.k), "+v"(c.v), "+v"(c.ks), "+v"(c.vs));
+        consume(c);
+        fetch(k + u + kRing, c);
+      }
     }
   }
 
@@ -228,13 +347,13 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, i
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const float mx = lsh::wave_max_from<LPR>(m[g]);
-    const float w = __builtin_amdgcn_exp2f((m[g] - mx) * kLog2e);
+    const float w = __builtin_amdgcn_exp2f(m[g] - mx);
     m[g] = mx;
     lt[g] = lsh::wave_sum_from<LPR>(w * l[g]);
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[g][i] = lsh::wave_sum_from<LPR>(w * acc[g][i]);
   }
-  if (a.NP == 1) {
+  if (whole) {
     if (r == 0) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -252,7 +371,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, i
   if (r == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float4* o = reinterpret_cast<float4*>(a.part_acc + (pidx * G + g) * D + seg * 16);
+      float4* o = reinterpret_cast<float4*>(a.part_acc + (slot * G + g) * D + seg * 16);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         o[i] = make_float4(acc[g][4 * i], acc[g][4 * i + 1], acc[g][4 * i + 2], acc[g][4 * i + 3]);
@@ -266,68 +385,133 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, i
         mm = m[g];
         ll = lt[g];
       }
-    a.part_ml[(pidx * G + lane) * 2] = mm;
-    a.part_ml[(pidx * G + lane) * 2 + 1] = ll;
+    a.part_ml[(slot * G + lane) * 2] = mm;
+    a.part_ml[(slot * G + lane) * 2 + 1] = ll;
   }
 }
 
-// Persistent decode kernel: a grid sized to the GPU (resident workgroups) strides over the
-// work items (b, group of 4 kv heads, p), p fastest. Each wavefront of a workgroup takes one
-// head of the group. Items past a sequence's end are cheap, so the strided assignment keeps
-// the waves evenly loaded without a second round of workgroups.
-template <int D, int G>
-__global__ __launch_bounds__(256) void paged_decode_int8_kernel(DecodeArgs a) {
-  const int wave = threadIdx.x / kWave;
-  const int hgroups = (a.Hk + kWavesPerBlock - 1) / kWavesPerBlock;
-  const int64_t items = static_cast<int64_t>(a.B) * hgroups * a.NP;
-  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
-    const int p = static_cast<int>(it % a.NP);
-    const int64_t bh = it / a.NP;
-    const int h = static_cast<int>(bh % hgroups) * kWavesPerBlock + wave;
-    const int b = static_cast<int>(bh / hgroups);
-    if (h < a.Hk) decode_item<D, G>(a, b, h, p);  // no barriers: waves proceed independently
+// Decode kernel: workgroup w runs work ranges w, w + W, ... (one range each with the
+// balanced default); its wavefront i takes kv head hg * HB + i. Waves proceed independently
+// (no barriers).
+template <int D, int G, bool kScalarBlk>
+__global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_int8_kernel(DecodeArgs a) {
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const Ranges rg = work_ranges(a);
+  for (int64_t j = blockIdx.x; j < rg.R; j += a.W) {
+    int64_t g = j * rg.Q;
+    const int64_t ge = g + rg.Q < rg.T ? g + rg.Q : rg.T;
+    const SeqPos sp = locate(a, g);
+    int b = sp.b;
+    int64_t gb = sp.pre * a.NHG;  // line index of (b, 0, 0)
+    int64_t ctx = sp.ctx;
+    if (b >= a.B || ctx <= 0) return;  // unreachable for g < T
+    for (;;) {
+      const int64_t rel = g - gb;
+      const int hg = static_cast<int>(rel / ctx);
+      const int64_t t0 = rel - hg * ctx;
+      const int64_t hend = gb + (hg + 1) * ctx;
+      const int64_t send = ge < hend ? ge : hend;
+      const int64_t t1 = t0 + (send - g);
+      const int h = hg * a.HB + wave;
+      const bool whole = t0 == 0 && t1 == ctx;
+      const int64_t slot = ((static_cast<int64_t>(b) * a.NHG + hg) + j) * a.HB + wave;
+      decode_segment<D, G, kScalarBlk>(a, b, h, static_cast<int>(t0), static_cast<int>(t1), whole,
+                                       slot);
+      g = send;
+      if (g >= ge) break;
+      if (hg + 1 == a.NHG) {  // next sequence with a non-empty context
+        gb += a.NHG * ctx;
+        do {
+          ++b;
+          ctx = b < a.B ? seq_ctx(a, b) : 1;
+        } while (ctx == 0);
+        if (b >= a.B) return;  // unreachable for g < T
+      }
+    }
   }
 }
 
-// Merge of the partitions (paged_attention.cpp:432-455): one wavefront per (b, q head).
-//   M = max_p m_p;  w_p = exp(m_p - M);  out = sum_p w_p acc_p / sum_p w_p l_p  (l_p = 0 skipped)
-// Lanes first read the (m, l) of 64 partitions at a time; the weighted sum over the
-// partitions' acc rows then runs with all loads of a 64-partition batch independent.
+// Merge of the split sequences (paged_attention.cpp:432-455): one wavefront per (b, q head).
+//   M = max_j m_j;  w_j = exp2(m_j - M);  out = sum_j w_j acc_j / sum_j w_j l_j  (l_j = 0 skipped)
+// A (b, hg) inside one range was written by the decode kernel; a zero context gives NaN (the
+// reference's 0 * (1 / 0)). Three dependent rounds of loads: the context lengths (one pass
+// gives the line length and the sequence's place on it), the (m, l) of up to 64 partials (one
+// per lane), then their acc rows, kMergeBatch partials at a time with all loads in flight.
+constexpr int kMergeBatch = 16;
+
 template <int D>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a, int B) {
+__global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int PER = (D + kWave - 1) / kWave;
   const int lane = threadIdx.x % kWave;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
-  if (item >= static_cast<int64_t>(B) * a.Hq) return;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kMergeWaves +
+                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  if (item >= static_cast<int64_t>(a.B) * a.Hq) return;
   const int b = static_cast<int>(item / a.Hq), hq = static_cast<int>(item % a.Hq);
   const int G = a.Hq / a.Hk;
   const int h = hq / G, g = hq % G;
-  const int64_t base = (static_cast<int64_t>(b) * a.Hk + h) * a.NP;
+  float* out = a.out + item * D;
+
+  int64_t tot = 0, pre = 0, cb = 0;
+  for (int b0 = 0; b0 < a.B; b0 += kWave) {
+    const int bb = b0 + lane;
+    const int64_t c = bb < a.B ? seq_ctx(a, bb) : 0;
+    tot += c;
+    pre += bb < b ? c : 0;
+    cb += bb == b ? c : 0;
+  }
+  tot = uniform64(wave_sum_i64(tot));
+  pre = uniform64(wave_sum_i64(pre));
+  const int64_t ctx = uniform64(wave_sum_i64(cb));
+  if (ctx == 0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (lane + i * kWave < D) out[lane + i * kWave] = __builtin_nanf("");
+    return;
+  }
+  const int64_t T = tot * a.NHG;
+  int64_t Q = a.range > 0 ? a.range : (T + a.W - 1) / a.W;
+  if (Q < 1) Q = 1;
+  const int hg = h / a.HB;
+  const int64_t g0 = pre * a.NHG + hg * ctx;
+  const int64_t j0 = g0 / Q, j1 = (g0 + ctx - 1) / Q;
+  if (j0 == j1) return;
+  // partial of range j0 + p: slot base + p * HB
+  const int64_t base = ((static_cast<int64_t>(b) * a.NHG + hg) + j0) * a.HB + h % a.HB;
+  const int np = static_cast<int>(j1 - j0 + 1);
+  auto ml = [&](int p) { return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2; };
   float M = kNegBig;
-  for (int p = lane; p < a.NP; p += kWave) M = fmaxf(M, a.part_ml[((base + p) * G + g) * 2]);
+  for (int p = lane; p < np; p += kWave) M = fmaxf(M, ml(p)[0]);
   M = lsh::wave_max_from<1>(M);
   float L = 0.f, o[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) o[i] = 0.f;
-  for (int p0 = 0; p0 < a.NP; p0 += kWave) {
-    const int pl = p0 + lane;
+  for (int p0 = 0; p0 < np; p0 += kWave) {
     float w = 0.f;
-    if (pl < a.NP) {
-      const int64_t pi = (base + pl) * G + g;
-      const float lp = a.part_ml[pi * 2 + 1];
-      w = lp == 0.f ? 0.f : __builtin_amdgcn_exp2f((a.part_ml[pi * 2] - M) * kLog2e);
+    if (p0 + lane < np) {
+      const float* pm = ml(p0 + lane);
+      const float lp = pm[1];
+      w = lp == 0.f ? 0.f : __builtin_amdgcn_exp2f(pm[0] - M);
       L += w * lp;
     }
-    const int n = a.NP - p0 < kWave ? a.NP - p0 : kWave;
-#pragma unroll 8
-    for (int j = 0; j < n; ++j) {
-      const float wj = __shfl(w, j, kWave);
-      if (wj == 0.f) continue;  // wave-uniform
-      const float* src = a.part_acc + ((base + p0 + j) * G + g) * D;
+    const int n = np - p0 < kWave ? np - p0 : kWave;
+    for (int j0b = 0; j0b < n; j0b += kMergeBatch) {
+      float v[kMergeBatch][PER];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int d = lane + i * kWave;
-        if (d < D) o[i] += wj * src[d];
+      for (int j = 0; j < kMergeBatch; ++j) {
+        const int jj = j0b + j < n ? j0b + j : n - 1;  // in-bounds row; its weight is zeroed below
+        const float* src =
+            a.part_acc + ((base + static_cast<int64_t>(p0 + jj) * a.HB) * G + g) * D;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int d = lane + i * kWave;
+          v[j][i] = d < D ? src[d] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        const float wj = j0b + j < n ? __shfl(w, j0b + j, kWave) : 0.f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) o[i] += wj * v[j][i];
       }
     }
   }
@@ -336,71 +520,107 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a, i
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int d = lane + i * kWave;
-    if (d < D) a.out[item * D + d] = o[i] * inv;
+    if (d < D) out[d] = o[i] * inv;
   }
 }
 
-// Partition size: a block multiple of at most kMaxPartBlocks blocks. Auto: ~8k wavefronts
-// over the context bound (max_blocks * block_size), at least 128 tokens each.
-int64_t round_partition(int64_t P, int64_t B, int64_t Hk, int64_t max_blocks, int64_t bs) {
-  const int64_t max_ctx = max_blocks * bs;
-  if (P <= 0) {
-    const int64_t parts = (8192 + B * Hk - 1) / (B * Hk);
-    P = (max_ctx + parts - 1) / parts;
-    if (P < 128) P = 128;
-  }
-  P = ((P + bs - 1) / bs) * bs;
-  if (P > kMaxPartBlocks * bs) P = kMaxPartBlocks * bs;
-  if (P > max_ctx && max_ctx > 0) P = ((max_ctx + bs - 1) / bs) * bs;
-  return P < bs ? bs : P;
-}
-
-// Resident workgroups of a kernel on the current device: CUs x blocks per CU (cached).
+// Resident workgroups of `waves` wavefronts of a kernel on the current device: CUs x blocks
+// per CU (cached per kernel, device and workgroup size).
 template <typename K>
-int resident_blocks(K kernel) {
-  static int cached[64][2] = {};  // [device] = {cus, blocks per CU}
+int resident_blocks(K kernel, int waves) {
+  static int cached[64][kMaxHeadsPerBlock + 1] = {};  // [device][waves]
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev][0] == 0) {
+  if (cached[dev][waves] == 0) {
     int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, kWavesPerBlock * kWave, 0) !=
-            hipSuccess || per < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, waves * kWave, 0) != hipSuccess ||
+        per < 1)
       per = 1;
-    cached[dev][1] = per;
-    cached[dev][0] = cus;
+    cached[dev][waves] = cus * per;
   }
-  return cached[dev][0] * cached[dev][1];
+  return cached[dev][waves];
+}
+
+// kv heads per decode workgroup: the largest divisor of Hk up to kMaxHeadsPerBlock.
+int heads_per_block(int64_t Hk) {
+  for (int hb = kMaxHeadsPerBlock; hb > 1; --hb)
+    if (Hk % hb == 0) return hb;
+  return 1;
+}
+
+// A step's block id is wave-uniform when each step lies inside one cache block (block size a
+// power of two and a multiple of the rows per step).
+bool scalar_blocks(int64_t D, int64_t block_size) {
+  return (block_size & (block_size - 1)) == 0 && block_size % (kWave / (D / 16)) == 0;
+}
+
+// Workgroups of the decode grid (all resident at once).
+template <int D, int G>
+int decode_blocks(bool scalar, int hb) {
+  return scalar ? resident_blocks(paged_decode_int8_kernel<D, G, true>, hb)
+                : resident_blocks(paged_decode_int8_kernel<D, G, false>, hb);
 }
 
 template <int D, int G>
-void launch_decode(const DecodeArgs& a, int B, hipStream_t st) {
-  const int64_t items = static_cast<int64_t>(B) * ((a.Hk + kWavesPerBlock - 1) / kWavesPerBlock) * a.NP;
-  const int64_t resident = resident_blocks(paged_decode_int8_kernel<D, G>);
-  const unsigned grid = static_cast<unsigned>(items < resident ? items : resident);
-  lsh::launch(paged_decode_int8_kernel<D, G>, dim3(grid), dim3(kWavesPerBlock * kWave), 0, st,
-              a.NP == 1, a);
-  if (a.NP > 1) {
-    const int64_t items = static_cast<int64_t>(B) * a.Hq;
-    lsh::launch(paged_decode_merge_kernel<D>,
-                dim3(static_cast<unsigned>((items + kWavesPerBlock - 1) / kWavesPerBlock)),
-                dim3(kWavesPerBlock * kWave), 0, st, true, a, B);
+void launch_decode(const DecodeArgs& a, bool scalar, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(a.W)), block(a.HB * kWave);
+  if (scalar)
+    lsh::launch(paged_decode_int8_kernel<D, G, true>, grid, block, 0, st, false, a);
+  else
+    lsh::launch(paged_decode_int8_kernel<D, G, false>, grid, block, 0, st, false, a);
+  const int64_t items = static_cast<int64_t>(a.B) * a.Hq;
+  lsh::launch(paged_decode_merge_kernel<D>,
+              dim3(static_cast<unsigned>((items + kMergeWaves - 1) / kMergeWaves)),
+              dim3(kMergeWaves * kWave), 0, st, true, a);
+}
+
+// Calls f.template operator()<D, G>() for the runtime (D, G); false when unsupported.
+template <typename F>
+bool with_shape(int64_t D, int64_t G, F&& f) {
+  auto g_switch = [&](auto dtag) {
+    constexpr int Dv = decltype(dtag)::value;
+    switch (G) {
+      case 1: f.template operator()<Dv, 1>(); return true;
+      case 2: f.template operator()<Dv, 2>(); return true;
+      case 3: f.template operator()<Dv, 3>(); return true;
+      case 4: f.template operator()<Dv, 4>(); return true;
+      case 5: f.template operator()<Dv, 5>(); return true;
+      case 6: f.template operator()<Dv, 6>(); return true;
+      case 7: f.template operator()<Dv, 7>(); return true;
+      case 8: f.template operator()<Dv, 8>(); return true;
+      default: return false;
+    }
+  };
+  switch (D) {
+    case 16: return g_switch(std::integral_constant<int, 16>{});
+    case 32: return g_switch(std::integral_constant<int, 32>{});
+    case 64: return g_switch(std::integral_constant<int, 64>{});
+    case 128: return g_switch(std::integral_constant<int, 128>{});
+    case 256: return g_switch(std::integral_constant<int, 256>{});
+    default: return false;
   }
 }
 
-template <int D>
-bool dispatch_g(int G, const DecodeArgs& a, int B, hipStream_t st) {
-  switch (G) {
-    case 1: launch_decode<D, 1>(a, B, st); return true;
-    case 2: launch_decode<D, 2>(a, B, st); return true;
-    case 3: launch_decode<D, 3>(a, B, st); return true;
-    case 4: launch_decode<D, 4>(a, B, st); return true;
-    case 5: launch_decode<D, 5>(a, B, st); return true;
-    case 6: launch_decode<D, 6>(a, B, st); return true;
-    case 7: launch_decode<D, 7>(a, B, st); return true;
-    case 8: launch_decode<D, 8>(a, B, st); return true;
-    default: return false;
-  }
+int grid_blocks(int64_t D, int64_t G, int64_t Hk, int64_t block_size) {
+  int w = 0;
+  const bool scalar = scalar_blocks(D, block_size);
+  const int hb = heads_per_block(Hk);
+  with_shape(D, G, [&]<int Dv, int Gv>() { w = decode_blocks<Dv, Gv>(scalar, hb); });
+  return w;
+}
+
+// Partial slots the workspace holds: HB per (b, head group) plus HB per work range (the
+// balanced split uses one range per resident workgroup; a fixed range size is bounded by the
+// longest possible work line).
+int64_t partial_slots(int64_t B, int64_t Hk, int64_t D, int64_t G, int64_t max_blocks,
+                      int64_t block_size, int64_t partition_size) {
+  const int64_t hb = heads_per_block(Hk), nhg = Hk / hb;
+  const int64_t ranges =
+      partition_size > 0
+          ? (B * nhg * max_blocks * block_size + partition_size - 1) / partition_size
+          : grid_blocks(D, G, Hk, block_size);
+  return (B * nhg + ranges) * hb;
 }
 
 }  // namespace
@@ -410,10 +630,10 @@ extern "C" int64_t llmserve_paged_attention_workspace_bytes(int64_t B, int64_t H
                                                             int64_t block_size,
                                                             int64_t partition_size) {
   if (B <= 0 || Hq <= 0 || Hk <= 0 || D <= 0 || max_blocks <= 0 || block_size <= 0) return 0;
-  const int64_t P = round_partition(partition_size, B, Hk, max_blocks, block_size);
-  const int64_t NP = (max_blocks * block_size + P - 1) / P;
-  if (NP <= 1) return 0;
-  return B * Hq * NP * (D + 2) * static_cast<int64_t>(sizeof(float));
+  if (Hq % Hk != 0 || Hq / Hk > 8) return 0;
+  const int64_t G = Hq / Hk;
+  const int64_t slots = partial_slots(B, Hk, D, G, max_blocks, block_size, partition_size);
+  return slots * G * (D + 2) * static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int llmserve_paged_attention_decode_int8(
@@ -433,24 +653,22 @@ extern "C" int llmserve_paged_attention_decode_int8(
             (long long)G);
   LSH_CHECK(D == 16 || D == 32 || D == 64 || D == 128 || D == 256,
             "paged_attention_decode_int8: head_dim %lld not in {16, 32, 64, 128, 256}", (long long)D);
-  LSH_CHECK(B <= 65535 && Hk <= 65535 * kWavesPerBlock, "paged_attention: grid too large");
-  LSH_CHECK(max_blocks * block_size < (1LL << 31) && num_slots / block_size < (1LL << 31),
+  LSH_CHECK(B < (1LL << 24) && Hk <= 4096, "paged_attention: batch or kv heads too large");
+  LSH_CHECK(max_blocks * block_size < (1LL << 31) && num_slots * Hk < (1LL << 31),
             "paged_attention: context or cache too long");
   LSH_CHECK(q && k_cache && v_cache && k_scale && v_scale && block_tables && context_lens && out,
             "paged_attention: null pointer");
   LSH_CHECK(lsh::aligned16(q) && lsh::aligned16(k_cache) && lsh::aligned16(v_cache) &&
                 lsh::aligned16(out) && (q_mult == nullptr || lsh::aligned16(q_mult)),
             "paged_attention: q, caches, out and q_mult must be 16-byte aligned");
-  const int64_t P = round_partition(partition_size, B, Hk, max_blocks, block_size);
-  const int64_t NP = (max_blocks * block_size + P - 1) / P;
-  const int64_t need =
-      llmserve_paged_attention_workspace_bytes(B, Hq, Hk, D, max_blocks, block_size, partition_size);
-  LSH_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+  const int64_t slots = partial_slots(B, Hk, D, G, max_blocks, block_size, partition_size);
+  const int64_t need = slots * G * (D + 2) * static_cast<int64_t>(sizeof(float));
+  LSH_CHECK(workspace != nullptr && workspace_bytes >= need,
             "paged_attention: workspace of %lld bytes needed, %lld given", (long long)need,
             (long long)workspace_bytes);
-  LSH_CHECK(need == 0 || lsh::aligned16(workspace), "paged_attention: workspace must be 16-byte aligned");
-  LSH_CHECK(NP < (1LL << 31), "paged_attention: too many partitions");
+  LSH_CHECK(lsh::aligned16(workspace), "paged_attention: workspace must be 16-byte aligned");
 
+  const bool scalar = scalar_blocks(D, block_size);
   DecodeArgs a{};
   a.q = q;
   a.kc = k_cache;
@@ -462,9 +680,10 @@ extern "C" int llmserve_paged_attention_decode_int8(
   a.q_mult = q_mult;
   a.out = out;
   float* ws = static_cast<float*>(workspace);
-  a.part_ml = NP > 1 ? ws : nullptr;
-  a.part_acc = NP > 1 ? ws + B * Hq * NP * 2 : nullptr;
+  a.part_ml = ws;
+  a.part_acc = ws + slots * G * 2;
   a.num_slots = num_slots;
+  a.range = partition_size > 0 ? partition_size : 0;
   a.B = static_cast<int>(B);
   a.Hq = static_cast<int>(Hq);
   a.Hk = static_cast<int>(Hk);
@@ -473,19 +692,13 @@ extern "C" int llmserve_paged_attention_decode_int8(
   a.bs_shift = -1;
   for (int sh = 0; sh < 31; ++sh)
     if ((1LL << sh) == block_size) a.bs_shift = sh;
-  a.P = static_cast<int>(P);
-  a.NP = static_cast<int>(NP);
-  a.scale = scale;
+  a.HB = heads_per_block(Hk);
+  a.NHG = static_cast<int>(Hk / a.HB);
+  a.W = grid_blocks(D, G, Hk, block_size);
+  a.qscale = scale * kLog2e;
+  LSH_CHECK(a.W >= 1, "paged_attention: no resident workgroups");
   hipStream_t st = lsh::as_stream(stream);
-  const int Bi = static_cast<int>(B), Gi = static_cast<int>(G);
-  bool ok = false;
-  switch (D) {
-    case 16: ok = dispatch_g<16>(Gi, a, Bi, st); break;
-    case 32: ok = dispatch_g<32>(Gi, a, Bi, st); break;
-    case 64: ok = dispatch_g<64>(Gi, a, Bi, st); break;
-    case 128: ok = dispatch_g<128>(Gi, a, Bi, st); break;
-    default: ok = dispatch_g<256>(Gi, a, Bi, st); break;
-  }
+  const bool ok = with_shape(D, G, [&]<int Dv, int Gv>() { launch_decode<Dv, Gv>(a, scalar, st); });
   LSH_CHECK(ok, "paged_attention: unsupported G=%lld", (long long)G);
   return lsh::launch_status("paged_attention_decode_int8");
 }

@@ -74,10 +74,22 @@ def test_paged_attention_argument_checks(lib):
 
 def test_paged_attention_workspace_size(lib):
     ws = lib.llmserve_paged_attention_workspace_bytes
-    # one partition -> no workspace
-    assert ws(4, 16, 8, 128, 4, 16, 10_000) == 0
-    # forced 32-token partitions over a 256-token bound: NP = 8
-    assert ws(2, 16, 8, 128, 16, 16, 32) == 2 * 16 * 8 * (128 + 2) * 4
+
+    def expect(B, Hq, Hk, D, max_blocks, bs, P, HB):
+        # (B * NHG + ranges) * HB partial slots of G (m, l, acc[D]) rows; with a fixed range
+        # size the ranges are bounded by the longest work line, B * NHG * max_blocks * bs
+        nhg, G = Hk // HB, Hq // Hk
+        ranges = -(-B * nhg * max_blocks * bs // P)
+        return (B * nhg + ranges) * HB * G * (D + 2) * 4
+
+    # 8 kv heads share a workgroup; one range covers the whole line
+    assert ws(4, 16, 8, 128, 4, 16, 10_000) == expect(4, 16, 8, 128, 4, 16, 10_000, 8)
+    # 32-token ranges over a 2 x 256-token bound: 16 ranges
+    assert ws(2, 16, 8, 128, 16, 16, 32) == expect(2, 16, 8, 128, 16, 16, 32, 8)
+    # 6 kv heads: groups of 6
+    assert ws(1, 12, 6, 64, 2, 16, 16) == expect(1, 12, 6, 64, 2, 16, 16, 6)
+    # 16 kv heads: two groups of 8
+    assert ws(3, 32, 16, 64, 5, 16, 40) == expect(3, 32, 16, 64, 5, 16, 40, 8)
     assert ws(0, 16, 8, 128, 16, 16, 32) == 0
 
 
