@@ -237,6 +237,24 @@ def extra_configs(torch, dev) -> dict:
                            "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}
     del qs
     # config 4
+    copies, q, cl, qm, bs, D, b = c4_inputs(torch, dev)
+    pa = load_paged_attention()
+
+    def launch(i):
+        kq, vq, ks, vs, bt = copies[i % len(copies)]
+        pa.paged_attention_decode_int8(q, kq, vq, ks, vs, bt, cl, bs, D ** -0.5, 0, qm)
+
+    us = kernel_avg_us(torch, launch, 40)
+    out["c4_int8kv_paged_decode"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                                     "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}
+    return out
+
+
+def c4_inputs(torch, dev):
+    """Config 4: 4 copies (~1.1 GB) of an int8 KV cache for 32 sequences, ctx ~ U[512, 8192],
+    block tables a random permutation of the physical blocks."""
+    import numpy as np
+
     rng = np.random.default_rng(2024)
     B, Hq, Hk, D, bs = 32, 16, 8, 128, 16
     ctx = rng.integers(512, 8193, B)
@@ -244,7 +262,7 @@ def extra_configs(torch, dev) -> dict:
     total = int(nblk.sum())
     width = int(nblk.max())
     copies = []
-    for c in range(4):  # 4 x ~300 MB of cache
+    for _ in range(4):
         perm = rng.permutation(total)
         bt = np.zeros((B, width), np.int64)
         used = 0
@@ -259,17 +277,39 @@ def extra_configs(torch, dev) -> dict:
     q = torch.randn(B, Hq, D, device=dev)
     cl = torch.from_numpy(ctx.astype(np.int64)).to(dev)
     qm = torch.rand(Hq, D, device=dev) + 0.5
-    pa = load_paged_attention()
+    nbytes = int(ctx.sum()) * Hk * (2 * D + 8) + 8 * B * Hq * D + 8 * int(nblk.sum()) + 4 * Hq * D
+    return copies, q, cl, qm, bs, D, nbytes
 
-    def launch(i):
-        kq, vq, ks, vs, bt = copies[i % len(copies)]
-        pa.paged_attention_decode_int8(q, kq, vq, ks, vs, bt, cl, bs, D ** -0.5, 0, qm)
 
-    us = kernel_avg_us(torch, launch, 40)
-    b = int(ctx.sum()) * Hk * (2 * D + 8) + 8 * B * Hq * D + 8 * int(nblk.sum()) + 4 * Hq * D
-    out["c4_int8kv_paged_decode"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
-                                     "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}
-    return out
+def profile_only(torch, dev, what: str) -> int:
+    """64 launches of one kernel, for rocprofv3 counter runs (no timing output)."""
+    from llmserve.kernels import load_int8_gemv, load_paged_attention, load_quant
+
+    if what == "gemv":  # the dominant kernel: int4 g128 GEMV at the gate_up shape, M = 1
+        N, K = SHAPES["gate_up"]
+        g = torch.Generator(device=dev).manual_seed(3)
+        lins = [load_quant().int4_quantize(torch.randn(N, K, device=dev, generator=g) * 0.02, GROUP,
+                                           torch.rand(K, device=dev, generator=g) + 0.5)
+                for _ in range(64)]
+        x = torch.randn(1, K, device=dev, generator=g)
+        gemv = load_int8_gemv()
+        for i in range(64):
+            nib, gs, gz, inv = lins[i]
+            gemv.int4_linear(x, nib, gs, gz, GROUP, inv)
+    elif what == "attention":
+        copies, q, cl, qm, bs, D, _ = c4_inputs(torch, dev)
+        pa = load_paged_attention()
+        for i in range(64):
+            kq, vq, ks, vs, bt = copies[i % len(copies)]
+            pa.paged_attention_decode_int8(q, kq, vq, ks, vs, bt, cl, bs, D ** -0.5, 0, qm)
+    else:  # copy of 256 MiB: the reference for scaling FETCH_SIZE / WRITE_SIZE
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).random_(0, 255)
+        dst = torch.empty_like(src)
+        for _ in range(64):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] profile run done: {what}")
+    return 0
 
 
 def main() -> int:
@@ -279,6 +319,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1 and 4")
+    ap.add_argument("--only", choices=["gemv", "attention", "copy"],
+                    help="profiling run: only launch that kernel (64 times) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run --gpus 1)",
@@ -290,6 +332,8 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.manual_seed(0)
+    if args.only:
+        return profile_only(torch, dev, args.only)
     log("[bench] quantizing 4 copies of the Qwen3-0.6B linears (int4 g128 AWQ)")
     model, calib = build_weights(torch, dev)
     gemv = load_int8_gemv()
