@@ -19,7 +19,8 @@ llmserve_time_next_call) on the stream it runs on — the interval a kernel-trac
 reports. `cpu_baseline` times the reference's own CPU
 kernels (oracle/_ref, built from the reference sources) — or the oracle's C restatement where
 that build is absent — on the host cores, on the same quantized weights, for about 10 s.
-Extra fields report M = 4 / 16 steps and configs 1 (int8 GEMV) and 4 (int8-KV decode).
+Extra fields report M = 4 / 16 steps and configs 1 (int8 GEMV), 3 (prefill int8 GEMM on the
+bf16 matrix cores, x conversion included) and 4 (int8-KV decode).
 """
 
 from __future__ import annotations
@@ -37,6 +38,7 @@ for _p in (REPO, REPO / "llm-serving-engine_amd"):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_TFLOPS = 2500.0  # MI355X dense bf16
 LAYERS = 28
 SHAPES = {"qkv": (4096, 1024), "o": (1024, 2048), "gate_up": (6144, 1024), "down": (1024, 3072)}
 GROUP = 128
@@ -236,6 +238,18 @@ def extra_configs(torch, dev) -> dict:
     out["c1_int8_gemv"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
                            "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}
     del qs
+    # config 3: prefill-sized int8 GEMMs (M = 2048) on the bf16 matrix cores
+    c3 = {}
+    for name, (N3, K3) in {"qkv": (6144, 2048), "gate_up": (16384, 2048), "down": (2048, 8192)}.items():
+        x3 = torch.randn(2048, K3, device=dev, generator=g)
+        ws3 = [load_quant().int8_quantize(torch.randn(N3, K3, device=dev, generator=g) * 0.02)
+               for _ in range(2)]
+        us3 = kernel_avg_us(torch, lambda i: gemv.int8_linear_prefill(x3, *ws3[i % 2]), 20)
+        fl = 2.0 * 2048 * N3 * K3
+        c3[name] = {"us": round(us3, 2), "TFLOPs": round(fl / us3 / 1e6, 1),
+                    "mfma_frac": round(fl / us3 / 1e6 / MFMA_BF16_TFLOPS, 4), "flops": fl}
+        del x3, ws3
+    out["c3_int8_prefill_gemm_bf16"] = c3
     # config 4
     copies, q, cl, qm, bs, D, b = c4_inputs(torch, dev)
     pa = load_paged_attention()

@@ -112,6 +112,20 @@ int llmserve_int4_linear(const float* x, const float* inv_act_scale /* nullable 
                          float* y, int64_t M, int64_t N, int64_t K, int64_t group_size,
                          void* stream);
 
+/*
+ * Prefill-sized int8 weight-only linear on the bf16 matrix cores (replaces Int8Linear's
+ * large-M path, quant.py:71-72 with dequantize quant.py:78-79: x @ (q * scale[:, None]).T):
+ *   y[m, n] = scale[n] * sum_k bf16(x[m, k]) * q[n, k]      (fp32 accumulate)
+ * x is rounded to bf16 (nearest even) once into `workspace`; the int8 weight is exact in
+ * bf16. x fp32 [M,K], q int8 [N,K], scale fp32 [N] -> y fp32 [M,N]. K must be a multiple of
+ * 32; x, q and the workspace 16-byte aligned; the workspace holds
+ * llmserve_int8_linear_prefill_workspace_bytes(M, K) bytes (the bf16 copy of x).
+ */
+int64_t llmserve_int8_linear_prefill_workspace_bytes(int64_t M, int64_t K);
+int llmserve_int8_linear_prefill(const float* x, const int8_t* qweight, const float* scale,
+                                 float* y, int64_t M, int64_t N, int64_t K, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+
 /* ---- int8-KV paged decode attention ------------------------------------------------------ */
 
 /*

@@ -124,6 +124,30 @@ at::Tensor int8_linear(const at::Tensor& x, const at::Tensor& qweight, const at:
   return y;
 }
 
+at::Tensor int8_linear_prefill(const at::Tensor& x, const at::Tensor& qweight,
+                               const at::Tensor& scale) {
+  TORCH_CHECK(x.scalar_type() == at::kFloat && qweight.scalar_type() == at::kChar &&
+                  scale.scalar_type() == at::kFloat,
+              "int8_linear_prefill: dtypes");
+  TORCH_CHECK(x.is_contiguous() && qweight.is_contiguous() && scale.is_contiguous(),
+              "int8_linear_prefill: contiguous inputs");
+  TORCH_CHECK(x.dim() == 2 && qweight.dim() == 2, "int8_linear_prefill: 2-D x and qweight");
+  check_device(x, {&qweight, &scale}, "int8_linear_prefill");
+  const int64_t M = x.size(0), K = x.size(1), N = qweight.size(0);
+  TORCH_CHECK(qweight.size(1) == K, "int8_linear_prefill: K mismatch");
+  TORCH_CHECK(scale.numel() == N,
+              "int8_linear_prefill: scale must have one entry per output channel");
+  const c10::DeviceGuard guard(x.device());
+  auto y = at::empty({M, N}, x.options());
+  const int64_t ws_bytes = llmserve_int8_linear_prefill_workspace_bytes(M, K);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({(ws_bytes + 15) / 16 * 4}, x.options());
+  check_status(llmserve_int8_linear_prefill(
+      x.data_ptr<float>(), qweight.data_ptr<int8_t>(), scale.data_ptr<float>(), y.data_ptr<float>(),
+      M, N, K, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(x)));
+  return y;
+}
+
 at::Tensor int4_linear(const at::Tensor& x, const at::Tensor& nibbles, const at::Tensor& scale,
                        const at::Tensor& zero, int64_t group_size,
                        const std::optional<at::Tensor>& inv_act_scale) {
@@ -218,6 +242,7 @@ TORCH_LIBRARY(llmserve_hip, m) {
   m.def("kv_quantize_write(Tensor x, Tensor slots, Tensor(a!) data, Tensor(b!) scale,"
         " Tensor? smooth=None) -> ()");
   m.def("int8_linear(Tensor x, Tensor qweight, Tensor scale) -> Tensor");
+  m.def("int8_linear_prefill(Tensor x, Tensor qweight, Tensor scale) -> Tensor");
   m.def("int4_linear(Tensor x, Tensor nibbles, Tensor scale, Tensor zero, int group_size,"
         " Tensor? inv_act_scale=None) -> Tensor");
   m.def("paged_attention_decode_int8(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale,"
@@ -230,6 +255,7 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("int4_quantize", &int4_quantize);
   m.impl("kv_quantize_write", &kv_quantize_write);
   m.impl("int8_linear", &int8_linear);
+  m.impl("int8_linear_prefill", &int8_linear_prefill);
   m.impl("int4_linear", &int4_linear);
   m.impl("paged_attention_decode_int8", &paged_attention_decode_int8);
 }

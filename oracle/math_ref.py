@@ -24,6 +24,27 @@ def int8_linear_f64(x, q, scale):
     return linear_f64(x, oq.int8_dequantize(q, scale))
 
 
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bfloat16 (ties to even), returned as float32: the rounding of
+    torch's float32 -> bfloat16 cast and of gfx950's v_cvt_pk_bf16_f32. Finite inputs only.
+    Pinned by tests/test_oracle_math.py against torch's CPU cast on random values, exact
+    ties (both parities), signed zeros, subnormals and values that round up to a new binade."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
+    return r.astype(np.uint32).view(np.float32)
+
+
+def int8_linear_prefill_f64(x, q, scale, round_x: bool = True):
+    """Int8Linear's large-M path (reference quant.py:71-72): x @ (q * scale[:, None]).T in
+    float64. With round_x, x is first rounded to bfloat16 — what the bf16 matrix-core GEMM
+    computes exactly up to its float32 accumulation; without, the weight-only product the
+    stated bf16 tolerance is measured against."""
+    x = np.asarray(x, np.float32)
+    xr = bf16_round(x) if round_x else x
+    y = np.asarray(xr, np.float64) @ np.asarray(q, np.float64).T
+    return y * np.asarray(scale, np.float64)[None, :]
+
+
 def int4_linear_f64(x, nib, g_scale, g_zero, group_size, inv_act_scale=None):
     """Int4Linear.forward: x * inv_act_scale (float32), then x @ dequantize()^T."""
     x = np.asarray(x, np.float32)

@@ -65,6 +65,18 @@ def int4_linear(x, nib, gs, gz, group, inv=None):
     return y
 
 
+def int8_linear_prefill(x, q, s):
+    M, K = x.shape
+    N = q.shape[0]
+    y = torch.empty(M, N, dtype=torch.float32, device=x.device)
+    L = capi()
+    nbytes = L.llmserve_int8_linear_prefill_workspace_bytes(M, K)
+    ws = torch.empty(max(nbytes, 16) // 4 + 4, dtype=torch.float32, device=x.device)
+    check(L.llmserve_int8_linear_prefill(_p(x), _p(q), _p(s), _p(y), M, N, K, _p(ws), nbytes,
+                                         _stream()))
+    return y
+
+
 def paged_decode_int8(q, kc, vc, ks, vs, bt, cl, block_size, scale, partition_size=0, q_mult=None):
     B, Hq, D = q.shape
     num_slots, Hk = kc.shape[0], kc.shape[1]

@@ -68,3 +68,39 @@ def test_paged_decode_closed_forms():
     out = mr.paged_decode_f64(q, k_same, v, bt, cl, bs, 0.3)
     slots = mr.context_slots(bt[0], int(cl[0]), bs)
     np.testing.assert_allclose(out[0], np.repeat(v[slots].astype(np.float64).mean(0), 2, axis=0), atol=1e-12)
+
+
+def test_bf16_round_matches_torch_cast():
+    """bf16_round against torch's CPU float32 -> bfloat16 cast (round half to even)."""
+    rng = np.random.default_rng(11)
+    x = np.concatenate([
+        rng.standard_normal(4096).astype(np.float32) * np.float32(10) ** rng.integers(-30, 30, 4096),
+        # exact ties: low half 0x8000 with an even and an odd kept mantissa
+        np.array([0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000], np.uint32).view(np.float32),
+        # just below / above a tie, rounding into the next binade, signed zeros, subnormals
+        np.array([0x3F807FFF, 0x3F808001, 0x3FFFFFFF, 0x7F7FFFFF - 0x10000, 0x80000000, 0x00000000,
+                  0x00000001, 0x8000FFFF, 0x007F8000], np.uint32).view(np.float32),
+    ]).astype(np.float32)
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    got = mr.bf16_round(x)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    # a plausible mistake, truncation instead of rounding, is caught
+    trunc = (x.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    assert not np.array_equal(trunc.view(np.uint32), want.view(np.uint32))
+
+
+def test_prefill_reference_brute_force():
+    """int8_linear_prefill_f64 = sum_k bf16(x) q scale, by loops on a tiny case; without the
+    rounding it is the plain weight-only product."""
+    rng = np.random.default_rng(12)
+    M, N, K = 3, 5, 7
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    q = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    s = (rng.random(N) * 0.01 + 1e-3).astype(np.float32)
+    xr = torch.from_numpy(x).to(torch.bfloat16).to(torch.float64).numpy()
+    want = np.array([[sum(xr[m, k] * float(q[n, k]) for k in range(K)) * float(s[n])
+                      for n in range(N)] for m in range(M)])
+    np.testing.assert_allclose(mr.int8_linear_prefill_f64(x, q, s), want, rtol=1e-13, atol=0)
+    plain = mr.int8_linear_f64(x, q, s)
+    np.testing.assert_allclose(mr.int8_linear_prefill_f64(x, q, s, round_x=False), plain,
+                               rtol=1e-6, atol=1e-12)
