@@ -310,6 +310,14 @@ def profile_only(torch, dev, what: str) -> int:
         for i in range(64):
             nib, gs, gz, inv = lins[i]
             gemv.int4_linear(x, nib, gs, gz, GROUP, inv)
+    elif what == "prefill":  # config 3 gate_up: M = 2048, 2048 -> 16384
+        g = torch.Generator(device=dev).manual_seed(4)
+        x = torch.randn(2048, 2048, device=dev, generator=g)
+        qs = [load_quant().int8_quantize(torch.randn(16384, 2048, device=dev, generator=g) * 0.02)
+              for _ in range(2)]
+        gemv = load_int8_gemv()
+        for i in range(16):
+            gemv.int8_linear_prefill(x, *qs[i % 2])
     elif what == "attention":
         copies, q, cl, qm, bs, D, _ = c4_inputs(torch, dev)
         pa = load_paged_attention()
@@ -333,7 +341,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1 and 4")
-    ap.add_argument("--only", choices=["gemv", "attention", "copy"],
+    ap.add_argument("--only", choices=["gemv", "attention", "prefill", "copy"],
                     help="profiling run: only launch that kernel (64 times) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

@@ -118,10 +118,12 @@ int llmserve_int4_linear(const float* x, const float* inv_act_scale /* nullable 
  *   y[m, n] = scale[n] * sum_k bf16(x[m, k]) * q[n, k]      (fp32 accumulate)
  * x is rounded to bf16 (nearest even) once into `workspace`; the int8 weight is exact in
  * bf16. x fp32 [M,K], q int8 [N,K], scale fp32 [N] -> y fp32 [M,N]. K must be a multiple of
- * 32; x, q and the workspace 16-byte aligned; the workspace holds
- * llmserve_int8_linear_prefill_workspace_bytes(M, K) bytes (the bf16 copy of x).
+ * 64; x, q and the workspace 16-byte aligned; the workspace holds
+ * llmserve_int8_linear_prefill_workspace_bytes(M, N, K) bytes: the bf16 copy of x and, when
+ * the output has fewer 256 x 256 tiles than the device has CUs, the fp32 partial sums of the
+ * K splits (their count depends on the current device).
  */
-int64_t llmserve_int8_linear_prefill_workspace_bytes(int64_t M, int64_t K);
+int64_t llmserve_int8_linear_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int llmserve_int8_linear_prefill(const float* x, const int8_t* qweight, const float* scale,
                                  float* y, int64_t M, int64_t N, int64_t K, void* workspace,
                                  int64_t workspace_bytes, void* stream);

@@ -5,24 +5,30 @@
 // (reference quant.py:71-72, dequantize :78-79: x @ (q * scale[:, None]).T) with the
 // per-channel scale moved to the epilogue.
 //
-// Tiling: a 256-thread workgroup owns a 256 x 256 output tile; its four wavefronts own
-// 128 x 128 quadrants, each a grid of 8 x 8 v_mfma_f32_16x16x32_bf16 tiles (256 fp32
-// accumulators per lane). K advances 32 at a time through two LDS stages (A: 256 rows x 32
-// bf16 of x; B: 256 rows x 32 weights, widened int8 -> fp32 -> bf16 on the way into LDS):
-// while the wavefronts run the 64 MFMAs of one stage, the next stage's global loads are in
-// flight. LDS rows are 64 bytes (four 16-byte chunks); chunk c of row r sits at position
-// c ^ ((r >> 1) & 3), so the 8 rows a ds_read_b128 quarter-wave touches hit distinct banks.
+// Tiling: a 256-thread workgroup owns a 256 x 256 output tile (or, split-K, one K range of
+// it); its four wavefronts (one per SIMD, 512 registers each) own 128 x 128 quadrants, each a
+// grid of 8 x 8 v_mfma_f32_16x16x32_bf16 tiles (256 fp32 accumulators per lane, in AGPRs). K advances 64 per stage:
+// A = 256 rows x 64 bf16 of x, B = 256 rows x 64 weights widened int8 -> fp32 -> bf16 on the
+// way into LDS. Two LDS buffers: the global loads of stage s + 1 are in flight (in registers)
+// while the 128 MFMAs per wavefront of stage s run from LDS, then go to the other buffer.
+// LDS rows are 128 bytes (eight 16-byte chunks); chunk c of row r sits at position
+// c ^ (r & 7) ^ ((r >> 3) & 1): the 16 rows of one ds_read_b128 fragment load then fall on
+// distinct banks whether the LDS serves 8 lanes from 32 banks or 16 lanes from 64 banks.
 // MFMA operands (16x16x32 bf16): lane l supplies row l % 16 of the A tile and column l % 16
 // of the B tile, k = 8 (l / 16) .. + 8; the result lane l holds rows 4 (l / 16) + r, column
 // l % 16.
-// Tiles map to blocks XCD-aware: block b runs on XCD b % 8, and each XCD gets whole columns of
-// tiles, so a weight panel is read from HBM into one XCD's L2 and reused there by every row
-// tile of the column.
+// Split-K: when the output has fewer tiles than the GPU has CUs, each tile's K range is split
+// (into at most 4, each a multiple of 64) and every split writes fp32 partials that a second
+// kernel sums in split order, applying scale[n] (deterministic, no atomics).
+// Units map to blocks XCD-aware: block b runs on XCD b % 8, and each XCD gets whole columns
+// of units (a tile column and its splits), so a weight panel is read from HBM into one XCD's
+// L2 and reused there by every row tile of the column.
 #include "common.h"
 
 namespace {
 
-constexpr int kBM = 256, kBN = 256, kBK = 32;
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kMaxSplits = 4;
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
 
@@ -47,7 +53,9 @@ __global__ __launch_bounds__(256) void x_to_bf16(const float* __restrict__ x, __
   }
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return chunk ^ (row & 7) ^ ((row >> 3) & 1);
+}
 
 // 16 int8 -> 16 bf16 (two 16-byte chunks), exact.
 __device__ __forceinline__ void widen16(const u32x4& w, u32x4& lo, u32x4& hi) {
@@ -66,66 +74,75 @@ struct GemmArgs {
   const int8_t* q;      // [N, K]
   const float* scale;   // [N]
   float* y;             // [M, N]
+  float* part;          // [splits, M, N] fp32 partials (splits > 1)
   int M, N, K;
-  int tiles_m, tiles_n;
+  int tiles_m, tiles_n, splits, k_split;  // k_split = K per split (multiple of kBK)
+};
+
+// One stage of global data held in registers: A (8 x 16 B: rows t / 8 + 32 i, chunk t % 8)
+// and B (4 x 16 B int8: rows t / 4 + 64 i, bytes 16 (t % 4) .. + 16).
+struct Stage {
+  u32x4 a[8], b[4];
 };
 
 __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) u32x4 lds_a[2][kBM * 4];  // [stage][row * 4 + chunk]
-  __shared__ __attribute__((aligned(16))) u32x4 lds_b[2][kBN * 4];
+  // [buf][row][8 chunks of 16 B]; A and B halves of one LDS stage
+  __shared__ __attribute__((aligned(16))) char lds[2 * 2 * kBM * 128];
+  constexpr int kBufBytes = 2 * kBM * 128;  // one stage: A (32 KB) then B (32 KB)
+  constexpr int kBOff = kBM * 128;
 
-  // XCD-aware tile order: block b runs on XCD b % 8; XCD x takes tile columns
-  // [x * tiles_n / 8, (x + 1) * tiles_n / 8) when tiles_n is a multiple of 8.
+  // XCD-aware unit order over "columns" (tile column, split): block b runs on XCD b % 8,
+  // XCD x takes columns [x * cols / 8, (x + 1) * cols / 8) when cols is a multiple of 8.
+  const int cols = a.tiles_n * a.splits;
   const int b = blockIdx.x;
-  int tm, tn;
-  if (a.tiles_n % kXcds == 0) {
+  int tm, col;
+  if (cols % kXcds == 0) {
     const int x = b % kXcds, idx = b / kXcds;
     tm = idx % a.tiles_m;
-    tn = x * (a.tiles_n / kXcds) + idx / a.tiles_m;
+    col = x * (cols / kXcds) + idx / a.tiles_m;
   } else {
     tm = b % a.tiles_m;
-    tn = b / a.tiles_m;
+    col = b / a.tiles_m;
   }
+  const int tn = col / a.splits, split = col % a.splits;
   const int m0 = tm * kBM, n0 = tn * kBN;
+  const int kbeg = split * a.k_split;
 
   const int t = threadIdx.x;
   const int lane = t % 64, wave = t / 64;
   const int wm = wave / 2, wn = wave % 2;  // 128 x 128 quadrant
+  const int K = a.K;
 
-  // global -> register loads of one K stage. A: thread t loads rows t / 4 + 64 i (i < 4),
-  // chunk t % 4 (8 bf16). B: rows t / 2 + 128 i (i < 2), bytes 16 (t % 2) .. + 16.
-  const int64_t K = a.K;
+  // Global loads: a lane-constant byte offset, the stage's k (and the row block i) in the
+  // scalar offset. A: rows t / 8 + 32 i, chunk t % 8; B: rows t / 4 + 64 i, 16 bytes t % 4.
   const auto ra = rsrc(a.xb, static_cast<int64_t>(a.M) * K * 2);
   const auto rb = rsrc(a.q, static_cast<int64_t>(a.N) * K);
-  u32x4 ga[4], gb[2];
-  auto load_stage = [&](int k0) {
+  const int ga_off = ((m0 + t / 8) * K + 8 * (t % 8)) * 2;
+  const int gb_off = (n0 + t / 4) * K + 16 * (t % 4);
+  auto load_stage = [&](Stage& g, int k0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = t / 4 + 64 * i;
-      const int64_t off = ((m0 + row) * K + k0 + 8 * (t % 4)) * 2;  // bytes
-      // rows past M read zeros (buffer bound); offsets past 2^31 cannot occur (checked on host)
-      ga[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, static_cast<int>(off), 0, 0));
-    }
+    for (int i = 0; i < 8; ++i)
+      g.a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             ra, ga_off, (k0 + i * 32 * K) * 2, 0));
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = t / 2 + 128 * i;
-      const int64_t off = (n0 + row) * K + k0 + 16 * (t % 2);
-      gb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, static_cast<int>(off), 0, 0));
-    }
+    for (int i = 0; i < 4; ++i)
+      g.b[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rb, gb_off, k0 + i * 64 * K, 0));
   };
-  auto store_stage = [&](int s) {
+  // LDS stores: the swizzle of rows t / 8 + 32 i (A) and t / 4 + 64 i (B) depends on t only.
+  const int sa_off = (t / 8) * 128 + swz(t / 8, t % 8) * 16;
+  const int sb_off0 = (t / 4) * 128 + swz(t / 4, 2 * (t % 4)) * 16;
+  const int sb_off1 = (t / 4) * 128 + swz(t / 4, 2 * (t % 4) + 1) * 16;
+  auto store_stage = [&](const Stage& g, int buf) {
+    char* base = lds + buf * kBufBytes;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(base + sa_off + i * 32 * 128) = g.a[i];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = t / 4 + 64 * i;
-      lds_a[s][row * 4 + swz(row, t % 4)] = ga[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = t / 2 + 128 * i;
       u32x4 lo, hi;
-      widen16(gb[i], lo, hi);
-      lds_b[s][row * 4 + swz(row, 2 * (t % 2))] = lo;
-      lds_b[s][row * 4 + swz(row, 2 * (t % 2) + 1)] = hi;
+      widen16(g.b[i], lo, hi);
+      *reinterpret_cast<u32x4*>(base + kBOff + sb_off0 + i * 64 * 128) = lo;
+      *reinterpret_cast<u32x4*>(base + kBOff + sb_off1 + i * 64 * 128) = hi;
     }
   };
 
@@ -135,56 +152,101 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int kt_n = a.K / kBK;
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
-  const int fr = lane % 16, fc = lane / 16;  // fragment row, k chunk
-  for (int kt = 0; kt < kt_n; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < kt_n) load_stage((kt + 1) * kBK);
-    bf16x8 fa[8], fb[8];
+  // Fragment reads: rows wm * 128 + 16 i + fr (A) and wn * 128 + 16 j + fr (B); the swizzle
+  // of such a row depends on fr only, so each substep has one lane offset per operand.
+  const int fr = lane % 16, fc = lane / 16;
+  int fa_off[kBK / 32], fb_off[kBK / 32];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int ra_row = wm * 128 + 16 * i + fr;
-      fa[i] = __builtin_bit_cast(bf16x8, lds_a[s][ra_row * 4 + swz(ra_row, fc)]);
-    }
+  for (int sub = 0; sub < kBK / 32; ++sub) {
+    fa_off[sub] = (wm * 128 + fr) * 128 + swz(fr, 4 * sub + fc) * 16;
+    fb_off[sub] = kBOff + (wn * 128 + fr) * 128 + swz(fr, 4 * sub + fc) * 16;
+  }
+  auto compute = [&](int buf) {
+    const char* base = lds + buf * kBufBytes;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int rb_row = wn * 128 + 16 * j + fr;
-      fb[j] = __builtin_bit_cast(bf16x8, lds_b[s][rb_row * 4 + swz(rb_row, fc)]);
-    }
+    for (int sub = 0; sub < kBK / 32; ++sub) {
+      bf16x8 fa[8], fb[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 8; ++i)
+        fa[i] = *reinterpret_cast<const bf16x8*>(base + fa_off[sub] + i * 16 * 128);
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    if (kt + 1 < kt_n) store_stage(s ^ 1);
+        fb[j] = *reinterpret_cast<const bf16x8*>(base + fb_off[sub] + j * 16 * 128);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // stage s + 1 is loaded into registers while stage s is computed from LDS, then stored to
+  // the other LDS buffer; one barrier per stage
+  const int n = a.k_split / kBK;
+  Stage g;
+  load_stage(g, kbeg);
+  store_stage(g, 0);
+  __syncthreads();
+  for (int kt = 0; kt < n; ++kt) {
+    if (kt + 1 < n) load_stage(g, kbeg + (kt + 1) * kBK);
+    compute(kt & 1);
+    if (kt + 1 < n) store_stage(g, (kt + 1) & 1);
     __syncthreads();
   }
 
-  // epilogue: y = acc * scale[n]; lane holds rows 4 (lane / 16) + r, column lane % 16
+  // epilogue: lane holds rows 4 (lane / 16) + r, column lane % 16 of each 16 x 16 tile
+  float* dst = a.splits > 1 ? a.part + static_cast<int64_t>(split) * a.M * a.N : a.y;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int n = n0 + wn * 128 + 16 * j + fr;
-    if (n >= a.N) continue;
-    const float sc = a.scale[n];
+    const int nn = n0 + wn * 128 + 16 * j + fr;
+    if (nn >= a.N) continue;
+    const float sc = a.splits > 1 ? 1.f : a.scale[nn];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + wm * 128 + 16 * i + 4 * fc + r;
-        if (m < a.M) a.y[static_cast<int64_t>(m) * a.N + n] = acc[i][j][r] * sc;
+        if (m < a.M) dst[static_cast<int64_t>(m) * a.N + nn] = acc[i][j][r] * sc;
       }
     }
   }
 }
 
+// y[m, n] = scale[n] * sum_s part[s, m, n], summed in split order.
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ part,
+                                                     const float* __restrict__ scale,
+                                                     float* __restrict__ y, int64_t MN, int N,
+                                                     int splits) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < MN; i += stride) {
+    float s = part[i];
+    for (int k = 1; k < splits; ++k) s += part[k * MN + i];
+    y[i] = s * scale[i % N];
+  }
+}
+
+// K splits for an M x N x K problem: enough (tile, split) units to give every CU one, at most
+// kMaxSplits, each split a multiple of kBK.
+int prefill_splits(int64_t M, int64_t N, int64_t K) {
+  int cus = 256, dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
+      cus = c;
+  }
+  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  int s = 1;
+  while (s < kMaxSplits && tiles * s * 2 <= cus && K % (static_cast<int64_t>(2 * s) * kBK) == 0) s *= 2;
+  return s;
+}
+
 }  // namespace
 
-extern "C" int64_t llmserve_int8_linear_prefill_workspace_bytes(int64_t M, int64_t K) {
-  if (M <= 0 || K <= 0) return 0;
-  return M * K * 2;
+extern "C" int64_t llmserve_int8_linear_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const int64_t xb = (M * K * 2 + 255) / 256 * 256;  // bf16 copy of x
+  const int s = prefill_splits(M, N, K);
+  return xb + (s > 1 ? s * M * N * static_cast<int64_t>(sizeof(float)) : 0);
 }
 
 extern "C" int llmserve_int8_linear_prefill(const float* x, const int8_t* qweight,
@@ -198,10 +260,10 @@ extern "C" int llmserve_int8_linear_prefill(const float* x, const int8_t* qweigh
   LSH_CHECK(x && qweight && scale && y, "int8_linear_prefill: null pointer");
   LSH_CHECK(lsh::aligned16(x) && lsh::aligned16(qweight),
             "int8_linear_prefill: x and qweight must be 16-byte aligned");
-  // buffer offsets are 32-bit: the bf16 copy of x and the weight must stay under 2 GiB
+  // buffer offsets are 32-bit: the bf16 copy of x and the weight stay under 2 GiB
   LSH_CHECK((M + kBM) * K * 2 < (1LL << 31) && (N + kBN) * K < (1LL << 31),
             "int8_linear_prefill: x (bf16) or weight over 2 GiB");
-  const int64_t need = llmserve_int8_linear_prefill_workspace_bytes(M, K);
+  const int64_t need = llmserve_int8_linear_prefill_workspace_bytes(M, N, K);
   LSH_CHECK(workspace != nullptr && workspace_bytes >= need && lsh::aligned16(workspace),
             "int8_linear_prefill: 16-byte aligned workspace of %lld bytes needed, %lld given",
             (long long)need, (long long)workspace_bytes);
@@ -210,18 +272,31 @@ extern "C" int llmserve_int8_linear_prefill(const float* x, const int8_t* qweigh
   const int64_t n4 = M * K / 4;
   const int64_t cgrid = (n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096;
   lsh::launch(x_to_bf16, dim3(static_cast<unsigned>(cgrid)), dim3(256), 0, st, false, x, xb, n4);
+  const int splits = prefill_splits(M, N, K);
   GemmArgs a{};
   a.xb = xb;
   a.q = qweight;
   a.scale = scale;
   a.y = y;
+  a.part = splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                 (M * K * 2 + 255) / 256 * 256)
+                      : nullptr;
   a.M = static_cast<int>(M);
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
   a.tiles_m = static_cast<int>((M + kBM - 1) / kBM);
   a.tiles_n = static_cast<int>((N + kBN - 1) / kBN);
-  const int64_t tiles = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
-  LSH_CHECK(tiles < (1LL << 31), "int8_linear_prefill: too many tiles");
-  lsh::launch(int8_gemm_bf16, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, st, true, a);
+  a.splits = splits;
+  a.k_split = static_cast<int>(K / splits);
+  const int64_t units = static_cast<int64_t>(a.tiles_m) * a.tiles_n * splits;
+  LSH_CHECK(units < (1LL << 31), "int8_linear_prefill: too many tiles");
+  lsh::launch(int8_gemm_bf16, dim3(static_cast<unsigned>(units)), dim3(kThreads), 0, st,
+              splits == 1, a);
+  if (splits > 1) {
+    const int64_t MN = M * N;
+    const int64_t rgrid = (MN + 255) / 256 < 8192 ? (MN + 255) / 256 : 8192;
+    lsh::launch(splitk_reduce, dim3(static_cast<unsigned>(rgrid)), dim3(256), 0, st, true,
+                static_cast<const float*>(a.part), scale, y, MN, static_cast<int>(N), splits);
+  }
   return lsh::launch_status("int8_linear_prefill");
 }

@@ -139,7 +139,7 @@ at::Tensor int8_linear_prefill(const at::Tensor& x, const at::Tensor& qweight,
               "int8_linear_prefill: scale must have one entry per output channel");
   const c10::DeviceGuard guard(x.device());
   auto y = at::empty({M, N}, x.options());
-  const int64_t ws_bytes = llmserve_int8_linear_prefill_workspace_bytes(M, K);
+  const int64_t ws_bytes = llmserve_int8_linear_prefill_workspace_bytes(M, N, K);
   at::Tensor ws;
   if (ws_bytes > 0) ws = at::empty({(ws_bytes + 15) / 16 * 4}, x.options());
   check_status(llmserve_int8_linear_prefill(

@@ -88,8 +88,8 @@ class Int8Linear(nn.Module):
             path = "gemv" if rows <= self.gemv_max_rows else "prefill"
         if path == "gemv" and rows > 64:
             path = "prefill"
-        if path == "prefill" and self.in_features % 32 != 0:
-            path = "dequant"  # the MFMA GEMM steps K by 32
+        if path == "prefill" and self.in_features % 64 != 0:
+            path = "dequant"  # the MFMA GEMM steps K by 64
         if path == "gemv":
             y = load_int8_gemv().int8_linear(x2, self.qweight, self.scale)
         elif path == "prefill":

@@ -70,7 +70,7 @@ def int8_linear_prefill(x, q, s):
     N = q.shape[0]
     y = torch.empty(M, N, dtype=torch.float32, device=x.device)
     L = capi()
-    nbytes = L.llmserve_int8_linear_prefill_workspace_bytes(M, K)
+    nbytes = L.llmserve_int8_linear_prefill_workspace_bytes(M, N, K)
     ws = torch.empty(max(nbytes, 16) // 4 + 4, dtype=torch.float32, device=x.device)
     check(L.llmserve_int8_linear_prefill(_p(x), _p(q), _p(s), _p(y), M, N, K, _p(ws), nbytes,
                                          _stream()))

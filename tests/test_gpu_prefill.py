@@ -48,8 +48,8 @@ def make(seed, M, N, K):
     return x, q, s
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 1, 32), (37, 100, 64), (256, 256, 32), (300, 520, 96),
-                                   (513, 257, 160), (64, 2048, 1024)])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 64), (37, 100, 64), (256, 256, 128), (300, 520, 192),
+                                   (513, 257, 320), (64, 2048, 1024), (200, 300, 4096)])
 def test_shapes(gpu, M, N, K):
     x, q, s = make(M * 7 + N, M, N, K)
     y = cu.int8_linear_prefill(cu.dev(x), cu.dev(q), cu.dev(s))
@@ -94,8 +94,8 @@ def test_module_prefill_and_dequant_agree(gpu):
 
 
 def test_rejects_bad_k(gpu):
-    x = torch.randn(4, 48, device="cuda")
-    q = torch.zeros(8, 48, dtype=torch.int8, device="cuda")
+    x = torch.randn(4, 96, device="cuda")
+    q = torch.zeros(8, 96, dtype=torch.int8, device="cuda")
     s = torch.ones(8, device="cuda")
-    with pytest.raises(RuntimeError, match="multiple of 32"):
+    with pytest.raises(RuntimeError, match="multiple of 64"):
         cu.int8_linear_prefill(x, q, s)
