@@ -80,6 +80,31 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Writes `v` from a DPP source into the rows of ROWMASK; lanes of the other rows get 0.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_rows(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               ROWMASK, 0xF, false));
+}
+
+constexpr int kRowBcast15 = 0x142;  // lane 15 of each row -> every lane of the next row
+constexpr int kRowBcast31 = 0x143;  // lane 31 -> every lane of rows 2 and 3
+
+// Sum over each aligned group of W consecutive lanes (W a power of two <= 64), valid in the
+// group's last lane (lane % W == W - 1). Rows of 16 lanes reduce with DPP butterflies; rows
+// are joined by DPP row broadcasts, so no step goes through the LDS crossbar.
+template <int W>
+__device__ __forceinline__ float group_total(float v) {
+  if constexpr (W <= 16) {
+    return group_sum<W>(v);
+  } else {
+    v = group_sum<16>(v);
+    v += dpp_rows<kRowBcast15, 0xA>(v);  // rows 1 and 3 hold the sums of lanes 0-31, 32-63
+    if constexpr (W == 64) v += dpp_rows<kRowBcast31, 0xC>(v);  // row 3 holds all 64
+    return v;
+  }
+}
+
 // Max over each aligned group of W consecutive lanes (W a power of two <= 16: DPP only).
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
