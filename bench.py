@@ -14,11 +14,11 @@ input channels x20; each layer shape's AWQ scale comes from the reference's grid
 `value` = algorithmic bytes per step (packed weights + group scales/zeros + inv_act_scale +
 x + y) x steps / wall time of the K timed steps. `roofline` is for the dominant kernel (the
 gate_up GEMV): its algorithmic bytes per launch over its average launch duration, measured
-here with HIP events that the kernel's own dispatch records (hipExtLaunchKernelGGL, via
-llmserve_time_next_call) on the stream it runs on — the interval a kernel-trace profiler
-reports. `cpu_baseline` times the reference's own CPU
-kernels (oracle/_ref, built from the reference sources) — or the oracle's C restatement where
-that build is absent — on the host cores, on the same quantized weights, for about 10 s.
+here with HIP events around graph replays of back-to-back launches (distinct weights) on the
+stream the kernel runs on — the per-dispatch interval a kernel-trace profiler reports.
+`cpu_baseline` times the reference's own CPU kernels (oracle/_ref, built from the reference
+sources) — or the oracle's C restatement where that build is absent — on the host cores, on
+the same quantized weights, for about 10 s.
 Extra fields report M = 4 / 16 steps and configs 1 (int8 GEMV), 3 (prefill int8 GEMM on the
 bf16 matrix cores, x conversion included) and 4 (int8-KV decode).
 """
@@ -136,20 +136,35 @@ def time_graphs(torch, graphs, steps: int, warmup: int) -> tuple[float, float]:
     return t1 - t0, e0.elapsed_time(e1) / 1e3
 
 
-def kernel_avg_us(torch, launch, n: int) -> float:
-    """Average kernel-execution time of `launch(i)` calls, each timed by HIP events that the
-    kernel's own dispatch records (llmserve_time_next_call), on the stream it runs on."""
-    from llmserve._native import KernelTimer
-
-    timer = KernelTimer(n)
-    for i in range(3):
-        launch(i)
+def kernel_avg_us(torch, launch, n: int, reps: int = 20) -> float:
+    """Average duration of one `launch(i)` call when the calls run back to back: n calls
+    (distinct inputs) are captured in a HIP graph, the graph is replayed `reps` times between
+    two HIP events recorded on the stream the kernels run on, and the interval is divided by
+    n * reps. This is the per-dispatch interval a kernel-trace profiler reports for the same
+    replays (profiles/bench_kernel_trace.md); no host launch overhead is inside it."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm the ops (allocator, LDS attributes) outside capture
+        for i in range(min(n, 3)):
+            launch(i)
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    for i in range(n):
-        timer.arm(i)
-        launch(i)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            launch(i)
+    for _ in range(2):
+        g.replay()
     torch.cuda.synchronize()
-    return sum(timer.elapsed_ms(i) for i in range(n)) / n * 1e3
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) * 1e3 / (n * reps)
 
 
 def read_traffic(kernel: str) -> dict | None:
@@ -390,11 +405,11 @@ def main() -> int:
     avg_us = kernel_avg_us(torch, gate_up, 224)
     kb = int4_bytes(N, K, 1)
     achieved = kb / avg_us / 1e3
-    traffic = read_traffic("gemv_fast int4 gate_up M=1")
+    traffic = read_traffic("gemv_lat int4 gate_up M=1")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None if traffic is None else int(traffic["fetch"] + traffic["write"]),
-                "kernel": "gemv_fast int4 (gate_up 1024->6144, M=1)",
+                "kernel": "gemv_lat int4 (gate_up 1024->6144, M=1)",
                 "bytes_per_launch": kb, "avg_launch_us": round(avg_us, 3)}
     log(f"[bench] roofline: {roofline}")
 

@@ -50,11 +50,11 @@ struct GemvArgs {
   float* y;            // [M, N]
   int N, K;
   int G;               // int4: quantization groups per row
-  int spg_log2;        // int4: log2 of slices (32 channels) per group, -1 if not a power of 2
-  // set by the host for the tiled kernel: activation rows, group size, slices per group,
-  // channels staged per chunk (a multiple of the segment), number of chunks, wavefronts
-  // per workgroup
-  int M, group, spg, KC, nchunk, wpb;
+  int16_t M;           // activation rows (<= 64)
+  int16_t spg_log2;    // int4: log2 of slices (32 channels) per group, -1 if not a power of 2
+  // set by the host for the tiled kernel: group size, channels staged per chunk (a multiple
+  // of the segment), number of chunks, wavefronts per workgroup
+  int group, KC, nchunk, wpb;
 };
 
 __device__ __forceinline__ u32x4 load16(const uint8_t* p) {
@@ -95,17 +95,21 @@ __device__ __forceinline__ int chunk_pos(int sl, int c) {
 }
 
 // Stages channels [c0, c0 + width) of x rows 0..MT-1 (rows >= Mt repeat row Mt-1; their
-// sums are never stored) and, when `inv` is given, multiplies them by inv (rounded as the
-// reference's separate x * inv_act_scale). LDS row m starts at float m * kcf; slice sl of a
-// row occupies floats [sl*CPL, (sl+1)*CPL) with its chunks placed by chunk_pos. The inv row
-// follows the MT x rows. Requires width <= kcf, width % 256 == 0 (a wavefront's 64 chunks
-// never straddle two rows) and 16-byte aligned x / inv rows. Ends with a barrier.
-template <int MT, int CPL>
-__device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x,
+// sums are never stored) with direct global->LDS loads and, when `inv` is given, multiplies
+// them by inv (rounded as the reference's separate x * inv_act_scale). LDS row m starts at
+// float m * kcf; slice sl of a row occupies floats [sl*CPL, (sl+1)*CPL) with its chunks
+// placed by chunk_pos. Row MT holds inv. With XSUM (int4), the channel sum of every slice of
+// every row, the (z - 8 s) term's factor, is written to xsum[m * kcf / CPL + sl], once per
+// workgroup instead of once per weight row. Requires width <= kcf, width % 256 == 0 (a
+// wavefront's 64 chunks never straddle two rows) and 16-byte aligned x / inv rows. Ends with
+// a barrier.
+template <int MT, int CPL, bool XSUM>
+__device__ __forceinline__ void stage_x(float* xs, float* xsum, const float* __restrict__ x,
                                         const float* __restrict__ inv, int Mt, int K, int c0,
                                         int width, int kcf, int wpb) {
   constexpr int CPC = CPL / 4;             // chunks per slice
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int bd = wpb * kWave;
   const int wchunks = width / 4;           // chunks staged per row
   const int bpr = wchunks / kWave;         // wavefront loads per row
   const int nblk = (MT + (inv ? 1 : 0)) * bpr;
@@ -122,19 +126,26 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x,
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0): the direct-to-LDS loads have landed
   __syncthreads();
-  if (inv) {
+  if (inv || XSUM) {
     const float* iv = xs + MT * kcf;
-    for (int i = threadIdx.x; i < MT * wchunks; i += wpb * kWave) {
-      const int m = i / wchunks, q = i - m * wchunks;
-      float* px = xs + m * kcf + q * 4;
-      float4 v = lds_ld4(px);
-      const float4 t = lds_ld4(iv + q * 4);
-      v.x = __fmul_rn(v.x, t.x);
-      v.y = __fmul_rn(v.y, t.y);
-      v.z = __fmul_rn(v.z, t.z);
-      v.w = __fmul_rn(v.w, t.w);
-      lds_st4(px, v);
-    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      for (int q = threadIdx.x; q < wchunks; q += bd) {  // whole wavefronts (wchunks % 64 == 0)
+        float* px = xs + m * kcf + q * 4;
+        float4 v = lds_ld4(px);
+        if (inv) {
+          const float4 t = lds_ld4(iv + q * 4);
+          v.x = __fmul_rn(v.x, t.x);
+          v.y = __fmul_rn(v.y, t.y);
+          v.z = __fmul_rn(v.z, t.z);
+          v.w = __fmul_rn(v.w, t.w);
+          lds_st4(px, v);
+        }
+        if constexpr (XSUM) {  // the CPC consecutive lanes of a slice
+          const float t = lsh::group_sum<CPC>((v.x + v.y) + (v.z + v.w));
+          if (q % CPC == 0) xsum[m * (kcf / CPL) + q / CPC] = t;
+        }
+      }
     __syncthreads();
   }
 }
@@ -201,7 +212,7 @@ __device__ __forceinline__ void stage_x_regs(float* xs, const float* __restrict_
 template <int MT, int LPR, int RPL, int S, bool INT4>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fast(GemvArgs a) {
   extern __shared__ float4 xs4[];
-  float* xs = reinterpret_cast<float*>(xs4);
+  float* xs = reinterpret_cast<float*>(xs4);  // [MT + 1][KC] x rows and the inv row
   constexpr int RPW = kWave / LPR;         // row slots per wavefront
   constexpr int CPL = INT4 ? 32 : 16;      // input channels per lane slice (16 bytes)
   constexpr int SEGK = LPR * CPL;          // input channels per row segment
@@ -256,8 +267,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fast(GemvArgs a) {
       stage_x_regs<MT, CPL>(xs, x, INT4 ? a.inv : nullptr, Mt, a.K, c0, min(a.KC, a.K - c0),
                             a.KC, wpb);
     else
-      stage_x<MT, CPL>(xs, x, INT4 ? a.inv : nullptr, Mt, a.K, c0, min(a.KC, a.K - c0), a.KC,
-                       wpb);
+      stage_x<MT, CPL, false>(xs, nullptr, x, INT4 ? a.inv : nullptr, Mt, a.K, c0,
+                              min(a.KC, a.K - c0), a.KC, wpb);
     const int nsc = min(spc, nseg - c * spc);
     for (int js = ks; js < nsc; js += S) {  // here j == c * spc + js
       const int nsn = min(spc, nseg - (c + 1) * spc);  // segments of the next chunk
@@ -363,7 +374,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fast(GemvArgs a) {
   }
 }
 
-// The decode (M <= 2) GEMV, straight-line: a lane issues the loads of all its NSEG segments
+// The decode (M <= 4) GEMV, straight-line: a lane issues the loads of all its NSEG segments
 // (and their group scales / zeros) at entry, the workgroup stages all of x (rows of K <= 4096
 // channels, at most four chunks per thread per row, times inv in registers), then each lane
 // finishes its rows. No loop carries a dependence on memory, so the kernel's time is one
@@ -399,8 +410,9 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
     if (u < rounds) {
       const int q = min(static_cast<int>(threadIdx.x) + u * BD, wchunks - 1);
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
-        xv4[m][u] = *reinterpret_cast<const float4*>(a.x + static_cast<int64_t>(m) * a.K + q * 4);
+      for (int m = 0; m < MT; ++m)  // rows past M repeat row M-1; their sums are not stored
+        xv4[m][u] = *reinterpret_cast<const float4*>(
+            a.x + static_cast<int64_t>(min(m, a.M - 1)) * a.K + q * 4);
       if (has_inv) iv4[u] = *reinterpret_cast<const float4*>(a.inv + q * 4);
     }
   // 2. weights of all segments and their group scales / zeros. Loads are unconditional,
@@ -511,7 +523,8 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       const float v = lsh::group_total<LPR>(acc[r][m]);
-      if (li == LPR - 1 && row < a.N) a.y[static_cast<int64_t>(m) * a.N + row] = INT4 ? v : v * sr;
+      if (li == LPR - 1 && row < a.N && m < a.M)
+        a.y[static_cast<int64_t>(m) * a.N + row] = INT4 ? v : v * sr;
     }
   }
 }
@@ -566,6 +579,9 @@ struct Config {
 
 constexpr int kLdsBudgetLarge = 160 * 1024;  // MT >= 8: one workgroup per CU if need be
 
+// LDS floats of the tiled kernel for a chunk of kc channels: MT x rows and the inv row.
+int lds_floats(bool int4, int MT, int kc) { return (MT + (int4 ? 1 : 0)) * kc; }
+
 int pick_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
 // Fast-path tiling for a (bits, MT, N, K, group) problem; lpr = 0 when it cannot tile.
@@ -582,7 +598,7 @@ Config choose(bool int4, int MT, int N, int K, int group, bool aligned) {
   int seg_bytes = 0;  // LDS bytes of one segment of staged x (+ the inv row)
   for (int lpr : {64, 32, 16}) {
     if (row_bytes % (lpr * 16) != 0) continue;
-    seg_bytes = (MT + (int4 ? 1 : 0)) * lpr * cpl * 4;
+    seg_bytes = lds_floats(int4, MT, lpr * cpl) * 4;
     if (seg_bytes > c.lds) continue;
     c.lpr = lpr;
     break;
@@ -612,10 +628,10 @@ int launch_fast(GemvArgs a, const Config& c, hipStream_t st) {
   a.wpb = c.wpb;
   if constexpr (INT4) {
     a.G = a.K / a.group;
-    a.spg = a.group / CPL;
-    a.spg_log2 = (a.spg & (a.spg - 1)) == 0 ? __builtin_ctz(a.spg) : -1;
+    const int spg = a.group / CPL;
+    a.spg_log2 = static_cast<int16_t>((spg & (spg - 1)) == 0 ? __builtin_ctz(spg) : -1);
   }
-  const size_t lds = static_cast<size_t>(MT + (a.inv ? 1 : 0)) * c.kc * sizeof(float);
+  const size_t lds = static_cast<size_t>(lds_floats(INT4, MT, c.kc)) * sizeof(float);
   if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit: raise it once per kernel
     static const hipError_t raised = hipFuncSetAttribute(
         reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -656,7 +672,7 @@ template <bool INT4>
 void run_generic(const GemvArgs& a, hipStream_t st) {
   for (int m0 = 0; m0 < a.M; m0 += kTileRows) {
     GemvArgs t = a;
-    t.M = a.M - m0 < kTileRows ? a.M - m0 : kTileRows;
+    t.M = static_cast<int16_t>(a.M - m0 < kTileRows ? a.M - m0 : kTileRows);
     t.x = a.x + static_cast<int64_t>(m0) * a.K;
     t.y = a.y + static_cast<int64_t>(m0) * a.N;
     const bool last = m0 + kTileRows >= a.M;
@@ -677,10 +693,12 @@ void launch_lat(const GemvArgs& a, int wpb, hipStream_t st) {
   const size_t lds = static_cast<size_t>(MT) * a.K * sizeof(float);
   const int rows_per_block = wpb * rpw;
   const dim3 grid((a.N + rows_per_block - 1) / rows_per_block);
-  if (wpb == 4)
+  constexpr int kSmallWpb = MT > 2 ? 4 : 2;  // MT > 2 always runs 4 wavefronts
+  if (MT > 2 || wpb == 4)
     lsh::launch(gemv_lat<MT, LPR, NSEG, 4, INT4>, grid, dim3(4 * kWave), lds, st, true, a);
   else
-    lsh::launch(gemv_lat<MT, LPR, NSEG, 2, INT4>, grid, dim3(2 * kWave), lds, st, true, a);
+    lsh::launch(gemv_lat<MT, LPR, NSEG, kSmallWpb, INT4>, grid, dim3(kSmallWpb * kWave), lds, st,
+                true, a);
 }
 
 template <int MT, int LPR, bool INT4>
@@ -699,7 +717,7 @@ void launch_lat_lpr(const GemvArgs& a, int nseg, int wpb, hipStream_t st) {
 // when it does not apply.
 template <bool INT4>
 bool try_lat(GemvArgs a, bool aligned, hipStream_t st) {
-  if (a.M > 2 || a.K > kLatMaxK || !aligned || (INT4 && a.group % 32 != 0)) return false;
+  if (a.M > 4 || a.K > kLatMaxK || !aligned || (INT4 && a.group % 32 != 0)) return false;
   const int cpl = INT4 ? 32 : 16;
   int lpr = 0;
   for (int l : {64, 32})
@@ -710,18 +728,21 @@ bool try_lat(GemvArgs a, bool aligned, hipStream_t st) {
   if (lpr == 0) return false;
   const int nseg = a.K / (lpr * cpl);
   const int waves = (a.N + kWave / lpr - 1) / (kWave / lpr);
-  const int wpb = waves >= 1024 ? 4 : 2;
+  const int wpb = waves >= 1024 || a.M > 2 ? 4 : 2;  // M > 2: x registers bound the stage
   if constexpr (INT4) {
     a.G = a.K / a.group;
     const int spg = a.group / cpl;
-    a.spg_log2 = (spg & (spg - 1)) == 0 ? __builtin_ctz(spg) : -1;
+    a.spg_log2 = static_cast<int16_t>((spg & (spg - 1)) == 0 ? __builtin_ctz(spg) : -1);
   }
   if (a.M == 1) {
     if (lpr == 64) launch_lat_lpr<1, 64, INT4>(a, nseg, wpb, st);
     else launch_lat_lpr<1, 32, INT4>(a, nseg, wpb, st);
-  } else {
+  } else if (a.M == 2) {
     if (lpr == 64) launch_lat_lpr<2, 64, INT4>(a, nseg, wpb, st);
     else launch_lat_lpr<2, 32, INT4>(a, nseg, wpb, st);
+  } else {
+    if (lpr == 64) launch_lat_lpr<4, 64, INT4>(a, nseg, wpb, st);
+    else launch_lat_lpr<4, 32, INT4>(a, nseg, wpb, st);
   }
   return true;
 }
@@ -762,7 +783,7 @@ extern "C" int llmserve_int8_linear(const float* x, const int8_t* q, const float
   a.w = reinterpret_cast<const uint8_t*>(q);
   a.s = scale;
   a.y = y;
-  a.M = static_cast<int>(M);
+  a.M = static_cast<int16_t>(M);
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
   a.group = 1;
@@ -788,7 +809,7 @@ extern "C" int llmserve_int4_linear(const float* x, const float* inv_act_scale,
   a.s = g_scale;
   a.z = g_zero;
   a.y = y;
-  a.M = static_cast<int>(M);
+  a.M = static_cast<int16_t>(M);
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
   a.group = static_cast<int>(group_size);
