@@ -113,6 +113,24 @@ int llmserve_int4_linear(const float* x, const float* inv_act_scale /* nullable 
                          void* stream);
 
 /*
+ * int4 weight-only linear for M > 16 activation rows on the bf16 matrix cores (replaces
+ * Int4Linear.forward's large-M branch, quant.py:141-142: x * inv_act_scale, then
+ * x @ dequantize().T), with the same group decomposition as int4_linear:
+ *   y[m,n] = sum_g s[n,g] * sum_{k in g} x'[m,k] q[n,k] + (z[n,g] - 8 s[n,g]) * sum_{k in g} x'[m,k]
+ * x' = x * inv_act_scale (fp32) is split into two bf16 terms (xh + xl = x' to 2^-18
+ * relative) by a pre-pass into `workspace`, so every matrix-core product is exact and the
+ * result is within a few 1e-6 (relative) of fp32 arithmetic. Requires K % 128 == 0,
+ * group_size % 128 == 0, N % 16 == 0, 16-byte aligned nibbles, 8-byte aligned x and
+ * inv_act_scale, and a 16-byte aligned workspace of
+ * llmserve_int4_linear_gemm_workspace_bytes(M, K) bytes.
+ */
+int64_t llmserve_int4_linear_gemm_workspace_bytes(int64_t M, int64_t K);
+int llmserve_int4_linear_gemm(const float* x, const float* inv_act_scale /* nullable [K] */,
+                              const uint8_t* nibbles, const float* g_scale, const float* g_zero,
+                              float* y, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                              void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Prefill-sized int8 weight-only linear on the bf16 matrix cores (replaces Int8Linear's
  * large-M path, quant.py:71-72 with dequantize quant.py:78-79: x @ (q * scale[:, None]).T):
  *   y[m, n] = scale[n] * sum_k bf16(x[m, k]) * q[n, k]      (fp32 accumulate)

@@ -48,7 +48,14 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
 ]
 
-HIP_SOURCES = ["errors.hip", "quant_pack.hip", "gemv.hip", "gemm_prefill.hip", "paged_decode.hip"]
+HIP_SOURCES = [
+    "errors.hip",
+    "quant_pack.hip",
+    "gemv.hip",
+    "gemm_prefill.hip",
+    "gemm_int4.hip",
+    "paged_decode.hip",
+]
 
 
 def _run(cmd: list[str], verbose: bool) -> None:

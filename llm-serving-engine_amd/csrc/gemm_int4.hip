@@ -1,0 +1,288 @@
+// Int4 (group-wise, AWQ-scaled) weight-only linear for more than 16 activation rows, on the
+// bf16 matrix cores. This is Int4Linear.forward's large-M branch (reference quant.py:141-142:
+// x * inv_act_scale, then x @ dequantize().T), computed with the same group decomposition as
+// the reference's kernel (int8_gemv.cpp:48-52):
+//   y[m, n] = sum_g s[n, g] * sum_{k in g} x'[m, k] q[n, k] + (z[n, g] - 8 s[n, g]) * sum_{k in g} x'[m, k]
+// so the matrix cores multiply only exact operands:
+//  * q in [0, 15] is exact in bf16;
+//  * x' = x * inv (fp32, rounded as the reference's separate multiply) is split by a pre-pass
+//    into bf16 xh = bf16(x') and xl = bf16(x' - xh): xh + xl equals x' to 2^-18 relative;
+//  * every product of two bf16 values is exact in fp32, and v_mfma_f32_16x16x32_bf16 adds
+//    them in fp32. The result is within a few 1e-6 (relative) of fp32 arithmetic.
+// The pre-pass also writes the channel sums of x' over every 128-channel block (the
+// (z - 8 s) factor). Requires K % 128 == 0 and group % 128 == 0 (the scale is constant over
+// a 128-channel block), N % 16 == 0.
+//
+// Work: a wavefront computes a 16 x 64 output slab (4 tiles of 16 x 16: 16 activation rows,
+// 64 output channels) over its share of the K blocks; the x fragments it loads for a block
+// feed all four channel tiles (x is re-read from L2 once per 64 output channels). ~150
+// registers, so 3 wavefronts per SIMD hide each other's load latency.
+// Lane l (fr = l % 16, fc = l / 16) of a k-step j (32 channels) of block b supplies the
+// channels 128 b + 32 fc + 8 j .. + 8, for
+// both operands: its 16-byte nibble load (row n0 + fr, bytes 64 b + 16 fc .. + 16) holds
+// exactly its 32 channels of the block, word j feeding step j; its x fragments are the 64
+// contiguous bytes of xh (and of xl) at the same channels. The mapping is a permutation of
+// the k index that both operands share, so the dot products are unchanged.
+// Blocks are software-pipelined: the loads of block b + 1 are in flight while block b runs.
+// When the output has few slabs, S = 2 or 4 wavefronts of a workgroup split the K blocks
+// of one slab and add their sums in LDS in a fixed order (deterministic).
+#include <algorithm>
+
+#include "common.h"
+
+namespace {
+
+using lsh::kWave;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlk = 128;              // channels per k block
+constexpr int kMT = 1;                 // 16-row tiles per wavefront
+constexpr int kNT = 4;                 // 16-channel tiles per wavefront
+constexpr int kRows = 16 * kMT;        // activation rows per wavefront
+constexpr int kCols = 16 * kNT;        // output channels per wavefront
+constexpr int kWaves = 4;              // wavefronts of the x-split workgroups
+constexpr int kSplitWaves = 4;         // largest K split
+
+// x' = x * inv -> xh, xl (bf16, round to nearest even) and xsum[b, m] = sum of x' over block
+// b. One wavefront per (m, b): lane i holds channels 2i, 2i + 1 of the block. xsum rows are
+// `mp` floats apart (mp >= M, a multiple of 4: a lane of the GEMM reads 4 consecutive rows).
+__global__ __launch_bounds__(kWaves * kWave) void x_split_kernel(
+    const float* __restrict__ x, const float* __restrict__ inv, __bf16* __restrict__ xh,
+    __bf16* __restrict__ xl, float* __restrict__ xsum, int M, int K, int mp) {
+  const int nb = K / kBlk;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+  if (item >= static_cast<int64_t>(M) * nb) return;  // whole wavefront
+  const int m = static_cast<int>(item / nb), b = static_cast<int>(item % nb);
+  const int lane = threadIdx.x % kWave;
+  const int64_t off = static_cast<int64_t>(m) * K + b * kBlk + 2 * lane;
+  float2 v = *reinterpret_cast<const float2*>(x + off);
+  if (inv) {
+    const float2 t = *reinterpret_cast<const float2*>(inv + b * kBlk + 2 * lane);
+    v.x = __fmul_rn(v.x, t.x);
+    v.y = __fmul_rn(v.y, t.y);
+  }
+  const __bf16 h0 = static_cast<__bf16>(v.x), h1 = static_cast<__bf16>(v.y);
+  const __bf16 l0 = static_cast<__bf16>(v.x - static_cast<float>(h0));
+  const __bf16 l1 = static_cast<__bf16>(v.y - static_cast<float>(h1));
+  const __bf16 hp[2] = {h0, h1}, lp[2] = {l0, l1};
+  *reinterpret_cast<uint32_t*>(xh + off) = *reinterpret_cast<const uint32_t*>(hp);
+  *reinterpret_cast<uint32_t*>(xl + off) = *reinterpret_cast<const uint32_t*>(lp);
+  const float s = lsh::wave_sum_from<1>(v.x + v.y);
+  if (lane == 0) xsum[static_cast<int64_t>(b) * mp + m] = s;
+}
+
+struct Int4GemmArgs {
+  const __bf16* xh;    // [M, K]
+  const __bf16* xl;    // [M, K]
+  const float* xsum;   // [K / 128, mp]
+  const uint8_t* w;    // nibbles [N, K / 2]
+  const float* s;      // g_scale [N, G]
+  const float* z;      // g_zero [N, G]
+  float* y;            // [M, N]
+  int M, N, K, G, bpg, mp;  // bpg: 128-channel blocks per quantization group
+};
+
+// 8 nibbles (channels 2e low, 2e + 1 high of byte e) -> 8 bf16, exact.
+__device__ __forceinline__ bf16x8 nibbles_bf16(uint32_t wd) {
+  const uint32_t lo = wd & 0x0f0f0f0fu, hi = (wd >> 4) & 0x0f0f0f0fu;
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[2 * e] = static_cast<__bf16>(static_cast<float>((lo >> (8 * e)) & 0xffu));
+    r[2 * e + 1] = static_cast<__bf16>(static_cast<float>((hi >> (8 * e)) & 0xffu));
+  }
+  return r;
+}
+
+// Workgroups of 4 wavefronts: R = 4 / S slabs side by side, S wavefronts splitting each
+// slab's K blocks.
+template <int S>
+__global__ __launch_bounds__(256) void int4_gemm_mfma(Int4GemmArgs a) {
+  extern __shared__ f32x4 red[];  // S > 1: [wave][kNT * kMT][64] sums of each wavefront
+  constexpr int R = 4 / S;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int ks = wave % S;                             // K split
+  const int slab = blockIdx.x * R + wave / S;          // 64-channel output slab
+  const int n0 = slab * kCols, m0 = blockIdx.y * kRows;
+  const int fr = lane % 16, fc = lane / 16;
+  const int nblk = a.K / kBlk;
+  const int per = (nblk + S - 1) / S;
+  const int kb0 = min(nblk, ks * per), kb1 = min(nblk, kb0 + per);
+
+  // Operand bases (rows clamped into the matrices; clamped rows are never stored).
+  int nrow[kNT];
+  const uint8_t* wp[kNT];
+#pragma unroll
+  for (int u = 0; u < kNT; ++u) {
+    nrow[u] = min(n0 + 16 * u + fr, a.N - 1);
+    wp[u] = a.w + static_cast<int64_t>(nrow[u]) * (a.K / 2) + 16 * fc;
+  }
+  const __bf16* hp[kMT];
+  const __bf16* lp[kMT];
+#pragma unroll
+  for (int t = 0; t < kMT; ++t) {
+    const int64_t m = min(m0 + 16 * t + fr, a.M - 1);
+    hp[t] = a.xh + m * a.K + 32 * fc;
+    lp[t] = a.xl + m * a.K + 32 * fc;
+  }
+
+  // one block's operands: nibbles of the 4 channel tiles (4 words each: steps 0..3), x
+  // fragments (4 steps x 16 bytes per tile and term), channel sums of the lane's 4 output rows
+  auto load = [&](int b, u32x4 (&w)[kNT], u32x4 (&xh)[kMT][4], u32x4 (&xl)[kMT][4],
+                  f32x4 (&xs)[kMT]) {
+#pragma unroll
+    for (int u = 0; u < kNT; ++u)
+      w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[u] + 64 * b));
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xh[t][j] = *reinterpret_cast<const u32x4*>(hp[t] + kBlk * b + 8 * j);
+        xl[t][j] = *reinterpret_cast<const u32x4*>(lp[t] + kBlk * b + 8 * j);
+      }
+      xs[t] = *reinterpret_cast<const f32x4*>(a.xsum + static_cast<int64_t>(b) * a.mp + m0 +
+                                              16 * t + 4 * fc);
+    }
+  };
+
+  f32x4 acc[kNT][kMT];
+#pragma unroll
+  for (int u = 0; u < kNT; ++u)
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 w[kNT], xh[kMT][4], xl[kMT][4];
+  f32x4 xs[kMT];
+  if (kb0 < kb1) load(kb0, w, xh, xl, xs);
+  for (int b = kb0; b < kb1; ++b) {
+    u32x4 wn[kNT], xhn[kMT][4], xln[kMT][4];
+    f32x4 xsn[kMT];
+    if (b + 1 < kb1) load(b + 1, wn, xhn, xln, xsn);
+    const int g = b / a.bpg;
+#pragma unroll
+    for (int u = 0; u < kNT; ++u) {
+      const float sc = a.s[static_cast<int64_t>(nrow[u]) * a.G + g];
+      const float zc = a.z[static_cast<int64_t>(nrow[u]) * a.G + g] - 8.f * sc;
+      bf16x8 bq[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bq[j] = nibbles_bf16(w[u][j]);
+#pragma unroll
+      for (int t = 0; t < kMT; ++t) {
+        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xh[t][j]), bq[j],
+                                                     d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xl[t][j]), bq[j],
+                                                     d, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[u][t][r] += sc * d[r] + zc * xs[t][r];
+      }
+    }
+    if (b + 1 < kb1) {
+#pragma unroll
+      for (int u = 0; u < kNT; ++u) w[u] = wn[u];
+#pragma unroll
+      for (int t = 0; t < kMT; ++t) {
+        xs[t] = xsn[t];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xh[t][j] = xhn[t][j];
+          xl[t][j] = xln[t][j];
+        }
+      }
+    }
+  }
+
+  if constexpr (S > 1) {
+#pragma unroll
+    for (int u = 0; u < kNT; ++u)
+#pragma unroll
+      for (int t = 0; t < kMT; ++t) red[(wave * kNT * kMT + u * kMT + t) * kWave + lane] = acc[u][t];
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int k = 1; k < S; ++k)
+#pragma unroll
+      for (int u = 0; u < kNT; ++u)
+#pragma unroll
+        for (int t = 0; t < kMT; ++t)
+          acc[u][t] += red[((wave + k) * kNT * kMT + u * kMT + t) * kWave + lane];
+  }
+  // lane holds rows 4 fc + r, column fr of each 16 x 16 tile
+#pragma unroll
+  for (int u = 0; u < kNT; ++u) {
+    const int n = n0 + 16 * u + fr;
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int t = 0; t < kMT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * t + 4 * fc + r;
+        if (m < a.M) a.y[static_cast<int64_t>(m) * a.N + n] = acc[u][t][r];
+      }
+  }
+}
+
+int64_t xsum_rows(int64_t M) { return (M + kRows - 1) / kRows * kRows; }
+
+}  // namespace
+
+extern "C" int64_t llmserve_int4_linear_gemm_workspace_bytes(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0) return 0;
+  return M * K * 4 + (K / kBlk) * xsum_rows(M) * 4;
+}
+
+extern "C" int llmserve_int4_linear_gemm(const float* x, const float* inv_act_scale,
+                                         const uint8_t* nibbles, const float* g_scale,
+                                         const float* g_zero, float* y, int64_t M, int64_t N,
+                                         int64_t K, int64_t group_size, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  LSH_CHECK(M >= 0 && N >= 0 && K >= 1 && group_size >= 2, "int4_linear_gemm: bad shape");
+  LSH_CHECK(K % kBlk == 0 && group_size % kBlk == 0 && K % group_size == 0,
+            "int4_linear_gemm: K and group_size must be multiples of 128 (K %% group == 0)");
+  LSH_CHECK(N % 16 == 0, "int4_linear_gemm: out_features must be a multiple of 16");
+  LSH_CHECK(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31) && M * K < (1LL << 40) &&
+                N * K < (1LL << 41),
+            "int4_linear_gemm: shape too large");
+  if (M == 0 || N == 0) return LLMSERVE_OK;
+  LSH_CHECK(x && nibbles && g_scale && g_zero && y, "int4_linear_gemm: null pointer");
+  LSH_CHECK(lsh::aligned16(nibbles) && (reinterpret_cast<uintptr_t>(x) & 7) == 0 &&
+                (inv_act_scale == nullptr || (reinterpret_cast<uintptr_t>(inv_act_scale) & 7) == 0),
+            "int4_linear_gemm: nibbles must be 16-byte and x / inv_act_scale 8-byte aligned");
+  const int64_t need = llmserve_int4_linear_gemm_workspace_bytes(M, K);
+  LSH_CHECK(workspace != nullptr && workspace_bytes >= need && lsh::aligned16(workspace),
+            "int4_linear_gemm: a 16-byte aligned workspace of %lld bytes is needed (%lld given)",
+            (long long)need, (long long)workspace_bytes);
+  hipStream_t st = lsh::as_stream(stream);
+  const int nb = static_cast<int>(K / kBlk);
+  const int mp = static_cast<int>(xsum_rows(M));
+  __bf16* xh = static_cast<__bf16*>(workspace);
+  __bf16* xl = xh + M * K;
+  float* xsum = reinterpret_cast<float*>(xl + M * K);
+  const int64_t items = M * nb;
+  lsh::launch(x_split_kernel, dim3(static_cast<unsigned>((items + kWaves - 1) / kWaves)),
+              dim3(kWaves * kWave), 0, st, false, x, inv_act_scale, xh, xl, xsum,
+              static_cast<int>(M), static_cast<int>(K), mp);
+
+  Int4GemmArgs a{xh, xl, xsum, nibbles, g_scale, g_zero, y, static_cast<int>(M),
+                 static_cast<int>(N), static_cast<int>(K), static_cast<int>(K / group_size),
+                 static_cast<int>(group_size / kBlk), mp};
+  // K split: the smallest S (1, 2, 4) that gives >= 768 wavefronts, with >= 2 blocks each
+  const int64_t slabs = (N + kCols - 1) / kCols, mtiles = (M + kRows - 1) / kRows;
+  int S = 1;
+  while (S < kSplitWaves && slabs * mtiles * S < 768 && nb >= 2 * (2 * S)) S *= 2;
+  const int R = 4 / S;  // slabs per workgroup
+  const dim3 grid(static_cast<unsigned>((slabs + R - 1) / R), static_cast<unsigned>(mtiles));
+  const dim3 block(static_cast<unsigned>(R * S * kWave));
+  const size_t lds = S > 1 ? static_cast<size_t>(R * S) * kNT * kMT * kWave * sizeof(f32x4) : 0;
+  switch (S) {
+    case 4: lsh::launch(int4_gemm_mfma<4>, grid, block, lds, st, true, a); break;
+    case 2: lsh::launch(int4_gemm_mfma<2>, grid, block, lds, st, true, a); break;
+    default: lsh::launch(int4_gemm_mfma<1>, grid, block, lds, st, true, a); break;
+  }
+  return lsh::launch_status("int4_linear_gemm");
+}

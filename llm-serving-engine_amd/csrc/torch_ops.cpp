@@ -179,6 +179,39 @@ at::Tensor int4_linear(const at::Tensor& x, const at::Tensor& nibbles, const at:
   return y;
 }
 
+at::Tensor int4_linear_gemm(const at::Tensor& x, const at::Tensor& nibbles, const at::Tensor& scale,
+                            const at::Tensor& zero, int64_t group_size,
+                            const std::optional<at::Tensor>& inv_act_scale) {
+  TORCH_CHECK(x.scalar_type() == at::kFloat && nibbles.scalar_type() == at::kByte, "int4: dtypes");
+  TORCH_CHECK(scale.scalar_type() == at::kFloat && zero.scalar_type() == at::kFloat, "int4: dtypes");
+  TORCH_CHECK(x.is_contiguous() && nibbles.is_contiguous() && scale.is_contiguous() &&
+                  zero.is_contiguous(),
+              "int4: contiguous inputs");
+  TORCH_CHECK(x.dim() == 2 && nibbles.dim() == 2, "int4: 2-D x and nibbles");
+  check_device(x, {&nibbles, &scale, &zero}, "int4_linear_gemm");
+  const int64_t M = x.size(0), K = x.size(1), N = nibbles.size(0);
+  TORCH_CHECK(group_size > 0, "int4: shapes");
+  const int64_t G = K / group_size;
+  TORCH_CHECK(nibbles.size(1) * 2 == K && G * group_size == K, "int4: shapes");
+  TORCH_CHECK(scale.numel() == N * G && zero.numel() == N * G, "int4: scale/zero must be [N, G]");
+  if (inv_act_scale.has_value()) {
+    check_device(x, {&*inv_act_scale}, "int4_linear_gemm");
+    TORCH_CHECK(inv_act_scale->scalar_type() == at::kFloat && inv_act_scale->is_contiguous() &&
+                    inv_act_scale->numel() == K,
+                "int4_linear_gemm: inv_act_scale must be a contiguous float32 [K] tensor");
+  }
+  const c10::DeviceGuard guard(x.device());
+  auto y = at::empty({M, N}, x.options());
+  const int64_t ws_bytes = llmserve_int4_linear_gemm_workspace_bytes(M, K);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({(ws_bytes + 15) / 16 * 4}, x.options());
+  check_status(llmserve_int4_linear_gemm(
+      x.data_ptr<float>(), opt_ptr<float>(inv_act_scale), nibbles.data_ptr<uint8_t>(),
+      scale.data_ptr<float>(), zero.data_ptr<float>(), y.data_ptr<float>(), M, N, K, group_size,
+      ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(x)));
+  return y;
+}
+
 // ---- int8-KV paged decode -------------------------------------------------------------------
 
 at::Tensor paged_attention_decode_int8(const at::Tensor& q, const at::Tensor& k_cache,
@@ -245,6 +278,8 @@ TORCH_LIBRARY(llmserve_hip, m) {
   m.def("int8_linear_prefill(Tensor x, Tensor qweight, Tensor scale) -> Tensor");
   m.def("int4_linear(Tensor x, Tensor nibbles, Tensor scale, Tensor zero, int group_size,"
         " Tensor? inv_act_scale=None) -> Tensor");
+  m.def("int4_linear_gemm(Tensor x, Tensor nibbles, Tensor scale, Tensor zero, int group_size,"
+        " Tensor? inv_act_scale=None) -> Tensor");
   m.def("paged_attention_decode_int8(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale,"
         " Tensor v_scale, Tensor block_tables, Tensor context_lens, int block_size, float scale,"
         " int partition_size=0, Tensor? q_mult=None) -> Tensor");
@@ -256,6 +291,7 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("kv_quantize_write", &kv_quantize_write);
   m.impl("int8_linear", &int8_linear);
   m.impl("int8_linear_prefill", &int8_linear_prefill);
+  m.impl("int4_linear_gemm", &int4_linear_gemm);
   m.impl("int4_linear", &int4_linear);
   m.impl("paged_attention_decode_int8", &paged_attention_decode_int8);
 }

@@ -51,6 +51,8 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
     "llmserve_kv_quantize_write": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "llmserve_int8_linear": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "llmserve_int4_linear": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "llmserve_int4_linear_gemm_workspace_bytes": (_I64, [_I64, _I64]),
+    "llmserve_int4_linear_gemm": (_I32, [_P] * 6 + [_I64] * 4 + [_P, _I64, _P]),
     "llmserve_int8_linear_prefill_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "llmserve_int8_linear_prefill": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P]),
     "llmserve_paged_attention_workspace_bytes": (_I64, [_I64] * 7),

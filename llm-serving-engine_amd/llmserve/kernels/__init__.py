@@ -9,7 +9,8 @@ objects expose the reference's function names and signatures:
   ``int4_linear(x, nibbles, scale, zero, group_size, inv_act_scale=None)``
   (int8_gemv.cpp:109-112; ``inv_act_scale`` fuses Int4Linear's AWQ pre-scale), and
   ``int8_linear_prefill(x, qweight, scale)``: Int8Linear's large-M path on the bf16 matrix
-  cores (quant.py:71-72);
+  cores (quant.py:71-72), and ``int4_linear_gemm(x, nibbles, scale, zero, group_size,
+  inv_act_scale=None)``: Int4Linear's large-M path (quant.py:141-142) on the matrix cores;
 * ``load_paged_attention()``: ``paged_attention_decode_int8(q, k_cache, v_cache, k_scale,
   v_scale, block_tables, context_lens, block_size, scale, partition_size=0, q_mult=None)``
   (paged_attention.cpp:386-399; ``q_mult`` fuses the key-smoothing multiply of q).
@@ -33,7 +34,8 @@ def load_int8_gemv() -> SimpleNamespace:
     """Weight-only int8 / int4 small-batch matmuls (HIP, gfx950)."""
     o = ops()
     return SimpleNamespace(int8_linear=o.int8_linear, int4_linear=o.int4_linear,
-                           int8_linear_prefill=o.int8_linear_prefill)
+                           int8_linear_prefill=o.int8_linear_prefill,
+                           int4_linear_gemm=o.int4_linear_gemm)
 
 
 @functools.cache

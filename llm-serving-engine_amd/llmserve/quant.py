@@ -136,8 +136,12 @@ class Int4Linear(nn.Module):
     same fp32 ``x * inv_act_scale`` the reference computes.
     """
 
-    max_fused_rows = 16  # above this: dequantize + GEMM (reference quant.py:123)
-    kernel = "auto"  # "auto" (HIP GEMV for small batches) or "aten" (dequantize + GEMM)
+    max_fused_rows = 16  # above this: the large-M path (reference quant.py:123)
+    # "auto": the HIP GEMV up to max_fused_rows rows, above that the HIP matrix-core GEMM
+    # (int4_linear_gemm) where its shape rules hold (K and group multiples of 128, out
+    # multiple of 16), else dequantize + GEMM; "gemv" / "gemm" force one HIP kernel;
+    # "aten": dequantize + GEMM (the reference's large-M algorithm) for every batch
+    kernel = "auto"
 
     def __init__(
         self,
@@ -176,24 +180,29 @@ class Int4Linear(nn.Module):
         w = (q - 8) * self.g_scale[..., None] + self.g_zero[..., None]
         return w.reshape(self.out_features, self.in_features)
 
+    def gemm_ok(self) -> bool:
+        """Shapes the matrix-core large-M kernel takes."""
+        return (self.in_features % 128 == 0 and self.group_size % 128 == 0
+                and self.out_features % 16 == 0)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        if x2.shape[0] > self.max_fused_rows or self.kernel == "aten":
+        rows = x2.shape[0]
+        if self.kernel == "auto":
+            path = "gemv" if rows <= self.max_fused_rows else ("gemm" if self.gemm_ok() else "aten")
+        elif self.kernel in ("gemv", "gemm", "aten"):
+            path = self.kernel
+        else:
+            raise ValueError(f"unknown Int4Linear kernel {self.kernel!r}")
+        if path == "aten":
             if self.inv_act_scale is not None:
                 x2 = x2 * self.inv_act_scale
             y = x2 @ self.dequantize().t()
-        elif self.kernel == "auto":
-            y = load_int8_gemv().int4_linear(
-                x2.contiguous(),
-                self.nibbles,
-                self.g_scale,
-                self.g_zero,
-                self.group_size,
-                self.inv_act_scale,
-            )
         else:
-            raise ValueError(f"unknown Int4Linear kernel {self.kernel!r}")
+            fn = load_int8_gemv().int4_linear if path == "gemv" else load_int8_gemv().int4_linear_gemm
+            y = fn(x2.contiguous(), self.nibbles, self.g_scale, self.g_zero, self.group_size,
+                   self.inv_act_scale)
         y = y.reshape(*shape[:-1], self.out_features)
         return y if self.bias is None else y + self.bias
 

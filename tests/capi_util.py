@@ -65,6 +65,18 @@ def int4_linear(x, nib, gs, gz, group, inv=None):
     return y
 
 
+def int4_linear_gemm(x, nib, gs, gz, group, inv=None):
+    M, K = x.shape
+    N = nib.shape[0]
+    y = torch.empty(M, N, dtype=torch.float32, device=x.device)
+    L = capi()
+    nbytes = L.llmserve_int4_linear_gemm_workspace_bytes(M, K)
+    ws = torch.empty(max(nbytes, 16) // 4 + 4, dtype=torch.float32, device=x.device)
+    check(L.llmserve_int4_linear_gemm(_p(x), _p(inv), _p(nib), _p(gs), _p(gz), _p(y), M, N, K,
+                                      group, _p(ws), nbytes, _stream()))
+    return y
+
+
 def int8_linear_prefill(x, q, s):
     M, K = x.shape
     N = q.shape[0]
