@@ -146,6 +146,70 @@ int llmserve_int8_linear_prefill(const float* x, const int8_t* qweight, const fl
                                  float* y, int64_t M, int64_t N, int64_t K, void* workspace,
                                  int64_t workspace_bytes, void* stream);
 
+/* ---- decoder-layer elementwise ops and decode-step glue ---------------------------------- */
+
+/*
+ * out = w * (x * inv), inv = 1 / sqrt(mean_h(x^2) + eps), per row of H (replaces rmsnorm,
+ * fused_ops.cpp:23-30 and :39-56). x, out fp32 [T, H]; w fp32 [H].
+ */
+int llmserve_rmsnorm(const float* x, const float* w, float* out, int64_t T, int64_t H, float eps,
+                     void* stream);
+
+/*
+ * x += r (in place), then out = rmsnorm(x) * w (replaces add_rmsnorm_, fused_ops.cpp:58-81).
+ */
+int llmserve_add_rmsnorm(float* x, const float* r, const float* w, float* out, int64_t T,
+                         int64_t H, float eps, void* stream);
+
+/*
+ * out[t, i] = gate / (1 + exp(-gate)) * up for a fused gate|up row (replaces silu_mul,
+ * fused_ops.cpp:83-99). gate_up fp32 [T, 2I] -> out fp32 [T, I].
+ */
+int llmserve_silu_mul(const float* gate_up, float* out, int64_t T, int64_t I, void* stream);
+
+/*
+ * In place on the fused qkv rows (replaces rope_qk_, fused_ops.cpp:101-127): for each of the
+ * first n_q (q) and next n_k (k) heads of a row, optional per-head RMSNorm with q_w / k_w
+ * (Qwen3), then rotate-half RoPE with cos/sin [T, D]:
+ *   out[d] = x[d] c[d] - x[d + D/2] s[d] (d < D/2),  x[d] c[d] + x[d - D/2] s[d] (d >= D/2).
+ * qkv fp32 rows of row_stride floats; head_dim D in {16, 32, 64, 128, 256}.
+ */
+int llmserve_rope_qk(float* qkv, const float* cos, const float* sin, int64_t T,
+                     int64_t row_stride, int64_t n_q, int64_t n_k, int64_t D,
+                     const float* q_w /* nullable */, const float* k_w /* nullable */, float eps,
+                     void* stream);
+
+/*
+ * Decode step glue after the qkv projection (one token per sequence; no single reference
+ * function: it is rope_qk_ followed by paged_attention's cache write, attention.py:221-228
+ * with QuantizedKV.write :159-162 and the key smoothing :243-245). For token t at position
+ * p = context_lens[t] - 1 (context_lens counts the new token):
+ *   q heads: norm(q_w) + RoPE with row p of cos_table/sin_table [max_pos, D] -> q_out [T, n_q, D]
+ *   k heads: norm(k_w) + RoPE, / k_smooth[h], int8 quantized into k_cache/k_scale at slot
+ *            block_tables[t, p / block_size] * block_size + p % block_size
+ *   v heads: int8 quantized into v_cache/v_scale at the same slot.
+ * The quantizer is llmserve_kv_quantize_write's (bit-identical). Tokens whose position or
+ * block is outside the tables or the cache are skipped.
+ */
+int llmserve_decode_qkv_kv(const float* qkv, int64_t row_stride, const float* cos_table,
+                           const float* sin_table, int64_t max_pos, const int64_t* context_lens,
+                           const int64_t* block_tables, int64_t max_blocks, int64_t block_size,
+                           const float* q_w, const float* k_w, float eps,
+                           const float* k_smooth /* nullable [n_k, D] */, float* q_out,
+                           int8_t* k_cache, int8_t* v_cache, float* k_scale, float* v_scale,
+                           int64_t num_slots, int64_t T, int64_t n_q, int64_t n_k, int64_t D,
+                           void* stream);
+
+/*
+ * Greedy decoding (sampling.py:151-170 at temperature 0): next_ids[t] = argmax over logits
+ * [T, V] of row t (the first index among equal maxima), then context_lens[t] += 1.
+ * `workspace` holds llmserve_argmax_advance_workspace_bytes(T) bytes (16-byte aligned).
+ */
+int64_t llmserve_argmax_advance_workspace_bytes(int64_t T);
+int llmserve_argmax_advance(const float* logits, int64_t T, int64_t V, int64_t* next_ids,
+                            int64_t* context_lens, void* workspace, int64_t workspace_bytes,
+                            void* stream);
+
 /* ---- int8-KV paged decode attention ------------------------------------------------------ */
 
 /*

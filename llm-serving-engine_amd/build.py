@@ -54,6 +54,7 @@ HIP_SOURCES = [
     "gemv.hip",
     "gemm_prefill.hip",
     "gemm_int4.hip",
+    "fused_ops.hip",
     "paged_decode.hip",
 ]
 

@@ -1,0 +1,404 @@
+// Fused elementwise kernels of the decoder layer (the reference's fused_ops.cpp:39-125:
+// rmsnorm, add_rmsnorm_, silu_mul, rope_qk_) and the decode-step glue around them:
+//  * the post-qkv decode kernel: per-head RMSNorm of q and k (Qwen3), rotate-half RoPE at each
+//    sequence's position, q written contiguous for the attention kernel, k and v quantized
+//    straight into the int8 KV cache (QuantizedKV.write, attention.py:153-162, with the
+//    key-smoothing division) at the slot of the new token: one launch where the reference runs
+//    rope_qk_, two index_copy_ writes and a copy of q;
+//  * greedy next-token selection (argmax over the logits row, sampling.py:151-170 at
+//    temperature 0) that also advances each sequence's context length by the new token.
+// The reference's sum-of-squares loops are OpenMP simd reductions (any order); here they are
+// trees over the wavefront / workgroup in a fixed order.
+#include "common.h"
+#include "kv_quant.h"
+
+namespace {
+
+using lsh::kWave;
+constexpr int kRowThreads = 256;
+
+// Sum over the 256 threads of the workgroup, in a fixed order; every thread gets it.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = lsh::wave_sum_from<1>(v);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+
+// out = w * (x * inv), inv = 1 / sqrt(mean(x^2) + eps) (fused_ops.cpp:23-30); ADD first does
+// x += r in place (add_rmsnorm_, fused_ops.cpp:60-81). One workgroup per row.
+template <bool ADD>
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(float* __restrict__ x,
+                                                              const float* __restrict__ r,
+                                                              const float* __restrict__ w,
+                                                              float* __restrict__ out, int64_t H,
+                                                              float eps) {
+  __shared__ float red[kRowThreads / kWave];
+  const int64_t t = blockIdx.x;
+  float* xr = x + t * H;
+  float* orow = out + t * H;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < H; i += kRowThreads) {
+    float v = xr[i];
+    if (ADD) {
+      v += r[t * H + i];
+      xr[i] = v;
+    }
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.f / sqrtf(ss / static_cast<float>(H) + eps);
+  for (int64_t i = threadIdx.x; i < H; i += kRowThreads) orow[i] = w[i] * (xr[i] * inv);
+}
+
+// out[t, i] = silu(gate) * up = gate / (1 + exp(-gate)) * up for a fused [T, 2I] gate|up row
+// (fused_ops.cpp:83-99).
+__global__ __launch_bounds__(kRowThreads) void silu_mul_kernel(const float* __restrict__ gu,
+                                                               float* __restrict__ out, int64_t T,
+                                                               int64_t I) {
+  const int64_t n = T * I;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kRowThreads;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x; e < n; e += stride) {
+    const int64_t t = e / I, i = e - t * I;
+    const float g = gu[t * 2 * I + i], u = gu[t * 2 * I + I + i];
+    out[e] = g / (1.f + expf(-g)) * u;
+  }
+}
+
+struct RopeArgs {
+  float* qkv;                 // [T, row_stride] floats: n_q q heads, n_k k heads, n_k v heads
+  int64_t row_stride;
+  const float* cos;           // rows of D: per token (rope_qk_) or per position (decode)
+  const float* sin;
+  const float* q_w;           // [D] per-head RMSNorm weights, or null
+  const float* k_w;
+  float eps;
+  int T, n_q, n_k, D;
+  // decode: position of token t = context_lens[t] - 1 (its cos/sin row and cache slot)
+  const int64_t* ctx;
+  const int64_t* bt;          // [T, max_blocks]
+  int64_t max_blocks, bs, num_slots, max_pos;
+  const float* smooth;        // [n_k, D] key smoothing, or null
+  float* q_out;               // [T, n_q, D]
+  int8_t* kc;                 // [num_slots, n_k, D]
+  int8_t* vc;
+  float* ks;                  // [num_slots, n_k]
+  float* vs;
+};
+
+// One wavefront per (token, head). Lane l holds elements d = l + 64 i (i < N = max(1, D / 64));
+// when D < 64 the lanes >= D hold nothing.
+// Per-head RMSNorm (norm_row with the head's weight), then out[d] = x[d] c[d] - x[d + D/2]
+// s[d] for d < D/2 and x[d] c[d] + x[d - D/2] s[d] above (rotate_half, fused_ops.cpp:121-124).
+template <int N>
+__device__ __forceinline__ void norm_rope(float (&v)[N], const float* w, const float* c,
+                                          const float* s, int D, float eps) {
+  const int lane = threadIdx.x % kWave;
+  if (w) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (lane + i * kWave < D) ss += v[i] * v[i];
+    ss = lsh::wave_sum_from<1>(ss);
+    const float inv = 1.f / sqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int d = lane + i * kWave;
+      if (d < D) v[i] = w[d] * (v[i] * inv);
+    }
+  }
+  const int half = D / 2;
+  float p[N];  // partner element d +- D/2
+  if (half % kWave == 0) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = v[(i + (half / kWave)) % N];
+  } else {  // D = 64: the partner is 32 lanes away; D = 32 / 16: within the first lanes
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = __shfl_xor(v[i], half, kWave);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int d = lane + i * kWave;
+    if (d < D) v[i] = d < half ? v[i] * c[d] - p[i] * s[d] : v[i] * c[d] + p[i] * s[d];
+  }
+}
+
+template <int N, bool DECODE>
+__global__ __launch_bounds__(kRowThreads) void rope_kernel(RopeArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int heads = DECODE ? a.n_q + 2 * a.n_k : a.n_q + a.n_k;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * (kRowThreads / kWave) + threadIdx.x / kWave;
+  if (gid >= static_cast<int64_t>(a.T) * heads) return;  // whole wavefront
+  const int t = static_cast<int>(gid / heads), hh = static_cast<int>(gid % heads);
+  float* row = a.qkv + t * a.row_stride + static_cast<int64_t>(hh) * a.D;
+  float v[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int d = lane + i * kWave;
+    v[i] = d < a.D ? row[d] : 0.f;
+  }
+  int64_t cs_row = t, slot = -1;
+  if constexpr (DECODE) {
+    const int64_t pos = a.ctx[t] - 1;
+    if (pos < 0 || pos >= a.max_pos || pos / a.bs >= a.max_blocks) return;
+    cs_row = pos;
+    const int64_t blk = a.bt[t * a.max_blocks + pos / a.bs];
+    slot = blk * a.bs + pos % a.bs;
+    if (blk < 0 || slot >= a.num_slots) slot = -1;
+  }
+  const bool is_q = hh < a.n_q, is_k = !is_q && hh < a.n_q + a.n_k;
+  if (is_q || is_k)
+    norm_rope(v, is_q ? a.q_w : a.k_w, a.cos + cs_row * a.D, a.sin + cs_row * a.D, a.D, a.eps);
+  if constexpr (!DECODE) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int d = lane + i * kWave;
+      if (d < a.D) row[d] = v[i];
+    }
+  } else {
+    if (is_q) {
+      float* o = a.q_out + (static_cast<int64_t>(t) * a.n_q + hh) * a.D;
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int d = lane + i * kWave;
+        if (d < a.D) o[d] = v[i];
+      }
+    } else if (slot >= 0) {
+      const int h = is_k ? hh - a.n_q : hh - a.n_q - a.n_k;
+      const int64_t at = slot * a.n_k + h;
+      if (is_k)
+        lsh::kv_quant_row(v, a.smooth ? a.smooth + static_cast<int64_t>(h) * a.D : nullptr, a.D,
+                          a.kc + at * a.D, a.ks + at);
+      else
+        lsh::kv_quant_row(v, nullptr, a.D, a.vc + at * a.D, a.vs + at);
+    }
+  }
+}
+
+// Greedy selection in two launches: argmax_parts splits each logits row into kArgParts
+// ranges (kArgParts workgroups per row, so the 64-row batch covers the GPU) and writes each
+// range's (max, first index of the max); argmax_finish picks the best range per row (larger
+// value, then smaller index: the first index among equal maxima), writes next_ids[t] and
+// advances context_lens[t] by the new token. NaN orders above every number, as in
+// torch.argmax (the reference's greedy path), so the first NaN of a row is selected.
+
+constexpr int kArgParts = 32;
+
+// x ranks above y: NaN above every number, else the larger value
+__device__ __forceinline__ bool arg_above(float x, float y) {
+  return x > y || (__builtin_isnan(x) && !__builtin_isnan(y));
+}
+
+// the higher-ranked value wins, then the smaller index
+__device__ __forceinline__ void arg_better(float& best, int64_t& idx, float ob, int64_t oi) {
+  const bool same = ob == best || (__builtin_isnan(ob) && __builtin_isnan(best));
+  if (arg_above(ob, best) || (same && oi < idx)) {
+    best = ob;
+    idx = oi;
+  }
+}
+
+__global__ __launch_bounds__(kRowThreads) void argmax_parts_kernel(const float* __restrict__ logits,
+                                                                   int64_t V,
+                                                                   float* __restrict__ part_v,
+                                                                   int64_t* __restrict__ part_i) {
+  __shared__ float bv[kRowThreads / kWave];
+  __shared__ int64_t bi[kRowThreads / kWave];
+  const int64_t t = blockIdx.x / kArgParts;
+  const int part = blockIdx.x % kArgParts;
+  const int64_t per = (V + kArgParts - 1) / kArgParts;
+  const int64_t lo = part * per, hi = lo + per < V ? lo + per : V;
+  const float* row = logits + t * V;
+  float best = -__builtin_inff();
+  int64_t idx = V;  // none
+  for (int64_t i = lo + threadIdx.x; i < hi; i += kRowThreads) {
+    const float x = row[i];
+    if (arg_above(x, best)) {  // strictly above: the first index of equal values stays
+      best = x;
+      idx = i;
+    }
+  }
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) arg_better(best, idx, __shfl_xor(best, d, kWave), __shfl_xor(idx, d, kWave));
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (lane == 0) {
+    bv[wave] = best;
+    bi[wave] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < kRowThreads / kWave; ++k) arg_better(best, idx, bv[k], bi[k]);
+    part_v[blockIdx.x] = best;
+    part_i[blockIdx.x] = idx;
+  }
+}
+
+__global__ __launch_bounds__(kWave) void argmax_finish_kernel(const float* __restrict__ part_v,
+                                                              const int64_t* __restrict__ part_i,
+                                                              int64_t V, int64_t* __restrict__ next_ids,
+                                                              int64_t* __restrict__ ctx) {
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x;
+  float best = -__builtin_inff();
+  int64_t idx = V;
+  if (lane < kArgParts) {
+    best = part_v[t * kArgParts + lane];
+    idx = part_i[t * kArgParts + lane];
+  }
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) arg_better(best, idx, __shfl_xor(best, d, kWave), __shfl_xor(idx, d, kWave));
+  if (lane == 0) {
+    next_ids[t] = idx < V ? idx : 0;
+    ctx[t] += 1;
+  }
+}
+
+int rope_slots(int64_t D) { return D <= kWave ? 1 : static_cast<int>((D + kWave - 1) / kWave); }
+
+template <bool DECODE>
+int launch_rope(const RopeArgs& a, hipStream_t st) {
+  const int heads = DECODE ? a.n_q + 2 * a.n_k : a.n_q + a.n_k;
+  const int64_t waves = static_cast<int64_t>(a.T) * heads;
+  const dim3 grid(static_cast<unsigned>((waves + 3) / 4)), block(kRowThreads);
+  switch (rope_slots(a.D)) {
+    case 1: lsh::launch(rope_kernel<1, DECODE>, grid, block, 0, st, true, a); break;
+    case 2: lsh::launch(rope_kernel<2, DECODE>, grid, block, 0, st, true, a); break;
+    default: lsh::launch(rope_kernel<4, DECODE>, grid, block, 0, st, true, a); break;
+  }
+  return LLMSERVE_OK;
+}
+
+bool head_dim_ok(int64_t D) { return D == 16 || D == 32 || D == 64 || D == 128 || D == 256; }
+
+}  // namespace
+
+extern "C" int llmserve_rmsnorm(const float* x, const float* w, float* out, int64_t T, int64_t H,
+                                float eps, void* stream) {
+  LSH_CHECK(T >= 0 && H >= 1 && T < (1LL << 31), "rmsnorm: bad shape T=%lld H=%lld", (long long)T,
+            (long long)H);
+  if (T == 0) return LLMSERVE_OK;
+  LSH_CHECK(x && w && out, "rmsnorm: null pointer");
+  lsh::launch(rmsnorm_kernel<false>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
+              lsh::as_stream(stream), true, const_cast<float*>(x), nullptr, w, out, H, eps);
+  return lsh::launch_status("rmsnorm");
+}
+
+extern "C" int llmserve_add_rmsnorm(float* x, const float* r, const float* w, float* out,
+                                    int64_t T, int64_t H, float eps, void* stream) {
+  LSH_CHECK(T >= 0 && H >= 1 && T < (1LL << 31), "add_rmsnorm: bad shape T=%lld H=%lld",
+            (long long)T, (long long)H);
+  if (T == 0) return LLMSERVE_OK;
+  LSH_CHECK(x && r && w && out, "add_rmsnorm: null pointer");
+  lsh::launch(rmsnorm_kernel<true>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
+              lsh::as_stream(stream), true, x, r, w, out, H, eps);
+  return lsh::launch_status("add_rmsnorm");
+}
+
+extern "C" int llmserve_silu_mul(const float* gate_up, float* out, int64_t T, int64_t I,
+                                 void* stream) {
+  LSH_CHECK(T >= 0 && I >= 1, "silu_mul: bad shape T=%lld I=%lld", (long long)T, (long long)I);
+  if (T == 0) return LLMSERVE_OK;
+  LSH_CHECK(gate_up && out, "silu_mul: null pointer");
+  const int64_t n = T * I;
+  const int64_t blocks = (n + kRowThreads - 1) / kRowThreads;
+  lsh::launch(silu_mul_kernel, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)),
+              dim3(kRowThreads), 0, lsh::as_stream(stream), true, gate_up, out, T, I);
+  return lsh::launch_status("silu_mul");
+}
+
+extern "C" int llmserve_rope_qk(float* qkv, const float* cos, const float* sin, int64_t T,
+                                int64_t row_stride, int64_t n_q, int64_t n_k, int64_t D,
+                                const float* q_w, const float* k_w, float eps, void* stream) {
+  LSH_CHECK(T >= 0 && n_q >= 0 && n_k >= 0 && head_dim_ok(D),
+            "rope_qk_: bad shape (head_dim %lld not in {16, 32, 64, 128, 256})", (long long)D);
+  LSH_CHECK(row_stride >= (n_q + n_k) * D, "rope_qk_: bad shapes");
+  LSH_CHECK(T < (1LL << 31) && n_q + n_k < 65536, "rope_qk_: too large");
+  if (T == 0 || n_q + n_k == 0) return LLMSERVE_OK;
+  LSH_CHECK(qkv && cos && sin, "rope_qk_: null pointer");
+  RopeArgs a{};
+  a.qkv = qkv;
+  a.row_stride = row_stride;
+  a.cos = cos;
+  a.sin = sin;
+  a.q_w = q_w;
+  a.k_w = k_w;
+  a.eps = eps;
+  a.T = static_cast<int>(T);
+  a.n_q = static_cast<int>(n_q);
+  a.n_k = static_cast<int>(n_k);
+  a.D = static_cast<int>(D);
+  launch_rope<false>(a, lsh::as_stream(stream));
+  return lsh::launch_status("rope_qk_");
+}
+
+extern "C" int llmserve_decode_qkv_kv(
+    const float* qkv, int64_t row_stride, const float* cos_table, const float* sin_table,
+    int64_t max_pos, const int64_t* context_lens, const int64_t* block_tables, int64_t max_blocks,
+    int64_t block_size, const float* q_w, const float* k_w, float eps, const float* k_smooth,
+    float* q_out, int8_t* k_cache, int8_t* v_cache, float* k_scale, float* v_scale,
+    int64_t num_slots, int64_t T, int64_t n_q, int64_t n_k, int64_t D, void* stream) {
+  LSH_CHECK(T >= 0 && n_q >= 1 && n_k >= 1 && head_dim_ok(D),
+            "decode_qkv_kv: bad shape (head_dim %lld not in {16, 32, 64, 128, 256})",
+            (long long)D);
+  LSH_CHECK(row_stride >= (n_q + 2 * n_k) * D, "decode_qkv_kv: qkv rows too short");
+  LSH_CHECK(block_size >= 1 && max_blocks >= 1 && num_slots >= 0 && max_pos >= 1,
+            "decode_qkv_kv: bad cache shape");
+  LSH_CHECK(T < (1LL << 31) && n_q + 2 * n_k < 65536, "decode_qkv_kv: too large");
+  if (T == 0) return LLMSERVE_OK;
+  LSH_CHECK(qkv && cos_table && sin_table && context_lens && block_tables && q_out && k_cache &&
+                v_cache && k_scale && v_scale,
+            "decode_qkv_kv: null pointer");
+  RopeArgs a{};
+  a.qkv = const_cast<float*>(qkv);
+  a.row_stride = row_stride;
+  a.cos = cos_table;
+  a.sin = sin_table;
+  a.q_w = q_w;
+  a.k_w = k_w;
+  a.eps = eps;
+  a.T = static_cast<int>(T);
+  a.n_q = static_cast<int>(n_q);
+  a.n_k = static_cast<int>(n_k);
+  a.D = static_cast<int>(D);
+  a.ctx = context_lens;
+  a.bt = block_tables;
+  a.max_blocks = max_blocks;
+  a.bs = block_size;
+  a.num_slots = num_slots;
+  a.max_pos = max_pos;
+  a.smooth = k_smooth;
+  a.q_out = q_out;
+  a.kc = k_cache;
+  a.vc = v_cache;
+  a.ks = k_scale;
+  a.vs = v_scale;
+  launch_rope<true>(a, lsh::as_stream(stream));
+  return lsh::launch_status("decode_qkv_kv");
+}
+
+extern "C" int64_t llmserve_argmax_advance_workspace_bytes(int64_t T) {
+  return T > 0 ? T * kArgParts * static_cast<int64_t>(sizeof(float) + sizeof(int64_t)) : 0;
+}
+
+extern "C" int llmserve_argmax_advance(const float* logits, int64_t T, int64_t V,
+                                       int64_t* next_ids, int64_t* context_lens, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  LSH_CHECK(T >= 0 && V >= 1 && T < (1LL << 24), "argmax_advance: bad shape");
+  if (T == 0) return LLMSERVE_OK;
+  LSH_CHECK(logits && next_ids && context_lens, "argmax_advance: null pointer");
+  LSH_CHECK(workspace != nullptr && workspace_bytes >= llmserve_argmax_advance_workspace_bytes(T) &&
+                lsh::aligned16(workspace),
+            "argmax_advance: a 16-byte aligned workspace of %lld bytes is needed",
+            (long long)llmserve_argmax_advance_workspace_bytes(T));
+  int64_t* part_i = static_cast<int64_t*>(workspace);
+  float* part_v = reinterpret_cast<float*>(part_i + T * kArgParts);
+  hipStream_t st = lsh::as_stream(stream);
+  lsh::launch(argmax_parts_kernel, dim3(static_cast<unsigned>(T * kArgParts)), dim3(kRowThreads), 0,
+              st, false, logits, V, part_v, part_i);
+  lsh::launch(argmax_finish_kernel, dim3(static_cast<unsigned>(T)), dim3(kWave), 0, st, true,
+              part_v, part_i, V, next_ids, context_lens);
+  return lsh::launch_status("argmax_advance");
+}

@@ -11,10 +11,12 @@
 #pragma clang fp contract(off)
 
 #include "common.h"
+#include "kv_quant.h"
 
 namespace {
 
 using lsh::kWave;
+constexpr int kMaxKvRow = 256;  // head_dim limit of the KV quantizer (one wavefront per row)
 
 __device__ __forceinline__ float clampf(float v, float lo, float hi) {
   return fminf(fmaxf(v, lo), hi);
@@ -103,21 +105,14 @@ __global__ __launch_bounds__(256) void kv_quantize_write_kernel(
   const int64_t slot = slots[t];
   if (slot < 0 || slot >= num_slots) return;
   const float* xr = x + (t * Hk + h) * D;
-  const float* sm = smooth ? smooth + h * D : nullptr;
-  float amax = 0.f;
-  for (int64_t d = lane; d < D; d += kWave) {
-    const float v = sm ? xr[d] / sm[d] : xr[d];
-    amax = fmaxf(amax, fabsf(v));
+  float v[kMaxKvRow / kWave];
+#pragma unroll
+  for (int i = 0; i < kMaxKvRow / kWave; ++i) {
+    const int64_t d = lane + i * kWave;
+    v[i] = d < D ? xr[d] : 0.f;
   }
-  amax = lsh::wave_max_from<1>(amax);
-  // x.abs().amax(-1).clamp_min(1e-8) / 127.0: clamp, then divide.
-  const float s = fmaxf(amax, 1e-8f) / 127.0f;
-  int8_t* out = data + (slot * Hk + h) * D;
-  for (int64_t d = lane; d < D; d += kWave) {
-    const float v = sm ? xr[d] / sm[d] : xr[d];
-    out[d] = static_cast<int8_t>(clampf(rintf(v / s), -127.f, 127.f));
-  }
-  if (lane == 0) scale[slot * Hk + h] = s;
+  lsh::kv_quant_row(v, smooth ? smooth + h * D : nullptr, static_cast<int>(D),
+                    data + (slot * Hk + h) * D, scale + slot * Hk + h);
 }
 
 constexpr int kWavesPerBlock = 4;
@@ -165,6 +160,7 @@ extern "C" int llmserve_kv_quantize_write(const float* x, const int64_t* slots,
                                           int64_t T, int64_t Hk, int64_t D, int64_t num_slots,
                                           void* stream) {
   LSH_CHECK(T >= 0 && Hk >= 1 && D >= 1 && num_slots >= 0, "kv_quantize_write: bad shape");
+  LSH_CHECK(D <= kMaxKvRow, "kv_quantize_write: head_dim %lld > %d", (long long)D, kMaxKvRow);
   const int64_t waves = T * Hk;
   if (waves == 0) return LLMSERVE_OK;
   LSH_CHECK(x && slots && data && scale, "kv_quantize_write: null pointer");

@@ -212,6 +212,147 @@ at::Tensor int4_linear_gemm(const at::Tensor& x, const at::Tensor& nibbles, cons
   return y;
 }
 
+// ---- decoder-layer elementwise ops (fused_ops.cpp:39-127) and decode glue --------------------
+
+void check_f32(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.scalar_type() == at::kFloat && t.is_contiguous(), name,
+              ": contiguous float32 tensor expected");
+}
+
+at::Tensor rmsnorm(const at::Tensor& x, const at::Tensor& w, double eps) {
+  check_f32(x, "x");
+  check_f32(w, "w");
+  check_device(x, {&w}, "rmsnorm");
+  const int64_t H = x.size(-1), T = x.numel() / H;
+  TORCH_CHECK(w.numel() == H, "rmsnorm: weight must have x.size(-1) entries");
+  const c10::DeviceGuard guard(x.device());
+  auto out = at::empty_like(x);
+  check_status(llmserve_rmsnorm(x.data_ptr<float>(), w.data_ptr<float>(), out.data_ptr<float>(), T,
+                                H, static_cast<float>(eps), stream_of(x)));
+  return out;
+}
+
+at::Tensor add_rmsnorm_(at::Tensor& x, const at::Tensor& r, const at::Tensor& w, double eps) {
+  check_f32(x, "x");
+  check_f32(r, "r");
+  check_f32(w, "w");
+  check_device(x, {&r, &w}, "add_rmsnorm_");
+  TORCH_CHECK(x.sizes() == r.sizes(), "add_rmsnorm_: shape mismatch");
+  const int64_t H = x.size(-1), T = x.numel() / H;
+  TORCH_CHECK(w.numel() == H, "add_rmsnorm_: weight must have x.size(-1) entries");
+  const c10::DeviceGuard guard(x.device());
+  auto out = at::empty_like(x);
+  check_status(llmserve_add_rmsnorm(x.data_ptr<float>(), r.data_ptr<float>(), w.data_ptr<float>(),
+                                    out.data_ptr<float>(), T, H, static_cast<float>(eps),
+                                    stream_of(x)));
+  return out;
+}
+
+at::Tensor silu_mul(const at::Tensor& gate_up) {
+  check_f32(gate_up, "gate_up");
+  check_device(gate_up, {}, "silu_mul");
+  TORCH_CHECK(gate_up.size(-1) % 2 == 0, "silu_mul: last dimension must be 2 * I");
+  const int64_t I = gate_up.size(-1) / 2, T = gate_up.numel() / (2 * I);
+  const c10::DeviceGuard guard(gate_up.device());
+  auto out = at::empty({T, I}, gate_up.options());
+  check_status(llmserve_silu_mul(gate_up.data_ptr<float>(), out.data_ptr<float>(), T, I,
+                                 stream_of(gate_up)));
+  return out;
+}
+
+void rope_qk_(at::Tensor& qkv, const at::Tensor& cos, const at::Tensor& sin, int64_t n_q,
+              int64_t n_k, int64_t head_dim, const std::optional<at::Tensor>& q_w,
+              const std::optional<at::Tensor>& k_w, double eps) {
+  check_f32(qkv, "qkv");
+  check_f32(cos, "cos");
+  check_f32(sin, "sin");
+  check_device(qkv, {&cos, &sin}, "rope_qk_");
+  TORCH_CHECK(qkv.dim() == 2, "rope_qk_: qkv must be [T, row]");
+  const int64_t T = qkv.size(0), row = qkv.size(1);
+  TORCH_CHECK(row >= (n_q + n_k) * head_dim && cos.numel() == T * head_dim &&
+                  sin.numel() == T * head_dim,
+              "rope_qk_: bad shapes");
+  for (const auto* w : {&q_w, &k_w})
+    if (w->has_value()) {
+      check_f32(**w, "norm weight");
+      check_device(qkv, {&**w}, "rope_qk_");
+      TORCH_CHECK((*w)->numel() == head_dim, "rope_qk_: norm weights must have head_dim entries");
+    }
+  const c10::DeviceGuard guard(qkv.device());
+  check_status(llmserve_rope_qk(qkv.data_ptr<float>(), cos.data_ptr<float>(), sin.data_ptr<float>(),
+                                T, row, n_q, n_k, head_dim, opt_ptr<float>(q_w), opt_ptr<float>(k_w),
+                                static_cast<float>(eps), stream_of(qkv)));
+}
+
+at::Tensor decode_qkv_kv(const at::Tensor& qkv, const at::Tensor& cos_table,
+                         const at::Tensor& sin_table, const at::Tensor& context_lens,
+                         const at::Tensor& block_tables, int64_t block_size,
+                         const std::optional<at::Tensor>& q_w, const std::optional<at::Tensor>& k_w,
+                         double eps, const std::optional<at::Tensor>& k_smooth, at::Tensor& k_cache,
+                         at::Tensor& v_cache, at::Tensor& k_scale, at::Tensor& v_scale, int64_t n_q,
+                         int64_t n_k, int64_t head_dim) {
+  check_f32(qkv, "qkv");
+  check_f32(cos_table, "cos_table");
+  check_f32(sin_table, "sin_table");
+  check_f32(k_scale, "k_scale");
+  check_f32(v_scale, "v_scale");
+  TORCH_CHECK(context_lens.scalar_type() == at::kLong && block_tables.scalar_type() == at::kLong &&
+                  context_lens.is_contiguous() && block_tables.is_contiguous(),
+              "decode_qkv_kv: int64 contiguous context_lens / block_tables");
+  TORCH_CHECK(k_cache.scalar_type() == at::kChar && v_cache.scalar_type() == at::kChar &&
+                  k_cache.is_contiguous() && v_cache.is_contiguous(),
+              "decode_qkv_kv: int8 contiguous caches");
+  check_device(qkv, {&cos_table, &sin_table, &context_lens, &block_tables, &k_cache, &v_cache,
+                     &k_scale, &v_scale},
+               "decode_qkv_kv");
+  TORCH_CHECK(qkv.dim() == 2 && block_tables.dim() == 2, "decode_qkv_kv: 2-D qkv and block_tables");
+  const int64_t T = qkv.size(0);
+  TORCH_CHECK(context_lens.numel() == T && block_tables.size(0) == T,
+              "decode_qkv_kv: one context length and block-table row per token");
+  TORCH_CHECK(cos_table.dim() == 2 && cos_table.size(1) == head_dim &&
+                  sin_table.sizes() == cos_table.sizes(),
+              "decode_qkv_kv: cos/sin tables must be [max_pos, head_dim]");
+  TORCH_CHECK(k_cache.dim() == 3 && k_cache.size(1) == n_k && k_cache.size(2) == head_dim &&
+                  v_cache.sizes() == k_cache.sizes() && k_scale.numel() == k_cache.size(0) * n_k &&
+                  v_scale.numel() == k_scale.numel(),
+              "decode_qkv_kv: caches must be [num_slots, n_k, head_dim], scales [num_slots, n_k]");
+  for (const auto* w : {&q_w, &k_w, &k_smooth})
+    if (w->has_value()) {
+      check_f32(**w, "weight");
+      check_device(qkv, {&**w}, "decode_qkv_kv");
+    }
+  const c10::DeviceGuard guard(qkv.device());
+  auto q_out = at::empty({T, n_q, head_dim}, qkv.options());
+  check_status(llmserve_decode_qkv_kv(
+      qkv.data_ptr<float>(), qkv.size(1), cos_table.data_ptr<float>(), sin_table.data_ptr<float>(),
+      cos_table.size(0), context_lens.data_ptr<int64_t>(), block_tables.data_ptr<int64_t>(),
+      block_tables.size(1), block_size, opt_ptr<float>(q_w), opt_ptr<float>(k_w),
+      static_cast<float>(eps), opt_ptr<float>(k_smooth), q_out.data_ptr<float>(),
+      k_cache.data_ptr<int8_t>(), v_cache.data_ptr<int8_t>(), k_scale.data_ptr<float>(),
+      v_scale.data_ptr<float>(), k_cache.size(0), T, n_q, n_k, head_dim, stream_of(qkv)));
+  return q_out;
+}
+
+at::Tensor argmax_advance(const at::Tensor& logits, at::Tensor& context_lens) {
+  check_f32(logits, "logits");
+  TORCH_CHECK(context_lens.scalar_type() == at::kLong && context_lens.is_contiguous(),
+              "argmax_advance: int64 contiguous context_lens");
+  check_device(logits, {&context_lens}, "argmax_advance");
+  TORCH_CHECK(logits.dim() == 2 && context_lens.numel() == logits.size(0),
+              "argmax_advance: logits [T, V] and T context lengths");
+  const c10::DeviceGuard guard(logits.device());
+  const int64_t T = logits.size(0), V = logits.size(1);
+  auto ids = at::empty({T}, context_lens.options());
+  const int64_t ws_bytes = llmserve_argmax_advance_workspace_bytes(T);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({(ws_bytes + 15) / 16 * 4}, logits.options());
+  check_status(llmserve_argmax_advance(logits.data_ptr<float>(), T, V, ids.data_ptr<int64_t>(),
+                                       context_lens.data_ptr<int64_t>(),
+                                       ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+                                       stream_of(logits)));
+  return ids;
+}
+
 // ---- int8-KV paged decode -------------------------------------------------------------------
 
 at::Tensor paged_attention_decode_int8(const at::Tensor& q, const at::Tensor& k_cache,
@@ -280,6 +421,16 @@ TORCH_LIBRARY(llmserve_hip, m) {
         " Tensor? inv_act_scale=None) -> Tensor");
   m.def("int4_linear_gemm(Tensor x, Tensor nibbles, Tensor scale, Tensor zero, int group_size,"
         " Tensor? inv_act_scale=None) -> Tensor");
+  m.def("rmsnorm(Tensor x, Tensor w, float eps) -> Tensor");
+  m.def("add_rmsnorm_(Tensor(a!) x, Tensor r, Tensor w, float eps) -> Tensor");
+  m.def("silu_mul(Tensor gate_up) -> Tensor");
+  m.def("rope_qk_(Tensor(a!) qkv, Tensor cos, Tensor sin, int n_q, int n_k, int head_dim,"
+        " Tensor? q_w=None, Tensor? k_w=None, float eps=1e-6) -> ()");
+  m.def("decode_qkv_kv(Tensor qkv, Tensor cos_table, Tensor sin_table, Tensor context_lens,"
+        " Tensor block_tables, int block_size, Tensor? q_w, Tensor? k_w, float eps,"
+        " Tensor? k_smooth, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor(c!) k_scale,"
+        " Tensor(d!) v_scale, int n_q, int n_k, int head_dim) -> Tensor");
+  m.def("argmax_advance(Tensor logits, Tensor(a!) context_lens) -> Tensor");
   m.def("paged_attention_decode_int8(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale,"
         " Tensor v_scale, Tensor block_tables, Tensor context_lens, int block_size, float scale,"
         " int partition_size=0, Tensor? q_mult=None) -> Tensor");
@@ -293,5 +444,11 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("int8_linear_prefill", &int8_linear_prefill);
   m.impl("int4_linear_gemm", &int4_linear_gemm);
   m.impl("int4_linear", &int4_linear);
+  m.impl("rmsnorm", &rmsnorm);
+  m.impl("add_rmsnorm_", &add_rmsnorm_);
+  m.impl("silu_mul", &silu_mul);
+  m.impl("rope_qk_", &rope_qk_);
+  m.impl("decode_qkv_kv", &decode_qkv_kv);
+  m.impl("argmax_advance", &argmax_advance);
   m.impl("paged_attention_decode_int8", &paged_attention_decode_int8);
 }

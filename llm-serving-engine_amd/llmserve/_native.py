@@ -55,6 +55,17 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
     "llmserve_int4_linear_gemm": (_I32, [_P] * 6 + [_I64] * 4 + [_P, _I64, _P]),
     "llmserve_int8_linear_prefill_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "llmserve_int8_linear_prefill": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P]),
+    "llmserve_rmsnorm": (_I32, [_P, _P, _P, _I64, _I64, _F32, _P]),
+    "llmserve_add_rmsnorm": (_I32, [_P, _P, _P, _P, _I64, _I64, _F32, _P]),
+    "llmserve_silu_mul": (_I32, [_P, _P, _I64, _I64, _P]),
+    "llmserve_rope_qk": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _F32, _P]),
+    "llmserve_decode_qkv_kv": (
+        _I32,
+        [_P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _F32, _P, _P, _P, _P, _P, _P]
+        + [_I64] * 5 + [_P],
+    ),
+    "llmserve_argmax_advance_workspace_bytes": (_I64, [_I64]),
+    "llmserve_argmax_advance": (_I32, [_P, _I64, _I64, _P, _P, _P, _I64, _P]),
     "llmserve_paged_attention_workspace_bytes": (_I64, [_I64] * 7),
     "llmserve_paged_attention_decode_int8": (
         _I32,

@@ -15,8 +15,13 @@ objects expose the reference's function names and signatures:
   v_scale, block_tables, context_lens, block_size, scale, partition_size=0, q_mult=None)``
   (paged_attention.cpp:386-399; ``q_mult`` fuses the key-smoothing multiply of q).
 
+* ``load_fused_ops()``: ``rmsnorm(x, w, eps)``, ``add_rmsnorm_(x, r, w, eps)``,
+  ``silu_mul(gate_up)`` and ``rope_qk_(qkv, cos, sin, n_q, n_k, head_dim, q_w=None, k_w=None,
+  eps=1e-6)`` (fused_ops.cpp:129-137), plus the decode-step glue ``decode_qkv_kv`` (q/k norm,
+  RoPE and the int8 KV-cache write in one launch) and ``argmax_advance`` (greedy next token).
+
 The fp32-KV decode variants (``paged_attention_decode``, ``paged_attention_decode_v1``,
-``set_simd``) and ``load_fused_ops`` are outside the quantized path and not provided.
+``set_simd``) are outside the quantized path and not provided.
 """
 
 from __future__ import annotations
@@ -26,7 +31,8 @@ from types import SimpleNamespace
 
 from llmserve._native import NativeLibraryMissing, ops
 
-__all__ = ["NativeLibraryMissing", "load_int8_gemv", "load_paged_attention", "load_quant"]
+__all__ = ["NativeLibraryMissing", "load_fused_ops", "load_int8_gemv", "load_paged_attention",
+           "load_quant"]
 
 
 @functools.cache
@@ -53,4 +59,18 @@ def load_quant() -> SimpleNamespace:
         int8_quantize=o.int8_quantize,
         int4_quantize=o.int4_quantize,
         kv_quantize_write=o.kv_quantize_write,
+    )
+
+
+@functools.cache
+def load_fused_ops() -> SimpleNamespace:
+    """Decoder-layer elementwise ops and decode-step glue (HIP, gfx950)."""
+    o = ops()
+    return SimpleNamespace(
+        rmsnorm=o.rmsnorm,
+        add_rmsnorm_=o.add_rmsnorm_,
+        silu_mul=o.silu_mul,
+        rope_qk_=o.rope_qk_,
+        decode_qkv_kv=o.decode_qkv_kv,
+        argmax_advance=o.argmax_advance,
     )

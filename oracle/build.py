@@ -4,7 +4,8 @@
 
 1. ``oracle/lib/<isa>/liboracle_cpu.so`` from ``oracle/cpu_kernels.c``.
 2. When ``/root/reference`` is present: the reference's own kernel sources
-   ``src/llmserve/kernels/csrc/int8_gemv.cpp`` and ``paged_attention.cpp`` compiled where
+   ``src/llmserve/kernels/csrc/int8_gemv.cpp``, ``paged_attention.cpp`` and ``fused_ops.cpp``
+   compiled where
    they lie, as PyTorch CPU extension modules, into ``oracle/_ref/<isa>/`` — the same
    sources and flags the reference's JIT loader uses (kernels/__init__.py:58-72), with
    g++ called directly instead of torch's build system. Nothing from the reference is
@@ -85,7 +86,8 @@ def build_ref(jobs: int = 4) -> list[Path]:
     if not REF_CSRC.is_dir():
         return []
     specs = [("int8_gemv.cpp", "llmserve_int8_gemv", []),
-             ("paged_attention.cpp", "llmserve_paged_attention", ["-lmvec"])]
+             ("paged_attention.cpp", "llmserve_paged_attention", ["-lmvec"]),
+             ("fused_ops.cpp", "llmserve_fused_ops", [])]
     cmds, outs = [], []
     for isa in ISAS:
         (HERE / "_ref" / isa).mkdir(parents=True, exist_ok=True)

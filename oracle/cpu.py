@@ -129,13 +129,14 @@ def ref_available(isa: str | None = None) -> bool:
     except RuntimeError:
         return False
     return all(ref_module_path(isa, n).is_file()
-               for n in ("llmserve_int8_gemv", "llmserve_paged_attention"))
+               for n in ("llmserve_int8_gemv", "llmserve_paged_attention", "llmserve_fused_ops"))
 
 
 @functools.cache
 def ref_module(name: str, isa: str | None = None):
-    """The reference's compiled kernel module ``name`` (llmserve_int8_gemv or
-    llmserve_paged_attention) from oracle/_ref/<isa>/. Needs torch (CPU tensors)."""
+    """The reference's compiled kernel module ``name`` (llmserve_int8_gemv,
+    llmserve_paged_attention or llmserve_fused_ops) from oracle/_ref/<isa>/. Needs torch
+    (CPU tensors)."""
     import torch  # noqa: F401  (the extension links libtorch)
 
     isa = isa or host_isa()

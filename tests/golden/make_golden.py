@@ -15,6 +15,11 @@ int4_linear, paged_attention_decode_int8 built from the reference sources into
 oracle/_ref/ by oracle/build.py) on small seeded inputs, including odd shapes, several
 group sizes, ragged contexts and forced partition sizes. Skipped when oracle/_ref is not
 built.
+
+fused_golden.npz — outputs of the reference's compiled fused decoder-layer ops (rmsnorm,
+add_rmsnorm_, silu_mul, rope_qk_ from fused_ops.cpp) on small seeded inputs: odd and Qwen3
+hidden sizes, q/k norms on and off, head dims 64 and 128, RoPE tables at arbitrary positions.
+Skipped when oracle/_ref is not built.
 """
 
 from __future__ import annotations
@@ -224,6 +229,45 @@ def kernels_golden() -> dict[str, np.ndarray] | None:
     return out
 
 
+def fused_golden() -> dict[str, np.ndarray] | None:
+    from oracle import cpu as ocpu
+    from oracle import fused_ops as ofo
+
+    if not ocpu.ref_available():
+        return None
+    fo = ocpu.ref_module("llmserve_fused_ops")
+    g = torch.Generator().manual_seed(123)
+    out: dict[str, np.ndarray] = {}
+    for T, H in ((3, 1024), (2, 200), (1, 2048)):
+        x = torch.randn(T, H, generator=g) * 3.0
+        r = torch.randn(T, H, generator=g)
+        w = torch.rand(H, generator=g) + 0.5
+        key = f"norm_T{T}_H{H}"
+        out.update({key + "_x": x.numpy().copy(), key + "_r": r.numpy(), key + "_w": w.numpy(),
+                    key + "_out": fo.rmsnorm(x, w, 1e-6).numpy()})
+        xa = x.clone()
+        o = fo.add_rmsnorm_(xa, r, w, 1e-6)
+        out.update({key + "_xadd": xa.numpy(), key + "_outadd": o.numpy()})
+    for T, I in ((2, 300), (4, 3072)):
+        gu = torch.randn(T, 2 * I, generator=g) * 4.0
+        out.update({f"silu_T{T}_I{I}_gu": gu.numpy(), f"silu_T{T}_I{I}_out": fo.silu_mul(gu).numpy()})
+    for name, T, nq, nk, D, norms in (("rope_d128", 3, 4, 2, 128, True), ("rope_d64", 2, 2, 1, 64, False)):
+        row = (nq + 2 * nk) * D
+        qkv = torch.randn(T, row, generator=g)
+        pos = np.array([0, 17, 4095][:T], np.int64)
+        c, s_ = ofo.rope_tables(pos, D, 1e6)
+        qw = torch.rand(D, generator=g) + 0.5 if norms else None
+        kw = torch.rand(D, generator=g) + 0.5 if norms else None
+        res = qkv.clone()
+        fo.rope_qk_(res, torch.from_numpy(c), torch.from_numpy(s_), nq, nk, D, qw, kw, 1e-6)
+        out.update({f"{name}_qkv": qkv.numpy(), f"{name}_cos": c, f"{name}_sin": s_,
+                    f"{name}_out": res.numpy(),
+                    f"{name}_meta": np.array([nq, nk, D, int(norms)], np.int64)})
+        if norms:
+            out.update({f"{name}_qw": qw.numpy(), f"{name}_kw": kw.numpy()})
+    return out
+
+
 def main() -> None:
     torch.set_num_threads(4)
     np.savez_compressed(HERE / "quant_golden.npz", **quant_golden())
@@ -234,6 +278,10 @@ def main() -> None:
     else:
         np.savez_compressed(HERE / "kernels_golden.npz", **k)
         print("wrote", HERE / "kernels_golden.npz")
+    f = fused_golden()
+    if f is not None:
+        np.savez_compressed(HERE / "fused_golden.npz", **f)
+        print("wrote", HERE / "fused_golden.npz")
 
 
 if __name__ == "__main__":

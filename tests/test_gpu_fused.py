@@ -1,0 +1,163 @@
+"""HIP fused decoder-layer ops and decode-step glue against the oracle.
+
+Tolerances (fp32, a different reduction order than the reference's): max-abs <= 2e-6 x max|y|
+against the float64 mathematics and the reference's compiled fused_ops (committed goldens).
+The fused post-qkv decode kernel (norm + RoPE + int8 KV write) is compared bit for bit with
+the composition of this build's rope_qk_ and llmserve_kv_quantize_write, whose quantizer is
+bit-exact with the reference's (tests/test_gpu_quant.py).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import capi_util as cu
+from conftest import GOLDEN
+from oracle import fused_ops as ofo
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+TOL = 2e-6
+
+
+def fo():
+    from llmserve.kernels import load_fused_ops
+
+    return load_fused_ops()
+
+
+@pytest.fixture(scope="module")
+def fg():
+    return dict(np.load(GOLDEN / "fused_golden.npz"))
+
+
+def _rel(a, b):
+    a = a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else a
+    return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+@pytest.mark.parametrize("T,H", [(3, 1024), (2, 200), (1, 2048)])
+def test_norms(gpu, fg, T, H):
+    k = f"norm_T{T}_H{H}"
+    x, r, w = fg[k + "_x"], fg[k + "_r"], fg[k + "_w"]
+    out = fo().rmsnorm(cu.dev(x), cu.dev(w), 1e-6)
+    assert _rel(out, fg[k + "_out"]) < 2 * TOL
+    assert _rel(out, ofo.rmsnorm_f64(x, w, 1e-6)) < TOL
+    xd = cu.dev(x)
+    o = fo().add_rmsnorm_(xd, cu.dev(r), cu.dev(w), 1e-6)
+    assert np.array_equal(xd.cpu().numpy(), fg[k + "_xadd"])  # x += r in place, one fp32 add
+    assert _rel(o, fg[k + "_outadd"]) < 2 * TOL
+
+
+@pytest.mark.parametrize("T,I", [(2, 300), (4, 3072)])
+def test_silu_mul(gpu, fg, T, I):
+    gu = fg[f"silu_T{T}_I{I}_gu"]
+    out = fo().silu_mul(cu.dev(gu))
+    assert _rel(out, fg[f"silu_T{T}_I{I}_out"]) < 2 * TOL
+    assert _rel(out, ofo.silu_mul_f64(gu)) < TOL
+
+
+@pytest.mark.parametrize("name", ["rope_d128", "rope_d64"])
+def test_rope_qk_inplace(gpu, fg, name):
+    nq, nk, D, norms = (int(v) for v in fg[f"{name}_meta"])
+    qw = fg.get(f"{name}_qw") if norms else None
+    kw = fg.get(f"{name}_kw") if norms else None
+    qkv = cu.dev(fg[f"{name}_qkv"])
+    fo().rope_qk_(qkv, cu.dev(fg[f"{name}_cos"]), cu.dev(fg[f"{name}_sin"]), nq, nk, D,
+                  None if qw is None else cu.dev(qw), None if kw is None else cu.dev(kw), 1e-6)
+    args = (fg[f"{name}_qkv"], fg[f"{name}_cos"], fg[f"{name}_sin"], nq, nk, D, qw, kw, 1e-6)
+    assert _rel(qkv, fg[f"{name}_out"]) < 2 * TOL
+    assert _rel(qkv, ofo.rope_qk_f64(*args)) < TOL
+
+
+@pytest.mark.parametrize("D", [16, 32, 256])
+def test_rope_other_head_dims(gpu, D):
+    rng = np.random.default_rng(D)
+    T, nq, nk = 3, 2, 1
+    qkv = rng.standard_normal((T, (nq + 2 * nk) * D)).astype(F32)
+    c, s = ofo.rope_tables(np.array([1, 9, 300]), D, 1e4)
+    qw = (rng.random(D) + 0.5).astype(F32)
+    t = cu.dev(qkv)
+    fo().rope_qk_(t, cu.dev(c), cu.dev(s), nq, nk, D, cu.dev(qw), None, 1e-6)
+    assert _rel(t, ofo.rope_qk_f64(qkv, c, s, nq, nk, D, qw, None, 1e-6)) < TOL
+
+
+@pytest.mark.parametrize("smooth", [False, True])
+def test_decode_qkv_kv_matches_composition(gpu, smooth):
+    """Fused norm + RoPE + KV write == rope_qk_ (cos/sin rows at each position) followed by
+    kv_quantize_write at the slots the block tables give, bit for bit."""
+    rng = np.random.default_rng(5 + smooth)
+    T, nq, nk, D, bs, nblk = 5, 4, 2, 128, 16, 40
+    ctx = np.array([1, 16, 17, 300, 64], np.int64)  # positions 0, 15, 16, 299, 63
+    width = -(-int(ctx.max()) // bs)
+    perm = rng.permutation(nblk)
+    bt = np.zeros((T, width), np.int64)
+    used = 0
+    for i, c in enumerate(ctx):
+        n = -(-int(c) // bs)
+        bt[i, :n] = perm[used:used + n] if used + n <= nblk else rng.integers(0, nblk, n)
+        used += n
+    qkv = rng.standard_normal((T, (nq + 2 * nk) * D)).astype(F32)
+    qkv[:, nq * D + 5] *= 30  # an outlier key channel
+    cos_t, sin_t = ofo.rope_tables(np.arange(512), D, 1e6)
+    qw = (rng.random(D) + 0.5).astype(F32)
+    kw = (rng.random(D) + 0.5).astype(F32)
+    sm = (rng.random((nk, D)) + 0.5).astype(F32) if smooth else None
+    kc = torch.zeros(nblk * bs, nk, D, dtype=torch.int8, device="cuda")
+    vc, ks, vs = torch.zeros_like(kc), torch.zeros(nblk * bs, nk, device="cuda"), None
+    vs = torch.zeros_like(ks)
+    q = fo().decode_qkv_kv(cu.dev(qkv), cu.dev(cos_t), cu.dev(sin_t), cu.dev(ctx), cu.dev(bt), bs,
+                           cu.dev(qw), cu.dev(kw), 1e-6, None if sm is None else cu.dev(sm),
+                           kc, vc, ks, vs, nq, nk, D)
+    # composition
+    pos = ctx - 1
+    ref = cu.dev(qkv)
+    fo().rope_qk_(ref, cu.dev(cos_t[pos]), cu.dev(sin_t[pos]), nq, nk, D, cu.dev(qw), cu.dev(kw), 1e-6)
+    refn = ref.cpu().numpy()
+    assert np.array_equal(q.cpu().numpy().reshape(T, nq * D), refn[:, :nq * D])
+    slots = cu.dev(np.array([bt[i, p // bs] * bs + p % bs for i, p in enumerate(pos)], np.int64))
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    ks2, vs2 = torch.zeros_like(ks), torch.zeros_like(vs)
+    k_rows = torch.from_numpy(refn[:, nq * D:(nq + nk) * D].reshape(T, nk, D).copy()).cuda()
+    v_rows = torch.from_numpy(qkv[:, (nq + nk) * D:].reshape(T, nk, D).copy()).cuda()
+    cu.kv_quantize_write(k_rows, slots, kc2, ks2, None if sm is None else cu.dev(sm))
+    cu.kv_quantize_write(v_rows, slots, vc2, vs2)
+    for a, b in ((kc, kc2), (vc, vc2), (ks, ks2), (vs, vs2)):
+        assert torch.equal(a, b)
+    # and the quantized K rows equal the oracle quantizer on the oracle's RoPE output
+    ko = ofo.rope_qk(qkv, cos_t[pos], sin_t[pos], nq, nk, D, qw, kw, 1e-6)[:, nq * D:(nq + nk) * D]
+    kq, kss = oq.kv_quantize(oq.kv_smooth(ko.reshape(T, nk, D), sm) if sm is not None else ko.reshape(T, nk, D))
+    got = kc[slots.cpu().numpy()].cpu().numpy()
+    assert np.abs(got.astype(np.int32) - kq.astype(np.int32)).max() <= 1  # fp32 ulps may move a tie
+
+
+def test_argmax_advance(gpu):
+    """Greedy selection == torch.argmax on the CPU (sampling.py:170): first index among equal
+    maxima, NaN above every number (the first NaN wins), an all -inf row gives 0."""
+    rng = np.random.default_rng(3)
+    T, V = 7, 151936
+    logits = rng.standard_normal((T, V)).astype(F32)
+    logits[1, 77] = logits[1, 150000] = 50.0  # tie: the first index wins
+    logits[2, V - 1] = 60.0
+    logits[3, 0] = 60.0
+    logits[4, 12345] = logits[4, 99999] = np.nan
+    logits[5] = -np.inf
+    ctx = np.arange(5, 5 + T, dtype=np.int64)
+    c = cu.dev(ctx)
+    ids = fo().argmax_advance(cu.dev(logits), c).cpu().numpy()
+    want = torch.from_numpy(logits).argmax(-1).numpy()
+    assert np.array_equal(ids, want)
+    assert ids[1] == 77 and ids[4] == 12345 and ids[5] == 0
+    assert np.array_equal(c.cpu().numpy(), ctx + 1)
+
+
+@pytest.mark.parametrize("V", [1, 31, 1000])
+def test_argmax_small_vocab(gpu, V):
+    rng = np.random.default_rng(V)
+    logits = rng.integers(-3, 3, (4, V)).astype(F32)  # many ties
+    c = cu.dev(np.zeros(4, np.int64))
+    ids = fo().argmax_advance(cu.dev(logits), c).cpu().numpy()
+    assert np.array_equal(ids, torch.from_numpy(logits).argmax(-1).numpy())
