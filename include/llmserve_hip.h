@@ -162,6 +162,15 @@ int llmserve_add_rmsnorm(float* x, const float* r, const float* w, float* out, i
                          int64_t H, float eps, void* stream);
 
 /*
+ * x[t] = embed[ids[t]], then out[t] = rmsnorm(x[t]) * w: the embedding lookup and the first
+ * layer's input norm of the fused forward (replaces embed_tokens + fo.rmsnorm,
+ * models/transformer.py:151-155). ids int64 [T] in [0, V) (an id outside gives a NaN row);
+ * embed fp32 [V, H]; x (the residual stream) and out fp32 [T, H].
+ */
+int llmserve_embed_rmsnorm(const int64_t* ids, const float* embed, int64_t V, const float* w,
+                           float* x, float* out, int64_t T, int64_t H, float eps, void* stream);
+
+/*
  * out[t, i] = gate / (1 + exp(-gate)) * up for a fused gate|up row (replaces silu_mul,
  * fused_ops.cpp:83-99). gate_up fp32 [T, 2I] -> out fp32 [T, I].
  */

@@ -28,11 +28,18 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
-// out = w * (x * inv), inv = 1 / sqrt(mean(x^2) + eps) (fused_ops.cpp:23-30); ADD first does
-// x += r in place (add_rmsnorm_, fused_ops.cpp:60-81). One workgroup per row.
-template <bool ADD>
+// out = w * (x * inv), inv = 1 / sqrt(mean(x^2) + eps) (fused_ops.cpp:23-30). One workgroup
+// per row. kNormAdd first does x += r in place (add_rmsnorm_, fused_ops.cpp:60-81);
+// kNormGather first copies the embedding row r[ids[t]] into x (the embedding lookup of
+// transformer.py:151 followed by its first rmsnorm, :155); an id outside [0, V) gives a NaN
+// row, so that a bad token shows in the logits instead of reading out of bounds.
+enum NormMode { kNormPlain = 0, kNormAdd = 1, kNormGather = 2 };
+
+template <int MODE>
 __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(float* __restrict__ x,
                                                               const float* __restrict__ r,
+                                                              const int64_t* __restrict__ ids,
+                                                              int64_t V,
                                                               const float* __restrict__ w,
                                                               float* __restrict__ out, int64_t H,
                                                               float eps) {
@@ -40,13 +47,19 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(float* __restrict_
   const int64_t t = blockIdx.x;
   float* xr = x + t * H;
   float* orow = out + t * H;
+  const float* src = xr;
+  bool bad = false;
+  if (MODE == kNormGather) {
+    const int64_t id = ids[t];
+    bad = id < 0 || id >= V;
+    src = r + (bad ? 0 : id) * H;
+  }
   float ss = 0.f;
   for (int64_t i = threadIdx.x; i < H; i += kRowThreads) {
-    float v = xr[i];
-    if (ADD) {
-      v += r[t * H + i];
-      xr[i] = v;
-    }
+    float v = src[i];
+    if (MODE == kNormAdd) v += r[t * H + i];
+    if (MODE == kNormGather && bad) v = __builtin_nanf("");
+    if (MODE != kNormPlain) xr[i] = v;
     ss += v * v;
   }
   ss = block_sum(ss, red);
@@ -281,8 +294,9 @@ extern "C" int llmserve_rmsnorm(const float* x, const float* w, float* out, int6
             (long long)H);
   if (T == 0) return LLMSERVE_OK;
   LSH_CHECK(x && w && out, "rmsnorm: null pointer");
-  lsh::launch(rmsnorm_kernel<false>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
-              lsh::as_stream(stream), true, const_cast<float*>(x), nullptr, w, out, H, eps);
+  lsh::launch(rmsnorm_kernel<kNormPlain>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
+              lsh::as_stream(stream), true, const_cast<float*>(x), nullptr, nullptr, int64_t{0},
+              w, out, H, eps);
   return lsh::launch_status("rmsnorm");
 }
 
@@ -292,9 +306,22 @@ extern "C" int llmserve_add_rmsnorm(float* x, const float* r, const float* w, fl
             (long long)T, (long long)H);
   if (T == 0) return LLMSERVE_OK;
   LSH_CHECK(x && r && w && out, "add_rmsnorm: null pointer");
-  lsh::launch(rmsnorm_kernel<true>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
-              lsh::as_stream(stream), true, x, r, w, out, H, eps);
+  lsh::launch(rmsnorm_kernel<kNormAdd>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
+              lsh::as_stream(stream), true, x, r, nullptr, int64_t{0}, w, out, H, eps);
   return lsh::launch_status("add_rmsnorm");
+}
+
+extern "C" int llmserve_embed_rmsnorm(const int64_t* ids, const float* embed, int64_t V,
+                                      const float* w, float* x, float* out, int64_t T, int64_t H,
+                                      float eps, void* stream) {
+  LSH_CHECK(T >= 0 && H >= 1 && V >= 1 && T < (1LL << 31),
+            "embed_rmsnorm: bad shape T=%lld H=%lld V=%lld", (long long)T, (long long)H,
+            (long long)V);
+  if (T == 0) return LLMSERVE_OK;
+  LSH_CHECK(ids && embed && w && x && out, "embed_rmsnorm: null pointer");
+  lsh::launch(rmsnorm_kernel<kNormGather>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
+              lsh::as_stream(stream), true, x, embed, ids, V, w, out, H, eps);
+  return lsh::launch_status("embed_rmsnorm");
 }
 
 extern "C" int llmserve_silu_mul(const float* gate_up, float* out, int64_t T, int64_t I,

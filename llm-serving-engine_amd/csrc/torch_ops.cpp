@@ -232,6 +232,26 @@ at::Tensor rmsnorm(const at::Tensor& x, const at::Tensor& w, double eps) {
   return out;
 }
 
+std::tuple<at::Tensor, at::Tensor> embed_rmsnorm(const at::Tensor& ids, const at::Tensor& embed,
+                                                 const at::Tensor& w, double eps) {
+  check_f32(embed, "embed");
+  check_f32(w, "w");
+  TORCH_CHECK(ids.scalar_type() == at::kLong && ids.is_contiguous() && ids.dim() == 1,
+              "embed_rmsnorm: ids must be a contiguous int64 [T] tensor");
+  check_device(embed, {&ids, &w}, "embed_rmsnorm");
+  TORCH_CHECK(embed.dim() == 2, "embed_rmsnorm: embed must be [V, H]");
+  const int64_t T = ids.numel(), V = embed.size(0), H = embed.size(1);
+  TORCH_CHECK(w.numel() == H, "embed_rmsnorm: weight must have H entries");
+  const c10::DeviceGuard guard(embed.device());
+  auto x = at::empty({T, H}, embed.options());
+  auto out = at::empty({T, H}, embed.options());
+  check_status(llmserve_embed_rmsnorm(ids.data_ptr<int64_t>(), embed.data_ptr<float>(), V,
+                                      w.data_ptr<float>(), x.data_ptr<float>(),
+                                      out.data_ptr<float>(), T, H, static_cast<float>(eps),
+                                      stream_of(embed)));
+  return {x, out};
+}
+
 at::Tensor add_rmsnorm_(at::Tensor& x, const at::Tensor& r, const at::Tensor& w, double eps) {
   check_f32(x, "x");
   check_f32(r, "r");
@@ -423,6 +443,7 @@ TORCH_LIBRARY(llmserve_hip, m) {
         " Tensor? inv_act_scale=None) -> Tensor");
   m.def("rmsnorm(Tensor x, Tensor w, float eps) -> Tensor");
   m.def("add_rmsnorm_(Tensor(a!) x, Tensor r, Tensor w, float eps) -> Tensor");
+  m.def("embed_rmsnorm(Tensor ids, Tensor embed, Tensor w, float eps) -> (Tensor, Tensor)");
   m.def("silu_mul(Tensor gate_up) -> Tensor");
   m.def("rope_qk_(Tensor(a!) qkv, Tensor cos, Tensor sin, int n_q, int n_k, int head_dim,"
         " Tensor? q_w=None, Tensor? k_w=None, float eps=1e-6) -> ()");
@@ -446,6 +467,7 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("int4_linear", &int4_linear);
   m.impl("rmsnorm", &rmsnorm);
   m.impl("add_rmsnorm_", &add_rmsnorm_);
+  m.impl("embed_rmsnorm", &embed_rmsnorm);
   m.impl("silu_mul", &silu_mul);
   m.impl("rope_qk_", &rope_qk_);
   m.impl("decode_qkv_kv", &decode_qkv_kv);

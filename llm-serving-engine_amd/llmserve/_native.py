@@ -57,6 +57,7 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
     "llmserve_int8_linear_prefill": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P]),
     "llmserve_rmsnorm": (_I32, [_P, _P, _P, _I64, _I64, _F32, _P]),
     "llmserve_add_rmsnorm": (_I32, [_P, _P, _P, _P, _I64, _I64, _F32, _P]),
+    "llmserve_embed_rmsnorm": (_I32, [_P, _P, _I64, _P, _P, _P, _I64, _I64, _F32, _P]),
     "llmserve_silu_mul": (_I32, [_P, _P, _I64, _I64, _P]),
     "llmserve_rope_qk": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _F32, _P]),
     "llmserve_decode_qkv_kv": (

@@ -17,7 +17,8 @@ objects expose the reference's function names and signatures:
 
 * ``load_fused_ops()``: ``rmsnorm(x, w, eps)``, ``add_rmsnorm_(x, r, w, eps)``,
   ``silu_mul(gate_up)`` and ``rope_qk_(qkv, cos, sin, n_q, n_k, head_dim, q_w=None, k_w=None,
-  eps=1e-6)`` (fused_ops.cpp:129-137), plus the decode-step glue ``decode_qkv_kv`` (q/k norm,
+  eps=1e-6)`` (fused_ops.cpp:129-137), plus the decode-step glue ``embed_rmsnorm(ids, embed,
+  w, eps) -> (x, h)`` (embedding lookup + first input norm), ``decode_qkv_kv`` (q/k norm,
   RoPE and the int8 KV-cache write in one launch) and ``argmax_advance`` (greedy next token).
 
 The fp32-KV decode variants (``paged_attention_decode``, ``paged_attention_decode_v1``,
@@ -69,6 +70,7 @@ def load_fused_ops() -> SimpleNamespace:
     return SimpleNamespace(
         rmsnorm=o.rmsnorm,
         add_rmsnorm_=o.add_rmsnorm_,
+        embed_rmsnorm=o.embed_rmsnorm,
         silu_mul=o.silu_mul,
         rope_qk_=o.rope_qk_,
         decode_qkv_kv=o.decode_qkv_kv,

@@ -1,0 +1,190 @@
+"""Quantized decoder-only model (Llama / Qwen3 layout) for the decode step on MI355X.
+
+Mirrors the reference's ``CausalLM`` (src/llmserve/models/transformer.py:106-193) with the
+linears swapped for ``Int4Linear`` (``quantize_model(method="int4-awq")``, quant.py:173-205)
+and the fused forward of ``_forward_fused`` (transformer.py:144-190), restricted to a batch of
+decode tokens over an int8 paged KV cache. Every op runs as a HIP kernel of this package:
+
+  embed_rmsnorm                      embedding row + layer 0's input norm (:151-155)
+  per layer:
+    qkv_proj                         Int4Linear (GEMV for <= 16 rows, matrix cores above)
+    decode_qkv_kv                    q/k RMSNorm + RoPE at position ctx - 1 + k / smooth +
+                                     int8 quantize-write of K and V (:157-171, attention.py:241-246)
+    paged_attention_decode_int8      split-context int8 decode, q * q_mult fused (attention.py:263-273)
+    o_proj, add_rmsnorm_             (:183-184)
+    gate_up_proj, silu_mul, down_proj, add_rmsnorm_ with the next norm   (:185-189)
+  lm_head                            fp32 [V, H] matrix (hipBLASLt) or Int4Linear (quantize_lm_head)
+
+Weights are seeded random (N(0, 0.02) linears and embedding, norms 1 + N(0, 0.1)); there are
+no checkpoints on this path. The AWQ per-input-channel scales are searched (the reference's
+``_search_awq_scale``) on synthetic calibration activations with 1% of channels scaled x20.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+
+from llmserve.kernels import load_fused_ops, load_paged_attention
+from llmserve.quant import Int4Linear, _search_awq_scale
+
+
+@dataclass
+class ModelConfig:
+    """The fields of the reference's ModelConfig (config.py:13-33) that the decode step uses;
+    defaults are Qwen3-0.6B."""
+
+    vocab_size: int = 151936
+    hidden_size: int = 1024
+    intermediate_size: int = 3072
+    num_hidden_layers: int = 28
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    max_position_embeddings: int = 40960
+    tie_word_embeddings: bool = True
+    qk_norm: bool = True
+    model_type: str = "qwen3"
+
+
+QWEN3_0_6B = ModelConfig()
+
+
+def rope_tables(head_dim: int, theta: float, max_positions: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos / sin [max_positions, head_dim] float32, built as RotaryEmbedding (models/layers.py:
+    51-63, no scaling): inv_freq = 1 / theta^(2i/D), emb = [t * inv_freq, t * inv_freq] in
+    float64, rounded to float32. Built once on the host at load time."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim))
+    t = torch.arange(max_positions, dtype=torch.float64)
+    freqs = torch.outer(t, inv_freq)
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().float(), emb.sin().float()
+
+
+class DecoderLayer(nn.Module):
+    """One layer's weights: fp32 norms (buffers) and four Int4Linear submodules."""
+
+    input_layernorm: torch.Tensor
+    post_attention_layernorm: torch.Tensor
+    q_norm: torch.Tensor | None
+    k_norm: torch.Tensor | None
+    qkv_proj: Int4Linear
+    o_proj: Int4Linear
+    gate_up_proj: Int4Linear
+    down_proj: Int4Linear
+
+
+class QuantCausalLM(nn.Module):
+    """Random-init int4-AWQ model with fp32 embedding and norms, on one ROCm device."""
+
+    def __init__(
+        self,
+        cfg: ModelConfig,
+        group_size: int = 128,
+        quantize_lm_head: bool = False,
+        awq: bool = True,
+        seed: int = 0,
+        device: torch.device | str = "cuda",
+        max_positions: int | None = None,
+        calib_rows: int = 64,
+    ) -> None:
+        super().__init__()
+        if cfg.num_attention_heads % cfg.num_key_value_heads:
+            raise ValueError("num_attention_heads must be a multiple of num_key_value_heads")
+        self.cfg = cfg
+        self.group_size = group_size
+        dev = torch.device(device)
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+        nq, nk, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+
+        def calib(n_in: int) -> torch.Tensor:
+            x = torch.randn(calib_rows, n_in, generator=g, device=dev)
+            out = torch.randperm(n_in, generator=g, device=dev)[: max(1, n_in // 100)]
+            x[:, out] *= 20
+            return x
+
+        def lin(n_out: int, n_in: int, w: torch.Tensor | None = None) -> Int4Linear:
+            if w is None:
+                w = torch.randn(n_out, n_in, generator=g, device=dev) * 0.02
+            base = nn.Linear(n_in, n_out, bias=False, device="meta")
+            base.weight = nn.Parameter(w, requires_grad=False)
+            s = _search_awq_scale(w, calib(n_in), group_size) if awq else None
+            return Int4Linear(base, group_size, s, device=dev)
+
+        def norm(n: int) -> torch.Tensor:
+            return 1 + 0.1 * torch.randn(n, generator=g, device=dev)
+
+        self.layers = nn.ModuleList()
+        for _ in range(cfg.num_hidden_layers):
+            L = DecoderLayer()
+            L.register_buffer("input_layernorm", norm(H))
+            L.register_buffer("post_attention_layernorm", norm(H))
+            L.register_buffer("q_norm", norm(D) if cfg.qk_norm else None)
+            L.register_buffer("k_norm", norm(D) if cfg.qk_norm else None)
+            L.qkv_proj = lin((nq + 2 * nk) * D, H)
+            L.o_proj = lin(H, nq * D)
+            L.gate_up_proj = lin(2 * I, H)
+            L.down_proj = lin(H, I)
+            self.layers.append(L)
+        self.register_buffer("embed", torch.randn(V, H, generator=g, device=dev) * 0.02)
+        self.register_buffer("norm", norm(H))
+        if cfg.tie_word_embeddings:
+            lm_w = self.embed
+        else:
+            lm_w = torch.randn(V, H, generator=g, device=dev) * 0.02
+        self.lm_head: Int4Linear | None = lin(V, H, lm_w) if quantize_lm_head else None
+        self.register_buffer("lm_weight", None if quantize_lm_head else lm_w)
+        cos, sin = rope_tables(D, cfg.rope_theta, max_positions or min(cfg.max_position_embeddings, 32768))
+        self.register_buffer("rope_cos", cos.to(dev))
+        self.register_buffer("rope_sin", sin.to(dev))
+        self.scale = D ** -0.5
+
+    def forward_decode(self, ids: torch.Tensor, context_lens: torch.Tensor,
+                       block_tables: torch.Tensor, kv_layers, block_size: int) -> torch.Tensor:
+        """Final hidden states [B, H] of one decode token per sequence.
+
+        ``ids`` [B] int64; ``context_lens`` [B] int64 counts the token being decoded (its
+        position is ctx - 1); ``block_tables`` [B, max_blocks] int64 holds the blocks of every
+        position up to ctx - 1; ``kv_layers`` is ``KVCache.layers`` with int8 ``QuantizedKV``
+        pairs. Writes this token's K and V into the caches. No host synchronization."""
+        cfg = self.cfg
+        fo, pa = load_fused_ops(), load_paged_attention()
+        nq, nk, D, eps = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rms_norm_eps
+        B = ids.shape[0]
+        x, h = fo.embed_rmsnorm(ids, self.embed, self.layers[0].input_layernorm, eps)
+        n = len(self.layers)
+        for i, (L, (kc, vc)) in enumerate(zip(self.layers, kv_layers, strict=True)):
+            qkv = L.qkv_proj(h)
+            q = fo.decode_qkv_kv(qkv, self.rope_cos, self.rope_sin, context_lens, block_tables,
+                                 block_size, L.q_norm, L.k_norm, eps, kc.smooth, kc.data, vc.data,
+                                 kc.scale, vc.scale, nq, nk, D)
+            o = pa.paged_attention_decode_int8(q, kc.data, vc.data, kc.scale, vc.scale,
+                                               block_tables, context_lens, block_size,
+                                               self.scale, 0, kc._q_mult)
+            h = fo.add_rmsnorm_(x, L.o_proj(o.view(B, nq * D)), L.post_attention_layernorm, eps)
+            down = L.down_proj(fo.silu_mul(L.gate_up_proj(h)))
+            nxt = self.layers[i + 1].input_layernorm if i + 1 < n else self.norm
+            h = fo.add_rmsnorm_(x, down, nxt, eps)
+        return h
+
+    def compute_logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        """lm_head (transformer.py:192-193): fp32 [B, V]."""
+        if self.lm_head is not None:
+            return self.lm_head(hidden)
+        return torch.mm(hidden, self.lm_weight.t())
+
+    def weight_bytes(self) -> dict[str, int]:
+        """Bytes a decode step reads from the weights, by part."""
+        lin = sum(sum(b.numel() * b.element_size() for b in m.buffers())
+                  for L in self.layers for m in (L.qkv_proj, L.o_proj, L.gate_up_proj, L.down_proj))
+        if self.lm_head is not None:
+            lm = sum(b.numel() * b.element_size() for b in self.lm_head.buffers())
+        else:
+            lm = self.lm_weight.numel() * 4
+        return {"linears": lin, "lm_head": lm}

@@ -65,11 +65,11 @@ def rope_qk(qkv: np.ndarray, cos: np.ndarray, sin: np.ndarray, n_q: int, n_k: in
 
 
 def rope_tables(positions: np.ndarray, D: int, theta: float) -> tuple[np.ndarray, np.ndarray]:
-    """cos / sin rows [len(positions), D] of the rotate-half RoPE (the reference's
-    RotaryEmbedding without scaling, models/layers.py): inv_freq = theta^(-2i/D),
-    emb = [pos * inv_freq, pos * inv_freq]."""
-    inv = (1.0 / theta ** (np.arange(0, D, 2, dtype=np.float64) / D)).astype(F32)
-    f = np.asarray(positions, F32)[:, None] * inv[None, :]
+    """cos / sin rows [len(positions), D] of the rotate-half RoPE, built as the reference's
+    RotaryEmbedding without scaling (models/layers.py:51-63): inv_freq = 1 / theta^(2i/D) and
+    emb = [pos * inv_freq, pos * inv_freq] in float64, cos / sin rounded to float32."""
+    inv = 1.0 / theta ** (np.arange(0, D, 2, dtype=np.float64) / D)
+    f = np.asarray(positions, np.float64)[:, None] * inv[None, :]
     emb = np.concatenate([f, f], axis=-1)
     return np.cos(emb).astype(F32), np.sin(emb).astype(F32)
 
