@@ -20,7 +20,9 @@ stream the kernel runs on — the per-dispatch interval a kernel-trace profiler 
 sources) — or the oracle's C restatement where that build is absent — on the host cores, on
 the same quantized weights, for about 10 s.
 Extra fields report M = 4 / 16 steps and configs 1 (int8 GEMV), 3 (prefill int8 GEMM on the
-bf16 matrix cores, x conversion included) and 4 (int8-KV decode).
+bf16 matrix cores, x conversion included), 4 (int8-KV decode) and 5 (the full greedy decode
+step of a random-init int4-AWQ Qwen3-0.6B at batch 64 over the int8 KV cache, one HIP graph
+replay per step: tokens/s, with the fp32 and the int4 LM head, and per-op times).
 """
 
 from __future__ import annotations
@@ -276,7 +278,164 @@ def extra_configs(torch, dev) -> dict:
     us = kernel_avg_us(torch, launch, 40)
     out["c4_int8kv_paged_decode"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
                                      "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}
+    del copies
     return out
+
+
+def c5_decode(torch, dev, steps: int, warmup: int) -> dict:
+    """Config 5: greedy decode of 64 sequences through a random-init int4-AWQ Qwen3-0.6B (28
+    layers, g128, AWQ scales searched on synthetic activations) over an int8 KV cache with key
+    smoothing; contexts ~ U[1024, 4096], block tables a random permutation of the physical
+    blocks, cache contents random int8 with random scales (the state after a prefill). Each
+    step is one graph replay of the whole step (embedding to greedy token, context lengths
+    advanced on the device). tok/s = 64 x steps / wall time; also the same with the LM head
+    quantized (quantize_lm_head), and per-op times at the step's shapes."""
+    import numpy as np
+
+    from llmserve.kv_cache import KVCache
+    from llmserve.model_runner import DecodeRunner
+    from llmserve.quant import Int4Linear
+    from llmserve.transformer import QWEN3_0_6B, QuantCausalLM
+
+    cfg = QWEN3_0_6B
+    B, bs = 64, 16
+    nq, nk, D, H = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.hidden_size
+    rng = np.random.default_rng(55)
+    ctx = rng.integers(1024, 4097, B).astype(np.int64)
+    grow = 2 * (warmup + steps) + 4  # two runs (fp32 and int4 LM head) plus capture steps
+    nblk = -(-(ctx + grow) // bs)
+    width, total = int(nblk.max()), int(nblk.sum())
+    perm = rng.permutation(total)
+    bt = np.zeros((B, width), np.int64)
+    used = 0
+    for i, n in enumerate(nblk):
+        bt[i, :n] = perm[used:used + n]
+        used += n
+    t0 = time.perf_counter()
+    model = QuantCausalLM(cfg, GROUP, seed=5, device=dev)
+    lm4 = Int4Linear(nn_linear(torch, model.embed), GROUP, None, device=dev)
+    log(f"[bench] c5 model built in {time.perf_counter() - t0:.1f} s")
+    cache = KVCache(cfg, total, bs, device=dev, kv_dtype="int8")
+    g = torch.Generator(device=dev).manual_seed(56)
+    for k, v in cache.layers:
+        for t in (k, v):
+            t.data.random_(-127, 128, generator=g)
+            t.scale.uniform_(0.005, 0.05, generator=g)
+        s = torch.rand(nk, D, device=dev, generator=g) * 1.5 + 0.5
+        k.set_smoothing(s / s.mean(-1, keepdim=True), nq)
+    ids = torch.from_numpy(rng.integers(0, cfg.vocab_size, B)).to(dev)
+    runner = DecodeRunner(model, cache, ids, torch.from_numpy(ctx), torch.from_numpy(bt))
+    out = {"batch": B, "layers": cfg.num_hidden_layers, "context": "U[1024,4096]",
+           "kv_cache_GB": round(cache.nbytes() / 1e9, 2)}
+    for head in ("fp32", "int4"):
+        model.lm_head = lm4 if head == "int4" else None
+        runner.capture(keep_state=False)
+        for _ in range(warmup):
+            runner.replay()
+        torch.cuda.synchronize()
+        ctx0 = runner.context_lens.clone()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(steps):
+            runner.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        gpu_ms = e0.elapsed_time(e1)
+        ctx_mid = (ctx0.double() + (steps - 1) / 2).cpu().numpy()
+        kv_read = int(cfg.num_hidden_layers * nk * (2 * D + 8) * ctx_mid.sum())
+        lin = model.weight_bytes()["linears"]
+        lm = (sum(b.numel() * b.element_size() for b in lm4.buffers()) if head == "int4"
+              else model.embed.numel() * 4)
+        step_bytes = lin + lm + kv_read
+        ms = wall / steps * 1e3
+        out[f"lm_head_{head}"] = {
+            "tok_per_s": round(B * steps / wall, 1), "ms_per_step": round(ms, 4),
+            "gpu_ms_per_step": round(gpu_ms / steps, 4), "steps": steps,
+            "bytes_per_step": step_bytes, "kv_read_bytes": kv_read, "weight_bytes": lin + lm,
+            "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"[bench] c5 lm_head {head}: {out[f'lm_head_{head}']}")
+        runner.graph = None
+    model.lm_head = None
+    out["per_op"] = c5_per_op(torch, dev, model, lm4, cache, runner)
+    return out
+
+
+def nn_linear(torch, w):
+    """A bias-free nn.Linear view of an existing [out, in] weight (for Int4Linear)."""
+    lin = torch.nn.Linear(w.shape[1], w.shape[0], bias=False, device="meta")
+    lin.weight = torch.nn.Parameter(w, requires_grad=False)
+    return lin
+
+
+def c5_per_op(torch, dev, model, lm4, cache, runner) -> dict:
+    """Average time of each op of the config-5 step at its shapes (64 rows), launched
+    back to back over the 28 layers' distinct weights and caches, with its algorithmic bytes
+    (and flops for the linears) as fractions of the HBM and bf16-MFMA peaks."""
+    from llmserve.kernels import load_fused_ops, load_paged_attention
+
+    cfg = model.cfg
+    fo, pa = load_fused_ops(), load_paged_attention()
+    nq, nk, D, H, I = (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
+                       cfg.hidden_size, cfg.intermediate_size)
+    B, L, eps = runner.ids.numel(), cfg.num_hidden_layers, cfg.rms_norm_eps
+    g = torch.Generator(device=dev).manual_seed(57)
+    x = {K: torch.randn(B, K, device=dev, generator=g) for K in (H, nq * D, I)}
+    resid = torch.randn(B, H, device=dev, generator=g)
+    qkv = torch.randn(B, (nq + 2 * nk) * D, device=dev, generator=g)
+    gu = torch.randn(B, 2 * I, device=dev, generator=g)
+    q = torch.randn(B, nq, D, device=dev, generator=g)
+    logits = torch.randn(B, cfg.vocab_size, device=dev, generator=g)
+    ctx, bt, bs = runner.context_lens, runner.block_tables, runner.block_size
+    kv_read = int(nk * (2 * D + 8) * ctx.double().sum().item())
+    lay = model.layers
+
+    def lin_entry(name, attr, N, K):
+        def launch(i):
+            getattr(lay[i % L], attr)(x[K])
+        return name, launch, int4_bytes(N, K, B), 2.0 * B * N * K, L
+
+    def attn(i):
+        kc, vc = cache.layers[i % L]
+        pa.paged_attention_decode_int8(q, kc.data, vc.data, kc.scale, vc.scale, bt, ctx, bs,
+                                       D ** -0.5, 0, kc._q_mult)
+
+    def qkv_kv(i):
+        kc, vc = cache.layers[i % L]
+        fo.decode_qkv_kv(qkv, model.rope_cos, model.rope_sin, ctx, bt, bs, lay[i % L].q_norm,
+                         lay[i % L].k_norm, eps, kc.smooth, kc.data, vc.data, kc.scale, vc.scale,
+                         nq, nk, D)
+
+    ctx_save = ctx.clone()
+    entries = [
+        lin_entry("qkv_proj (int4, 1024->4096)", "qkv_proj", (nq + 2 * nk) * D, H),
+        ("decode_qkv_kv (norm + RoPE + KV write)", qkv_kv, 4 * B * (nq + 2 * nk) * D + 4 * B * nq * D
+         + 2 * B * nk * (D + 4), 0.0, L),
+        ("paged_attention_decode_int8", attn, kv_read + 8 * B * nq * D, 0.0, L),
+        lin_entry("o_proj (int4, 2048->1024)", "o_proj", H, nq * D),
+        ("add_rmsnorm_", lambda i: fo.add_rmsnorm_(resid, x[H], lay[i % L].input_layernorm, eps),
+         4 * B * H * 4, 0.0, L),
+        lin_entry("gate_up_proj (int4, 1024->6144)", "gate_up_proj", 2 * I, H),
+        ("silu_mul", lambda i: fo.silu_mul(gu), 4 * B * 3 * I, 0.0, L),
+        lin_entry("down_proj (int4, 3072->1024)", "down_proj", H, I),
+        ("lm_head fp32 (hipBLASLt)", lambda i: model.compute_logits(x[H]),
+         model.embed.numel() * 4 + 4 * B * (H + cfg.vocab_size), 2.0 * B * cfg.vocab_size * H, 1),
+        ("lm_head int4", lambda i: lm4(x[H]), int4_bytes(cfg.vocab_size, H, B),
+         2.0 * B * cfg.vocab_size * H, 1),
+        ("argmax_advance", lambda i: fo.argmax_advance(logits, ctx), 4 * B * cfg.vocab_size, 0.0, 1),
+    ]
+    res = {}
+    for name, launch, nbytes, flops, per_step in entries:
+        us = kernel_avg_us(torch, launch, 56 if per_step > 1 else 8)
+        r = {"us": round(us, 2), "per_step": per_step, "GBps": round(nbytes / us / 1e3, 1),
+             "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        if flops:
+            r["TFLOPs"] = round(flops / us / 1e6, 2)
+            r["mfma_frac"] = round(flops / us / 1e6 / MFMA_BF16_TFLOPS, 4)
+        res[name] = r
+    ctx.copy_(ctx_save)
+    return res
 
 
 def c4_inputs(torch, dev):
@@ -355,7 +514,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-extra", action="store_true", help="skip configs 1 and 4")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
     ap.add_argument("--only", choices=["gemv", "attention", "prefill", "copy"],
                     help="profiling run: only launch that kernel (64 times) and exit")
     args = ap.parse_args()
@@ -414,6 +573,8 @@ def main() -> int:
     log(f"[bench] roofline: {roofline}")
 
     extra = {} if args.no_extra else extra_configs(torch, dev)
+    if not args.no_extra:
+        extra["c5_decode_step"] = c5_decode(torch, dev, max(20, args.steps // 4), 5)
     if extra:
         log(f"[bench] extra: {extra}")
     cpu = None
