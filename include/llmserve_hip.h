@@ -131,6 +131,36 @@ int llmserve_int4_linear_gemm(const float* x, const float* inv_act_scale /* null
                               void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * The weights of llmserve_int4_linear_gemm_packed: nibbles, group scales and zeros of
+ * llmserve_int4_quantize rearranged once (per weight, at load time) into the order the
+ * matrix-core kernel reads them, so that each of its load instructions reads contiguous bytes
+ * (no counterpart in the reference, which keeps only the [N, K/2] buffers of Int4Linear,
+ * quant.py:109-121). The buffer holds llmserve_int4_gemm_pack_bytes(N, K, group_size) bytes:
+ * the nibbles of each 64-row slab and 128-channel block (rows past N zero), then per group,
+ * slab and row the scale and z - 8 * scale. Requires K and group_size multiples of 128;
+ * nibbles and the packed buffer 16-byte aligned.
+ */
+int64_t llmserve_int4_gemm_pack_bytes(int64_t N, int64_t K, int64_t group_size);
+int llmserve_int4_gemm_pack(const uint8_t* nibbles, const float* g_scale, const float* g_zero,
+                            int64_t N, int64_t K, int64_t group_size, void* packed,
+                            int64_t packed_bytes, void* stream);
+
+/*
+ * Int4Linear's batched path (replaces quant.py:141-142 like llmserve_int4_linear_gemm) on a
+ * packed weight: the same arithmetic (x' = x * inv_act_scale split into bf16 hi / lo, exact
+ * bf16 products, fp32 accumulation; within a few 1e-6 relative of fp32) with the decode-batch
+ * kernel, whose wavefronts issue all loads of their 1-3 K blocks before the first product.
+ * Any M, N >= 1; K and group_size multiples of 128. x, inv_act_scale and the packed weight
+ * 16-byte aligned; `workspace` (16-byte aligned) holds
+ * llmserve_int4_linear_gemm_packed_workspace_bytes(M, K) bytes.
+ */
+int64_t llmserve_int4_linear_gemm_packed_workspace_bytes(int64_t M, int64_t K);
+int llmserve_int4_linear_gemm_packed(const float* x, const float* inv_act_scale /* nullable */,
+                                     const void* packed, float* y, int64_t M, int64_t N,
+                                     int64_t K, int64_t group_size, void* workspace,
+                                     int64_t workspace_bytes, void* stream);
+
+/*
  * Prefill-sized int8 weight-only linear on the bf16 matrix cores (replaces Int8Linear's
  * large-M path, quant.py:71-72 with dequantize quant.py:78-79: x @ (q * scale[:, None]).T):
  *   y[m, n] = scale[n] * sum_k bf16(x[m, k]) * q[n, k]      (fp32 accumulate)

@@ -227,7 +227,252 @@ __global__ __launch_bounds__(256) void int4_gemm_mfma(Int4GemmArgs a) {
   }
 }
 
+// Packed operands of the decode-sized kernel (written once per weight by
+// llmserve_int4_gemm_pack, and per call by x_split_frag). Each is laid out in the order the
+// wavefronts read it, so that every load instruction of int4_gemm_lat reads contiguous bytes
+// (1 KB for a nibble tile or an x fragment) instead of 16 rows x 64 bytes:
+//  * nibbles: [slab][block][tile u][lane][16 bytes]; lane l of tile u holds row
+//    64 slab + 16 u + l % 16 (zero past N), bytes 64 b + 16 (l / 16) .. + 16 of that row;
+//  * scales:  [group][slab][fr][8 floats]: s of the rows 64 slab + 16 u + fr (u = 0..3), then
+//    z - 8 s of the same rows (the constant term of the group decomposition, rounded as the
+//    kernel would round it);
+//  * x:       [row tile][block][step q][hi, lo][lane][8 bf16]: lane (fr, fc) holds row
+//    16 t + fr (zero past M), channels 128 b + 32 fc + 8 q .. + 8, of xh and of xl.
+constexpr int kPkTile = kWave * 16;           // bytes of one nibble tile (4 per slab and block)
+constexpr int kPkFrag = kWave * 8;            // bf16 of one x fragment
+
+__host__ __device__ inline int64_t pk_slabs(int64_t N) { return (N + kCols - 1) / kCols; }
+inline int64_t pk_weight_bytes(int64_t N, int64_t K) { return pk_slabs(N) * (K / kBlk) * kNT * kPkTile; }
+inline int64_t pk_scale_floats(int64_t N, int64_t G) { return G * pk_slabs(N) * 16 * 8; }
+
+__global__ __launch_bounds__(256) void pack_nibbles_kernel(const uint8_t* __restrict__ nib,
+                                                           uint8_t* __restrict__ out, int N, int K,
+                                                           int64_t pieces) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= pieces) return;
+  const int nblk = K / kBlk;
+  const int lane = static_cast<int>(i % kWave);
+  const int u = static_cast<int>((i / kWave) % kNT);
+  const int64_t sb = i / (kWave * kNT);  // slab * nblk + b
+  const int b = static_cast<int>(sb % nblk);
+  const int64_t slab = sb / nblk;
+  const int64_t n = slab * kCols + 16 * u + lane % 16;
+  u32x4 v = u32x4{0u, 0u, 0u, 0u};
+  if (n < N)
+    v = *reinterpret_cast<const u32x4*>(nib + n * (K / 2) + 64 * b + 16 * (lane / 16));
+  *reinterpret_cast<u32x4*>(out + i * 16) = v;
+}
+
+__global__ __launch_bounds__(256) void pack_scales_kernel(const float* __restrict__ gs,
+                                                          const float* __restrict__ gz,
+                                                          float* __restrict__ out, int N, int G,
+                                                          int64_t items) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // (g, slab, fr, u)
+  if (i >= items) return;
+  const int u = static_cast<int>(i % kNT);
+  const int fr = static_cast<int>((i / kNT) % 16);
+  const int64_t gslab = i / (kNT * 16);
+  const int64_t slabs = pk_slabs(N);
+  const int64_t slab = gslab % slabs, g = gslab / slabs;
+  const int64_t n = slab * kCols + 16 * u + fr;
+  float sc = 0.f, zz = 0.f;
+  if (n < N) {
+    sc = gs[n * G + g];
+    zz = gz[n * G + g] - 8.f * sc;
+  }
+  float* o = out + (gslab * 16 + fr) * 8;
+  o[u] = sc;
+  o[4 + u] = zz;
+}
+
+// x' = x * inv split into bf16 hi / lo fragments (packed layout above) and xsum[b, m]. One
+// workgroup per (row tile, block), wavefront q writing step q; rows past M are zeros. The
+// channel sums add the 8 values of a lane, then the 4 lanes of a row, then the 4 steps
+// (fixed order).
+__global__ __launch_bounds__(4 * kWave) void x_split_frag_kernel(
+    const float* __restrict__ x, const float* __restrict__ inv, __bf16* __restrict__ xf,
+    float* __restrict__ xsum, int M, int K, int mp) {
+  __shared__ float part[4][16];
+  const int nblk = K / kBlk;
+  const int t = blockIdx.x / nblk, b = blockIdx.x % nblk;
+  const int q = threadIdx.x / kWave, lane = threadIdx.x % kWave, fr = lane % 16, fc = lane / 16;
+  const int m = 16 * t + fr;
+  const int c = kBlk * b + 32 * fc + 8 * q;
+  float v[8];
+  if (m < M) {
+    const f32x4 a0 = *reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(m) * K + c);
+    const f32x4 a1 = *reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(m) * K + c + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = a0[e];
+      v[4 + e] = a1[e];
+    }
+    if (inv) {
+      const f32x4 i0 = *reinterpret_cast<const f32x4*>(inv + c);
+      const f32x4 i1 = *reinterpret_cast<const f32x4*>(inv + c + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = __fmul_rn(v[e], i0[e]);
+        v[4 + e] = __fmul_rn(v[4 + e], i1[e]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.f;
+  }
+  bf16x8 hi, lo;
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    hi[e] = static_cast<__bf16>(v[e]);
+    lo[e] = static_cast<__bf16>(v[e] - static_cast<float>(hi[e]));
+    s += v[e];
+  }
+  __bf16* f = xf + ((((static_cast<int64_t>(t) * nblk + b) * 4 + q) * 2) * kWave + lane) * 8;
+  *reinterpret_cast<bf16x8*>(f) = hi;
+  *reinterpret_cast<bf16x8*>(f + kPkFrag) = lo;
+  s += __shfl_xor(s, 16, kWave);
+  s += __shfl_xor(s, 32, kWave);
+  if (fc == 0) part[q][fr] = s;
+  __syncthreads();
+  if (threadIdx.x < 16)
+    xsum[static_cast<int64_t>(b) * mp + 16 * t + threadIdx.x] =
+        (part[0][threadIdx.x] + part[1][threadIdx.x]) + (part[2][threadIdx.x] + part[3][threadIdx.x]);
+}
+
+// Decode-sized batches (up to a few 16-row tiles). The time goes to each CU's memory
+// requests, not to bandwidth or matrix-core throughput: int4_gemm_lat gives a wavefront
+// only KB <= 3 blocks of K per round (one round up to K = 3072), issues every load of them
+// (nibbles, x fragments, channel sums, group scales and zeros) before the first use, and
+// lets S wavefronts of a workgroup split the K blocks of one 16 x 64 slab; their partial sums meet in LDS and each output tile is
+// finished by one wavefront adding the S partials in a fixed order (deterministic).
+// Workgroups are numbered so that the row tiles of one slab run on the same XCD: the slab's
+// nibbles come from HBM into that XCD's L2 once. Operands are the packed ones (a.w, a.s and
+// a.xh as above; a.z and a.xl are unused).
+template <int KB, int S>
+__global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int slabs_pad, int mtiles) {
+  extern __shared__ f32x4 red[];  // S > 1: [S][kNT][64]
+  const int lane = threadIdx.x % kWave, ks = threadIdx.x / kWave;
+  const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+  const int t = j % mtiles;
+  const int slab = (j / mtiles) * 8 + xcd;
+  const int n0 = slab * kCols, m0 = t * kRows;
+  if (n0 >= a.N) return;  // padding workgroup (whole workgroup: no barrier is reached)
+  const int fr = lane % 16, fc = lane / 16;
+  const int nblk = a.K / kBlk;
+  const int slabs = (a.N + kCols - 1) / kCols;
+
+  f32x4 acc[kNT];
+#pragma unroll
+  for (int u = 0; u < kNT; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Rounds of S x KB blocks (one round up to K = 3072 at S = 8, KB = 3).
+  for (int base = 0; base < nblk; base += S * KB) {
+    u32x4 w[KB][kNT], xh[KB][4], xl[KB][4];
+    f32x4 xs[KB];
+    float sc[KB][kNT], zc[KB][kNT];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int b = min(base + ks * KB + kb, nblk - 1);  // clamped: loads stay unconditional
+      const int g = b / a.bpg;
+      const uint8_t* wt = a.w + ((static_cast<int64_t>(slab) * nblk + b) * kNT) * kPkTile + 16 * lane;
+#pragma unroll
+      for (int u = 0; u < kNT; ++u)
+        w[kb][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wt + u * kPkTile));
+      const __bf16* xt = a.xh + ((static_cast<int64_t>(t) * nblk + b) * 8) * kPkFrag + 8 * lane;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        xh[kb][q] = *reinterpret_cast<const u32x4*>(xt + (2 * q) * kPkFrag);
+        xl[kb][q] = *reinterpret_cast<const u32x4*>(xt + (2 * q + 1) * kPkFrag);
+      }
+      const float* st = a.s + ((static_cast<int64_t>(g) * slabs + slab) * 16 + fr) * 8;
+      const f32x4 s4 = *reinterpret_cast<const f32x4*>(st);
+      const f32x4 z4 = *reinterpret_cast<const f32x4*>(st + 4);  // z - 8 s
+#pragma unroll
+      for (int u = 0; u < kNT; ++u) {
+        sc[kb][u] = s4[u];
+        zc[kb][u] = z4[u];
+      }
+      xs[kb] = *reinterpret_cast<const f32x4*>(a.xsum + static_cast<int64_t>(b) * a.mp + m0 + 4 * fc);
+    }
+    // all loads above are issued before any of the products below (the scheduler would
+    // otherwise interleave them, turning one memory round trip into several)
+    __builtin_amdgcn_sched_barrier(0);
+    // Blocks past the end (when S x KB does not divide nblk) were loaded clamped and are
+    // weighted by 0: no branch, so that the compiler keeps every load ahead of the first use.
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const float on = base + ks * KB + kb < nblk ? 1.f : 0.f;
+#pragma unroll
+      for (int u = 0; u < kNT; ++u) {
+        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const bf16x8 bq = nibbles_bf16(w[kb][u][q]);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xh[kb][q]), bq, d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xl[kb][q]), bq, d, 0, 0, 0);
+        }
+        const float s1 = on * sc[kb][u];
+        const float zz = on * zc[kb][u];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[u][r] += s1 * d[r] + zz * xs[kb][r];
+      }
+    }
+  }
+
+  if constexpr (S > 1) {
+#pragma unroll
+    for (int u = 0; u < kNT; ++u) red[(ks * kNT + u) * kWave + lane] = acc[u];
+    __syncthreads();
+  }
+  // wavefront ks finishes the tiles u = ks, ks + S, ...
+#pragma unroll
+  for (int u = 0; u < kNT; ++u) {
+    const bool mine = S == 1 || (S <= kNT ? u % S == ks : u == ks);
+    if (!mine) continue;
+    f32x4 v = acc[u];
+    if constexpr (S > 1) {
+      v = red[u * kWave + lane];
+#pragma unroll
+      for (int k = 1; k < S; ++k) v += red[(k * kNT + u) * kWave + lane];
+    }
+    const int n = n0 + 16 * u + fr;
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 4 * fc + r;
+      if (m < a.M) a.y[static_cast<int64_t>(m) * a.N + n] = v[r];
+    }
+  }
+}
+
 int64_t xsum_rows(int64_t M) { return (M + kRows - 1) / kRows * kRows; }
+
+template <int KB, int S>
+void launch_lat_ks(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, hipStream_t st) {
+  const int64_t slabs_pad = (slabs + 7) / 8 * 8;
+  const dim3 grid(static_cast<unsigned>(slabs_pad * mtiles)), block(S * kWave);
+  const size_t lds = S > 1 ? static_cast<size_t>(S) * kNT * kWave * sizeof(f32x4) : 0;
+  lsh::launch(int4_gemm_lat<KB, S>, grid, block, lds, st, true, a,
+              static_cast<int>(slabs_pad), static_cast<int>(mtiles));
+}
+
+// Blocks per wavefront and round KB = ceil(nb / 8) (at most 3), then the fewest of 1, 2, 4, 8
+// wavefronts that cover the nb blocks (8 when more than one round is needed).
+void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb, hipStream_t st) {
+  int KB = std::min(3, (nb + 7) / 8);
+  int S = 1;
+  while (S < 8 && S * KB < nb) S *= 2;
+  // very large outputs (an LM head) fill the GPU anyway: fewer, longer wavefronts
+  if (KB == 1 && S == 8 && slabs * mtiles * S > 16384) {
+    KB = 2;
+    S = 4;
+  }
+#define LSH_LAT(kb, s) \
+  if (KB == kb && S == s) return launch_lat_ks<kb, s>(a, slabs, mtiles, st);
+  LSH_LAT(1, 1) LSH_LAT(1, 2) LSH_LAT(1, 4) LSH_LAT(1, 8)
+  LSH_LAT(2, 4) LSH_LAT(2, 8) LSH_LAT(3, 8)
+#undef LSH_LAT
+}
 
 }  // namespace
 
@@ -271,8 +516,8 @@ extern "C" int llmserve_int4_linear_gemm(const float* x, const float* inv_act_sc
   Int4GemmArgs a{xh, xl, xsum, nibbles, g_scale, g_zero, y, static_cast<int>(M),
                  static_cast<int>(N), static_cast<int>(K), static_cast<int>(K / group_size),
                  static_cast<int>(group_size / kBlk), mp};
-  // K split: the smallest S (1, 2, 4) that gives >= 768 wavefronts, with >= 2 blocks each
   const int64_t slabs = (N + kCols - 1) / kCols, mtiles = (M + kRows - 1) / kRows;
+  // K split: the smallest S (1, 2, 4) that gives >= 768 wavefronts, with >= 2 blocks each
   int S = 1;
   while (S < kSplitWaves && slabs * mtiles * S < 768 && nb >= 2 * (2 * S)) S *= 2;
   const int R = 4 / S;  // slabs per workgroup
@@ -285,4 +530,81 @@ extern "C" int llmserve_int4_linear_gemm(const float* x, const float* inv_act_sc
     default: lsh::launch(int4_gemm_mfma<1>, grid, block, lds, st, true, a); break;
   }
   return lsh::launch_status("int4_linear_gemm");
+}
+
+extern "C" int64_t llmserve_int4_gemm_pack_bytes(int64_t N, int64_t K, int64_t group_size) {
+  if (N <= 0 || K <= 0 || group_size <= 0 || K % kBlk || K % group_size) return 0;
+  const int64_t w = (pk_weight_bytes(N, K) + 255) / 256 * 256;
+  return w + pk_scale_floats(N, K / group_size) * 4;
+}
+
+extern "C" int llmserve_int4_gemm_pack(const uint8_t* nibbles, const float* g_scale,
+                                       const float* g_zero, int64_t N, int64_t K,
+                                       int64_t group_size, void* packed, int64_t packed_bytes,
+                                       void* stream) {
+  LSH_CHECK(N >= 1 && K >= 1 && group_size >= 2 && N < (1LL << 31) && K < (1LL << 31),
+            "int4_gemm_pack: bad shape");
+  LSH_CHECK(K % kBlk == 0 && group_size % kBlk == 0 && K % group_size == 0,
+            "int4_gemm_pack: K and group_size must be multiples of 128 (K %% group == 0)");
+  LSH_CHECK(nibbles && g_scale && g_zero && packed, "int4_gemm_pack: null pointer");
+  LSH_CHECK(lsh::aligned16(nibbles) && lsh::aligned16(packed),
+            "int4_gemm_pack: nibbles and the packed buffer must be 16-byte aligned");
+  const int64_t need = llmserve_int4_gemm_pack_bytes(N, K, group_size);
+  LSH_CHECK(packed_bytes >= need, "int4_gemm_pack: %lld bytes needed, %lld given",
+            (long long)need, (long long)packed_bytes);
+  hipStream_t st = lsh::as_stream(stream);
+  uint8_t* wpk = static_cast<uint8_t*>(packed);
+  float* spk = reinterpret_cast<float*>(wpk + (pk_weight_bytes(N, K) + 255) / 256 * 256);
+  const int64_t pieces = pk_weight_bytes(N, K) / 16;
+  lsh::launch(pack_nibbles_kernel, dim3(static_cast<unsigned>((pieces + 255) / 256)), dim3(256), 0,
+              st, false, nibbles, wpk, static_cast<int>(N), static_cast<int>(K), pieces);
+  const int64_t G = K / group_size;
+  const int64_t items = pk_scale_floats(N, G) / 2;
+  lsh::launch(pack_scales_kernel, dim3(static_cast<unsigned>((items + 255) / 256)), dim3(256), 0,
+              st, true, g_scale, g_zero, spk, static_cast<int>(N), static_cast<int>(G), items);
+  return lsh::launch_status("int4_gemm_pack");
+}
+
+extern "C" int64_t llmserve_int4_linear_gemm_packed_workspace_bytes(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0) return 0;
+  return xsum_rows(M) * K * 4 + (K / kBlk) * xsum_rows(M) * 4;
+}
+
+extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv_act_scale,
+                                                const void* packed, float* y, int64_t M,
+                                                int64_t N, int64_t K, int64_t group_size,
+                                                void* workspace, int64_t workspace_bytes,
+                                                void* stream) {
+  LSH_CHECK(M >= 0 && N >= 1 && K >= 1 && group_size >= 2, "int4_linear_gemm_packed: bad shape");
+  LSH_CHECK(K % kBlk == 0 && group_size % kBlk == 0 && K % group_size == 0,
+            "int4_linear_gemm_packed: K and group_size must be multiples of 128 (K %% group == 0)");
+  LSH_CHECK(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31) && M * K < (1LL << 40) &&
+                N * K < (1LL << 41),
+            "int4_linear_gemm_packed: shape too large");
+  if (M == 0) return LLMSERVE_OK;
+  LSH_CHECK(x && packed && y, "int4_linear_gemm_packed: null pointer");
+  LSH_CHECK(lsh::aligned16(x) && lsh::aligned16(packed) &&
+                (inv_act_scale == nullptr || lsh::aligned16(inv_act_scale)),
+            "int4_linear_gemm_packed: x, inv_act_scale and the packed weight must be 16-byte "
+            "aligned");
+  const int64_t need = llmserve_int4_linear_gemm_packed_workspace_bytes(M, K);
+  LSH_CHECK(workspace != nullptr && workspace_bytes >= need && lsh::aligned16(workspace),
+            "int4_linear_gemm_packed: a 16-byte aligned workspace of %lld bytes is needed "
+            "(%lld given)",
+            (long long)need, (long long)workspace_bytes);
+  hipStream_t st = lsh::as_stream(stream);
+  const int nb = static_cast<int>(K / kBlk);
+  const int64_t mtiles = (M + kRows - 1) / kRows;
+  const int mp = static_cast<int>(xsum_rows(M));
+  __bf16* xf = static_cast<__bf16*>(workspace);
+  float* xsum = reinterpret_cast<float*>(xf + 2 * static_cast<int64_t>(mp) * K);
+  lsh::launch(x_split_frag_kernel, dim3(static_cast<unsigned>(mtiles * nb)), dim3(4 * kWave), 0, st,
+              false, x, inv_act_scale, xf, xsum, static_cast<int>(M), static_cast<int>(K), mp);
+  const uint8_t* wpk = static_cast<const uint8_t*>(packed);
+  const float* spk = reinterpret_cast<const float*>(wpk + (pk_weight_bytes(N, K) + 255) / 256 * 256);
+  Int4GemmArgs a{xf, nullptr, xsum, wpk, spk, nullptr, y, static_cast<int>(M),
+                 static_cast<int>(N), static_cast<int>(K), static_cast<int>(K / group_size),
+                 static_cast<int>(group_size / kBlk), mp};
+  launch_lat(a, pk_slabs(N), mtiles, nb, st);
+  return lsh::launch_status("int4_linear_gemm_packed");
 }

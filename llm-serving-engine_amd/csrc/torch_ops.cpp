@@ -212,6 +212,57 @@ at::Tensor int4_linear_gemm(const at::Tensor& x, const at::Tensor& nibbles, cons
   return y;
 }
 
+at::Tensor int4_gemm_pack(const at::Tensor& nibbles, const at::Tensor& scale,
+                          const at::Tensor& zero, int64_t group_size) {
+  TORCH_CHECK(nibbles.scalar_type() == at::kByte && scale.scalar_type() == at::kFloat &&
+                  zero.scalar_type() == at::kFloat,
+              "int4_gemm_pack: uint8 nibbles, float32 scale / zero");
+  TORCH_CHECK(nibbles.is_contiguous() && scale.is_contiguous() && zero.is_contiguous() &&
+                  nibbles.dim() == 2,
+              "int4_gemm_pack: contiguous [N, K/2] nibbles and [N, G] scale / zero");
+  check_device(nibbles, {&scale, &zero}, "int4_gemm_pack");
+  const int64_t N = nibbles.size(0), K = nibbles.size(1) * 2;
+  TORCH_CHECK(group_size > 0 && K % group_size == 0 && scale.numel() == N * (K / group_size) &&
+                  zero.numel() == scale.numel(),
+              "int4_gemm_pack: scale / zero must be [N, K / group_size]");
+  const c10::DeviceGuard guard(nibbles.device());
+  const int64_t bytes = llmserve_int4_gemm_pack_bytes(N, K, group_size);
+  TORCH_CHECK(bytes > 0, "int4_gemm_pack: K and group_size must be multiples of 128");
+  auto packed = at::empty({bytes}, nibbles.options());
+  check_status(llmserve_int4_gemm_pack(nibbles.data_ptr<uint8_t>(), scale.data_ptr<float>(),
+                                       zero.data_ptr<float>(), N, K, group_size, packed.data_ptr(),
+                                       bytes, stream_of(nibbles)));
+  return packed;
+}
+
+at::Tensor int4_linear_gemm_packed(const at::Tensor& x, const at::Tensor& packed, int64_t N,
+                                   int64_t group_size,
+                                   const std::optional<at::Tensor>& inv_act_scale) {
+  TORCH_CHECK(x.scalar_type() == at::kFloat && x.is_contiguous() && x.dim() == 2,
+              "int4_linear_gemm_packed: contiguous float32 [M, K] x");
+  TORCH_CHECK(packed.scalar_type() == at::kByte && packed.is_contiguous(),
+              "int4_linear_gemm_packed: packed must come from int4_gemm_pack");
+  check_device(x, {&packed}, "int4_linear_gemm_packed");
+  const int64_t M = x.size(0), K = x.size(1);
+  TORCH_CHECK(packed.numel() == llmserve_int4_gemm_pack_bytes(N, K, group_size),
+              "int4_linear_gemm_packed: packed buffer does not match N, K, group_size");
+  if (inv_act_scale.has_value()) {
+    check_device(x, {&*inv_act_scale}, "int4_linear_gemm_packed");
+    TORCH_CHECK(inv_act_scale->scalar_type() == at::kFloat && inv_act_scale->is_contiguous() &&
+                    inv_act_scale->numel() == K,
+                "int4_linear_gemm_packed: inv_act_scale must be a contiguous float32 [K] tensor");
+  }
+  const c10::DeviceGuard guard(x.device());
+  auto y = at::empty({M, N}, x.options());
+  const int64_t ws_bytes = llmserve_int4_linear_gemm_packed_workspace_bytes(M, K);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({(ws_bytes + 15) / 16 * 4}, x.options());
+  check_status(llmserve_int4_linear_gemm_packed(
+      x.data_ptr<float>(), opt_ptr<float>(inv_act_scale), packed.data_ptr(), y.data_ptr<float>(),
+      M, N, K, group_size, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(x)));
+  return y;
+}
+
 // ---- decoder-layer elementwise ops (fused_ops.cpp:39-127) and decode glue --------------------
 
 void check_f32(const at::Tensor& t, const char* name) {
@@ -441,6 +492,9 @@ TORCH_LIBRARY(llmserve_hip, m) {
         " Tensor? inv_act_scale=None) -> Tensor");
   m.def("int4_linear_gemm(Tensor x, Tensor nibbles, Tensor scale, Tensor zero, int group_size,"
         " Tensor? inv_act_scale=None) -> Tensor");
+  m.def("int4_gemm_pack(Tensor nibbles, Tensor scale, Tensor zero, int group_size) -> Tensor");
+  m.def("int4_linear_gemm_packed(Tensor x, Tensor packed, int out_features, int group_size,"
+        " Tensor? inv_act_scale=None) -> Tensor");
   m.def("rmsnorm(Tensor x, Tensor w, float eps) -> Tensor");
   m.def("add_rmsnorm_(Tensor(a!) x, Tensor r, Tensor w, float eps) -> Tensor");
   m.def("embed_rmsnorm(Tensor ids, Tensor embed, Tensor w, float eps) -> (Tensor, Tensor)");
@@ -464,6 +518,8 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("int8_linear", &int8_linear);
   m.impl("int8_linear_prefill", &int8_linear_prefill);
   m.impl("int4_linear_gemm", &int4_linear_gemm);
+  m.impl("int4_gemm_pack", &int4_gemm_pack);
+  m.impl("int4_linear_gemm_packed", &int4_linear_gemm_packed);
   m.impl("int4_linear", &int4_linear);
   m.impl("rmsnorm", &rmsnorm);
   m.impl("add_rmsnorm_", &add_rmsnorm_);

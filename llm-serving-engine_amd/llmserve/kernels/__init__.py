@@ -11,6 +11,9 @@ objects expose the reference's function names and signatures:
   ``int8_linear_prefill(x, qweight, scale)``: Int8Linear's large-M path on the bf16 matrix
   cores (quant.py:71-72), and ``int4_linear_gemm(x, nibbles, scale, zero, group_size,
   inv_act_scale=None)``: Int4Linear's large-M path (quant.py:141-142) on the matrix cores;
+  ``int4_gemm_pack(nibbles, scale, zero, group_size)`` rearranges an int4 weight once for
+  ``int4_linear_gemm_packed(x, packed, out_features, group_size, inv_act_scale=None)``, the
+  same product with the decode-batch matrix-core kernel;
 * ``load_paged_attention()``: ``paged_attention_decode_int8(q, k_cache, v_cache, k_scale,
   v_scale, block_tables, context_lens, block_size, scale, partition_size=0, q_mult=None)``
   (paged_attention.cpp:386-399; ``q_mult`` fuses the key-smoothing multiply of q).
@@ -42,7 +45,9 @@ def load_int8_gemv() -> SimpleNamespace:
     o = ops()
     return SimpleNamespace(int8_linear=o.int8_linear, int4_linear=o.int4_linear,
                            int8_linear_prefill=o.int8_linear_prefill,
-                           int4_linear_gemm=o.int4_linear_gemm)
+                           int4_linear_gemm=o.int4_linear_gemm,
+                           int4_gemm_pack=o.int4_gemm_pack,
+                           int4_linear_gemm_packed=o.int4_linear_gemm_packed)
 
 
 @functools.cache

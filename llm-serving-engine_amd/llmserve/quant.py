@@ -8,7 +8,7 @@ the current GPU when it is quantized.
 
 Kernel switches (class attributes, as in the reference, quant.py:35-37 and :123-124):
   Int8Linear.kernel: "auto" | "gemv" | "prefill" | "dequant" | "aten" | "w8a8"
-  Int4Linear.kernel: "auto" | "aten"
+  Int4Linear.kernel: "auto" | "gemv" | "gemm" | "gemm_ref" | "aten"
 "auto" runs the HIP GEMV up to ``gemv_max_rows`` activation rows and the bf16-MFMA prefill
 GEMM above. "dequant"/"aten" multiply by the dequantized weight with torch (the reference's
 exact large-M path, quant.py:71-72; there is no aten int8pack kernel for ROCm). "w8a8" keeps the
@@ -137,10 +137,12 @@ class Int4Linear(nn.Module):
     """
 
     max_fused_rows = 16  # above this: the large-M path (reference quant.py:123)
-    # "auto": the HIP GEMV up to max_fused_rows rows, above that the HIP matrix-core GEMM
-    # (int4_linear_gemm) where its shape rules hold (K and group multiples of 128, out
-    # multiple of 16), else dequantize + GEMM; "gemv" / "gemm" force one HIP kernel;
-    # "aten": dequantize + GEMM (the reference's large-M algorithm) for every batch
+    max_packed_rows = 256  # up to this: the decode-batch kernel on the packed weight
+    # "auto": the HIP GEMV up to max_fused_rows rows; above that the HIP matrix-core GEMM on
+    # the packed weight ("gemm", K and group multiples of 128) up to max_packed_rows rows, and
+    # the matrix-core GEMM on the reference layout ("gemm_ref", out also a multiple of 16)
+    # beyond; else dequantize + GEMM ("aten", the reference's large-M algorithm). Each name
+    # forces its kernel for every batch.
     kernel = "auto"
 
     def __init__(
@@ -168,6 +170,12 @@ class Int4Linear(nn.Module):
         self.register_buffer("nibbles", nib)  # [out, in/2]
         self.register_buffer("g_scale", g_scale)  # [out, n_groups]
         self.register_buffer("g_zero", g_zero)
+        # the same weight rearranged for the batched matrix-core kernel (not saved: it is a
+        # function of the three buffers above)
+        packed = None
+        if self.in_features % 128 == 0 and group_size % 128 == 0:
+            packed = load_int8_gemv().int4_gemm_pack(nib, g_scale, g_zero, group_size)
+        self.register_buffer("gemm_packed", packed, persistent=False)
         self.bias = (
             None if linear.bias is None else nn.Parameter(linear.bias.detach().to(dev).clone(), False)
         )
@@ -181,7 +189,7 @@ class Int4Linear(nn.Module):
         return w.reshape(self.out_features, self.in_features)
 
     def gemm_ok(self) -> bool:
-        """Shapes the matrix-core large-M kernel takes."""
+        """Shapes the reference-layout matrix-core kernel (int4_linear_gemm) takes."""
         return (self.in_features % 128 == 0 and self.group_size % 128 == 0
                 and self.out_features % 16 == 0)
 
@@ -190,15 +198,27 @@ class Int4Linear(nn.Module):
         x2 = x.reshape(-1, shape[-1])
         rows = x2.shape[0]
         if self.kernel == "auto":
-            path = "gemv" if rows <= self.max_fused_rows else ("gemm" if self.gemm_ok() else "aten")
-        elif self.kernel in ("gemv", "gemm", "aten"):
+            if rows <= self.max_fused_rows:
+                path = "gemv"
+            elif self.gemm_packed is not None and (rows <= self.max_packed_rows or not self.gemm_ok()):
+                path = "gemm"
+            else:
+                path = "gemm_ref" if self.gemm_ok() else "aten"
+        elif self.kernel in ("gemv", "gemm", "gemm_ref", "aten"):
             path = self.kernel
         else:
             raise ValueError(f"unknown Int4Linear kernel {self.kernel!r}")
+        if path == "gemm" and self.gemm_packed is None:
+            raise ValueError("Int4Linear: the packed matrix-core kernel needs in_features and "
+                             "group_size multiples of 128")
         if path == "aten":
             if self.inv_act_scale is not None:
                 x2 = x2 * self.inv_act_scale
             y = x2 @ self.dequantize().t()
+        elif path == "gemm":
+            y = load_int8_gemv().int4_linear_gemm_packed(x2.contiguous(), self.gemm_packed,
+                                                         self.out_features, self.group_size,
+                                                         self.inv_act_scale)
         else:
             fn = load_int8_gemv().int4_linear if path == "gemv" else load_int8_gemv().int4_linear_gemm
             y = fn(x2.contiguous(), self.nibbles, self.g_scale, self.g_zero, self.group_size,

@@ -77,6 +77,27 @@ def int4_linear_gemm(x, nib, gs, gz, group, inv=None):
     return y
 
 
+def int4_gemm_pack(nib, gs, gz, group):
+    N, K = nib.shape[0], nib.shape[1] * 2
+    L = capi()
+    nbytes = L.llmserve_int4_gemm_pack_bytes(N, K, group)
+    packed = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=nib.device)
+    check(L.llmserve_int4_gemm_pack(_p(nib), _p(gs), _p(gz), N, K, group, _p(packed), nbytes,
+                                    _stream()))
+    return packed[:nbytes]
+
+
+def int4_linear_gemm_packed(x, packed, N, group, inv=None):
+    M, K = x.shape
+    y = torch.empty(M, N, dtype=torch.float32, device=x.device)
+    L = capi()
+    nbytes = L.llmserve_int4_linear_gemm_packed_workspace_bytes(M, K)
+    ws = torch.empty(max(nbytes, 16) // 4 + 4, dtype=torch.float32, device=x.device)
+    check(L.llmserve_int4_linear_gemm_packed(_p(x), _p(inv), _p(packed), _p(y), M, N, K, group,
+                                             _p(ws), nbytes, _stream()))
+    return y
+
+
 def int8_linear_prefill(x, q, s):
     M, K = x.shape
     N = q.shape[0]

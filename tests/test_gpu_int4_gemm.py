@@ -1,5 +1,7 @@
 """int4 weight-only linear for M > 16 on the matrix cores (Int4Linear's large-M branch,
-reference quant.py:141-142) through the C ABI, against the float64 oracle.
+reference quant.py:141-142) through the C ABI, against the float64 oracle: the kernel on the
+reference [N, K/2] layout and the decode-batch kernel on the packed weight, whose packing is
+checked byte for byte by unpacking it on the host.
 
 Tolerance: max-abs error <= 2e-5 * max|y| and rel-L2 <= 2e-5 against the float64 mathematics.
 x' = x * inv_act_scale is carried as two bf16 terms (xh + xl equals x' to 2^-18 relative) and
@@ -91,3 +93,102 @@ def test_int4linear_large_batch_uses_gemm(gpu):
     ref = q(x)
     err = (y - ref).abs().max().item() / ref.abs().max().item()
     assert err < 2e-5, err
+
+
+# ---- packed weight + decode-batch kernel ------------------------------------------------------
+
+def unpack(packed: np.ndarray, N: int, K: int, G: int):
+    """Inverse of llmserve_int4_gemm_pack, written from its documented layout."""
+    slabs, nblk = -(-N // 64), K // 128
+    wbytes = slabs * nblk * 4 * 1024
+    wpk = packed[:wbytes].reshape(slabs, nblk, 4, 64, 16)
+    nib = np.zeros((slabs * 64, K // 2), np.uint8)
+    for u in range(4):
+        for lane in range(64):
+            rows = np.arange(slabs) * 64 + 16 * u + lane % 16
+            for b in range(nblk):
+                c = 64 * b + 16 * (lane // 16)
+                nib[rows, c:c + 16] = wpk[:, b, u, lane]
+    off = -(-wbytes // 256) * 256
+    sz = packed[off:off + G * slabs * 16 * 8 * 4].view(np.float32).reshape(G, slabs, 16, 8)
+    s = np.zeros((slabs * 64, G), np.float32)
+    zz = np.zeros((slabs * 64, G), np.float32)
+    for u in range(4):
+        rows = np.arange(slabs)[:, None] * 64 + 16 * u + np.arange(16)[None, :]
+        s[rows.ravel()] = sz[:, :, :, u].transpose(1, 2, 0).reshape(-1, G)
+        zz[rows.ravel()] = sz[:, :, :, 4 + u].transpose(1, 2, 0).reshape(-1, G)
+    return nib, s, zz
+
+
+@pytest.mark.parametrize("N,K,g", [(4096, 1024, 128), (77, 256, 128), (1000, 1536, 256)])
+def test_pack_layout(gpu, N, K, g):
+    _, nib, gs, gz, _ = _case(4, N, K, g, N + K, awq=False)
+    packed = cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), g).cpu().numpy()
+    G = K // g
+    assert packed.size == cu.capi().llmserve_int4_gemm_pack_bytes(N, K, g)
+    pn, ps, pz = unpack(packed, N, K, G)
+    assert np.array_equal(pn[:N], nib) and not pn[N:].any()
+    assert np.array_equal(ps[:N], gs) and not ps[N:].any()
+    assert np.array_equal(pz[:N], (gz - F32(8) * gs).astype(F32)) and not pz[N:].any()
+
+
+@pytest.mark.parametrize("M", [17, 32, 64])
+@pytest.mark.parametrize("N,K", QWEN)
+def test_packed_gemm_qwen_shapes(gpu, M, N, K):
+    x, nib, gs, gz, inv = _case(M, N, K, 128, M * 37 + N + K)
+    packed = cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), 128)
+    y = cu.int4_linear_gemm_packed(cu.dev(x), packed, N, 128, cu.dev(inv))
+    cu.assert_rel_close(y, mr.int4_linear_f64(x, nib, gs, gz, 128, inv), TOL, f"M={M} {N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K,g", [(1, 32, 512, 128), (5, 77, 256, 128), (64, 1000, 1536, 256),
+                                     (33, 16, 128, 128), (100, 160, 4096, 128), (300, 72, 640, 128),
+                                     (64, 151936 // 8, 1024, 128), (48, 64, 3200, 640)])
+def test_packed_gemm_tails(gpu, M, N, K, g):
+    """Any N (packed slabs pad to 64 rows), K past one round of 24 blocks (4096, 3200),
+    groups of several blocks, row tails, a wide output, no AWQ scale on odd M."""
+    x, nib, gs, gz, inv = _case(M, N, K, g, M + N + K + g, awq=(M % 2 == 0))
+    packed = cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), g)
+    y = cu.int4_linear_gemm_packed(cu.dev(x), packed, N, g, None if inv is None else cu.dev(inv))
+    cu.assert_rel_close(y, mr.int4_linear_f64(x, nib, gs, gz, g, inv), TOL, f"M={M} {N}x{K} g{g}")
+
+
+def test_packed_gemm_rejects_bad_shapes(gpu):
+    x, nib, gs, gz, _ = _case(20, 48, 256, 64, 3, awq=False)
+    with pytest.raises(RuntimeError, match="multiples of 128"):
+        cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), 64)
+    x, nib, gs, gz, _ = _case(20, 48, 256, 128, 3, awq=False)
+    packed = cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), 128)
+    with pytest.raises(RuntimeError, match="workspace"):
+        L = cu.capi()
+        y = torch.empty(20, 48, device="cuda")
+        xd = cu.dev(x)
+        cu.check(L.llmserve_int4_linear_gemm_packed(cu._p(xd), None, cu._p(packed), cu._p(y), 20, 48,
+                                                    256, 128, None, 0, cu._stream()))
+
+
+@pytest.mark.parametrize("rows", [17, 64, 300])
+def test_int4linear_packed_paths(gpu, rows):
+    """Int4Linear's auto choice agrees with dequantize + GEMM: with 1000 outputs (not a
+    multiple of 16) only the packed kernel applies at every batch, and forcing the
+    reference-layout kernel is an error."""
+    from llmserve.quant import Int4Linear
+
+    rng = np.random.default_rng(rows)
+    lin = torch.nn.Linear(1024, 1000, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(torch.from_numpy((rng.standard_normal((1000, 1024)) * 0.02).astype(F32)))
+    act = torch.from_numpy((np.abs(rng.standard_normal(1024)) + 0.5).astype(F32))
+    q = Int4Linear(lin, 128, act, device="cuda")
+    assert q.gemm_packed is not None
+    x = torch.from_numpy(rng.standard_normal((rows, 1024)).astype(F32)).cuda()
+    q.kernel = "aten"
+    ref = q(x)
+    for k in ("auto", "gemm"):
+        q.kernel = k
+        y = q(x)
+        err = (y - ref).abs().max().item() / ref.abs().max().item()
+        assert err < 2e-5, (k, err)
+    q.kernel = "gemm_ref"
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        q(x)
