@@ -345,9 +345,8 @@ def c5_decode(torch, dev, steps: int, warmup: int) -> dict:
         gpu_ms = e0.elapsed_time(e1)
         ctx_mid = (ctx0.double() + (steps - 1) / 2).cpu().numpy()
         kv_read = int(cfg.num_hidden_layers * nk * (2 * D + 8) * ctx_mid.sum())
-        lin = model.weight_bytes()["linears"]
-        lm = (sum(b.numel() * b.element_size() for b in lm4.buffers()) if head == "int4"
-              else model.embed.numel() * 4)
+        wb = model.weight_bytes(B)
+        lin, lm = wb["linears"], wb["lm_head"]
         step_bytes = lin + lm + kv_read
         ms = wall / steps * 1e3
         out[f"lm_head_{head}"] = {

@@ -179,12 +179,19 @@ class QuantCausalLM(nn.Module):
             return self.lm_head(hidden)
         return torch.mm(hidden, self.lm_weight.t())
 
-    def weight_bytes(self) -> dict[str, int]:
-        """Bytes a decode step reads from the weights, by part."""
-        lin = sum(sum(b.numel() * b.element_size() for b in m.buffers())
-                  for L in self.layers for m in (L.qkv_proj, L.o_proj, L.gate_up_proj, L.down_proj))
-        if self.lm_head is not None:
-            lm = sum(b.numel() * b.element_size() for b in self.lm_head.buffers())
-        else:
-            lm = self.lm_weight.numel() * 4
+    def weight_bytes(self, rows: int) -> dict[str, int]:
+        """Bytes a decode step of ``rows`` tokens reads from the weights, by part: for each
+        int4 linear the buffers its kernel at that batch reads (the reference-layout nibbles,
+        scales and zeros for the GEMV, the packed copy for the matrix-core kernel) and the
+        AWQ pre-scale; the fp32 LM head matrix."""
+
+        def lin_bytes(m: Int4Linear) -> int:
+            inv = 0 if m.inv_act_scale is None else m.inv_act_scale.numel() * 4
+            if rows > m.max_fused_rows and m.gemm_packed is not None:
+                return m.gemm_packed.numel() + inv
+            return (m.nibbles.numel() + (m.g_scale.numel() + m.g_zero.numel()) * 4) + inv
+
+        lin = sum(lin_bytes(m) for L in self.layers
+                  for m in (L.qkv_proj, L.o_proj, L.gate_up_proj, L.down_proj))
+        lm = lin_bytes(self.lm_head) if self.lm_head is not None else self.lm_weight.numel() * 4
         return {"linears": lin, "lm_head": lm}
