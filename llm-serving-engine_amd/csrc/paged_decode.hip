@@ -173,7 +173,10 @@ struct Tok {
 };
 
 // Runs tokens [t0, t1) of (b, h) and writes the output rows (whole) or partial `slot`.
-template <int D, int G, bool kScalarBlk>
+// kOff32: the K / V caches and their scales are each under 4 GB, so one buffer resource per
+// tensor (built once) with the step's slot offset in the scalar offset register addresses a
+// step; else the resources are rebuilt per step from 64-bit bases.
+template <int D, int G, bool kScalarBlk, bool kOff32>
 __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h, int t0, int t1,
                                                bool whole, int64_t slot) {
   constexpr int LPR = D / 16;       // lanes per token row
@@ -224,6 +227,12 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
   const int64_t head_off = static_cast<int64_t>(h) * D + seg * 16;
   const uint32_t step_bytes = static_cast<uint32_t>(RPW * row_stride);
   const uint32_t sc_bytes = static_cast<uint32_t>(RPW * a.Hk * sizeof(float));
+  // kOff32 resources over whole tensors (the byte counts fit 32 bits by the host's choice)
+  const uint32_t rs32 = static_cast<uint32_t>(row_stride), hk4 = static_cast<uint32_t>(a.Hk * 4);
+  const __amdgpu_buffer_rsrc_t rk = rsrc(a.kc, static_cast<uint32_t>(a.num_slots * row_stride));
+  const __amdgpu_buffer_rsrc_t rv = rsrc(a.vc, static_cast<uint32_t>(a.num_slots * row_stride));
+  const __amdgpu_buffer_rsrc_t rks = rsrc(a.ks, static_cast<uint32_t>(a.num_slots * a.Hk * 4));
+  const __amdgpu_buffer_rsrc_t rvs = rsrc(a.vs, static_cast<uint32_t>(a.num_slots * a.Hk * 4));
 
   for (int wb = t0 / bs; static_cast<int64_t>(wb) * bs < t1; wb += kWin) {
     const int ws = t0 > wb * bs ? t0 : wb * bs;
@@ -255,15 +264,23 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
         const int bi = (tk >> a.bs_shift) - wb;  // wave-uniform
         const int id = bi < kWin ? __builtin_amdgcn_readlane(my_blk, bi) : -1;
         o.valid = id >= 0 && t >= ws && t < we;
-        const int64_t sb = static_cast<int64_t>(id >= 0 ? id : 0) * bs + (tk & (bs - 1));
-        o.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rsrc(a.kc + sb * row_stride, step_bytes), kv_lane, 0, kNT));
-        o.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rsrc(a.vc + sb * row_stride, step_bytes), kv_lane, 0, kNT));
-        o.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             rsrc(a.ks + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
-        o.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             rsrc(a.vs + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
+        if constexpr (kOff32) {
+          const uint32_t sb = static_cast<uint32_t>(id >= 0 ? id : 0) * bs + (tk & (bs - 1));
+          o.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, kv_lane, sb * rs32, kNT));
+          o.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, kv_lane, sb * rs32, kNT));
+          o.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, sc_lane, sb * hk4, 0));
+          o.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, sc_lane, sb * hk4, 0));
+        } else {
+          const int64_t sb = static_cast<int64_t>(id >= 0 ? id : 0) * bs + (tk & (bs - 1));
+          o.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rsrc(a.kc + sb * row_stride, step_bytes), kv_lane, 0, kNT));
+          o.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rsrc(a.vc + sb * row_stride, step_bytes), kv_lane, 0, kNT));
+          o.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                               rsrc(a.ks + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
+          o.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                               rsrc(a.vs + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
+        }
       } else {
         // every lane takes part in the shuffle (a lane's block id is read even when that
         // lane has no token of its own in this step)
@@ -393,7 +410,7 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
 // Decode kernel: workgroup w runs work ranges w, w + W, ... (one range each with the
 // balanced default); its wavefront i takes kv head hg * HB + i. Waves proceed independently
 // (no barriers).
-template <int D, int G, bool kScalarBlk>
+template <int D, int G, bool kScalarBlk, bool kOff32>
 __global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_int8_kernel(DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const Ranges rg = work_ranges(a);
@@ -415,7 +432,7 @@ __global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_int8_k
       const int h = hg * a.HB + wave;
       const bool whole = t0 == 0 && t1 == ctx;
       const int64_t slot = ((static_cast<int64_t>(b) * a.NHG + hg) + j) * a.HB + wave;
-      decode_segment<D, G, kScalarBlk>(a, b, h, static_cast<int>(t0), static_cast<int>(t1), whole,
+      decode_segment<D, G, kScalarBlk, kOff32>(a, b, h, static_cast<int>(t0), static_cast<int>(t1), whole,
                                        slot);
       g = send;
       if (g >= ge) break;
@@ -555,20 +572,26 @@ bool scalar_blocks(int64_t D, int64_t block_size) {
   return (block_size & (block_size - 1)) == 0 && block_size % (kWave / (D / 16)) == 0;
 }
 
-// Workgroups of the decode grid (all resident at once).
+// Workgroups of the decode grid (all resident at once) of the variant that runs; off32 < 0:
+// the larger of the two scalar-block variants (the workspace bound, which does not know the
+// cache size).
 template <int D, int G>
-int decode_blocks(bool scalar, int hb) {
-  return scalar ? resident_blocks(paged_decode_int8_kernel<D, G, true>, hb)
-                : resident_blocks(paged_decode_int8_kernel<D, G, false>, hb);
+int decode_blocks(bool scalar, int off32, int hb) {
+  if (!scalar) return resident_blocks(paged_decode_int8_kernel<D, G, false, false>, hb);
+  const int w32 = resident_blocks(paged_decode_int8_kernel<D, G, true, true>, hb);
+  const int w64 = resident_blocks(paged_decode_int8_kernel<D, G, true, false>, hb);
+  return off32 > 0 ? w32 : (off32 == 0 ? w64 : (w32 > w64 ? w32 : w64));
 }
 
 template <int D, int G>
-void launch_decode(const DecodeArgs& a, bool scalar, hipStream_t st) {
+void launch_decode(const DecodeArgs& a, bool scalar, bool off32, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.W)), block(a.HB * kWave);
-  if (scalar)
-    lsh::launch(paged_decode_int8_kernel<D, G, true>, grid, block, 0, st, false, a);
+  if (scalar && off32)
+    lsh::launch(paged_decode_int8_kernel<D, G, true, true>, grid, block, 0, st, false, a);
+  else if (scalar)
+    lsh::launch(paged_decode_int8_kernel<D, G, true, false>, grid, block, 0, st, false, a);
   else
-    lsh::launch(paged_decode_int8_kernel<D, G, false>, grid, block, 0, st, false, a);
+    lsh::launch(paged_decode_int8_kernel<D, G, false, false>, grid, block, 0, st, false, a);
   const int64_t items = static_cast<int64_t>(a.B) * a.Hq;
   lsh::launch(paged_decode_merge_kernel<D>,
               dim3(static_cast<unsigned>((items + kMergeWaves - 1) / kMergeWaves)),
@@ -602,11 +625,11 @@ bool with_shape(int64_t D, int64_t G, F&& f) {
   }
 }
 
-int grid_blocks(int64_t D, int64_t G, int64_t Hk, int64_t block_size) {
+int grid_blocks(int64_t D, int64_t G, int64_t Hk, int64_t block_size, int off32 = -1) {
   int w = 0;
   const bool scalar = scalar_blocks(D, block_size);
   const int hb = heads_per_block(Hk);
-  with_shape(D, G, [&]<int Dv, int Gv>() { w = decode_blocks<Dv, Gv>(scalar, hb); });
+  with_shape(D, G, [&]<int Dv, int Gv>() { w = decode_blocks<Dv, Gv>(scalar, off32, hb); });
   return w;
 }
 
@@ -694,11 +717,14 @@ extern "C" int llmserve_paged_attention_decode_int8(
     if ((1LL << sh) == block_size) a.bs_shift = sh;
   a.HB = heads_per_block(Hk);
   a.NHG = static_cast<int>(Hk / a.HB);
-  a.W = grid_blocks(D, G, Hk, block_size);
+  // one buffer resource per cache tensor when each is addressable with 32-bit offsets
+  const bool off32 = num_slots * Hk * D <= static_cast<int64_t>(0xffffffffu);
+  a.W = grid_blocks(D, G, Hk, block_size, off32 ? 1 : 0);
   a.qscale = scale * kLog2e;
   LSH_CHECK(a.W >= 1, "paged_attention: no resident workgroups");
   hipStream_t st = lsh::as_stream(stream);
-  const bool ok = with_shape(D, G, [&]<int Dv, int Gv>() { launch_decode<Dv, Gv>(a, scalar, st); });
+  const bool ok =
+      with_shape(D, G, [&]<int Dv, int Gv>() { launch_decode<Dv, Gv>(a, scalar, off32, st); });
   LSH_CHECK(ok, "paged_attention: unsupported G=%lld", (long long)G);
   return lsh::launch_status("paged_attention_decode_int8");
 }

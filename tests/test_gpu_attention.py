@@ -114,6 +114,36 @@ def test_baseline_config4_size(gpu):
     assert torch.equal(out3, out)
 
 
+def test_cache_beyond_4gb(gpu):
+    """A cache tensor of more than 4 GB (num_slots * Hk * D > 2^32) takes the kernel variant
+    with 64-bit slot addressing; its sequences live in blocks past the 4 GB mark. The used
+    blocks are copied into the big cache on the device and checked against the oracle on a
+    compact copy of the same blocks (same tokens, relabelled)."""
+    c = make_case(41, 3, 16, 8, 128, 16, 20, 120, slack_blocks=0)
+    bs, Hk, D = 16, 8, 128
+    nb_small = c["kq"].shape[0] // bs
+    nb_big = (1 << 32) // (bs * Hk * D) + 64  # 4.3 GB of K, as much of V
+    dev_blocks = nb_big - 1 - np.arange(nb_small)  # block i of the small cache -> a high id
+    kq = torch.zeros(nb_big * bs, Hk, D, dtype=torch.int8, device="cuda")
+    vq = torch.zeros_like(kq)
+    ks = torch.zeros(nb_big * bs, Hk, device="cuda")
+    vs = torch.zeros_like(ks)
+    rows = torch.from_numpy((dev_blocks[:, None] * bs + np.arange(bs)[None, :]).ravel()).cuda()
+    kq[rows] = cu.dev(c["kq"])
+    vq[rows] = cu.dev(c["vq"])
+    ks[rows] = cu.dev(c["ks"])
+    vs[rows] = cu.dev(c["vs"])
+    bt_big = dev_blocks[c["bt"]]
+    assert kq.numel() > (1 << 32)
+    out = cu.paged_decode_int8(cu.dev(c["q"]), kq, vq, ks, vs, cu.dev(bt_big), cu.dev(c["cl"]), bs,
+                               D ** -0.5, 0, cu.dev(c["q_mult"]))
+    ref = mr.paged_decode_f64(oq.q_smooth(c["q"], c["q_mult"]), mr.kv_dequantize(c["kq"], c["ks"]),
+                              mr.kv_dequantize(c["vq"], c["vs"]), c["bt"], c["cl"], bs, D ** -0.5)
+    cu.assert_rel_close(out, ref, TOL, "cache > 4 GB")
+    del kq, vq, ks, vs
+    torch.cuda.empty_cache()
+
+
 def test_edge_contexts(gpu):
     """ctx = 1 returns the token's value row; ctx = 0 gives NaN (the reference's 0 * (1/0))."""
     c = make_case(5, 3, 4, 2, 32, 4, 9, 9, outlier=False)
