@@ -161,6 +161,19 @@ int llmserve_int4_linear_gemm_packed(const float* x, const float* inv_act_scale 
                                      int64_t workspace_bytes, void* stream);
 
 /*
+ * Activation fragments: x' = x * inv_act_scale as the packed kernel reads it (bf16 hi / lo
+ * pieces in wavefront order, then fp32 sums of x' over every 128-channel block; rows up to M
+ * rounded to 16, the extra rows zero). llmserve_int4_xfrag_bytes(M, K) bytes, 16-byte aligned.
+ * Written by llmserve_int4_linear_gemm_packed's own split pass or by the fused producers
+ * below (bit-identical for the same x'); read by llmserve_int4_linear_gemm_xfrag, which is
+ * llmserve_int4_linear_gemm_packed without its split pass. No counterpart in the reference:
+ * they fuse Int4Linear's `x * inv_act_scale` (quant.py:141) into the producing kernel.
+ */
+int64_t llmserve_int4_xfrag_bytes(int64_t M, int64_t K);
+int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* packed, float* y, int64_t M,
+                                    int64_t N, int64_t K, int64_t group_size, void* stream);
+
+/*
  * Prefill-sized int8 weight-only linear on the bf16 matrix cores (replaces Int8Linear's
  * large-M path, quant.py:71-72 with dequantize quant.py:78-79: x @ (q * scale[:, None]).T):
  *   y[m, n] = scale[n] * sum_k bf16(x[m, k]) * q[n, k]      (fp32 accumulate)
@@ -199,6 +212,28 @@ int llmserve_add_rmsnorm(float* x, const float* r, const float* w, float* out, i
  */
 int llmserve_embed_rmsnorm(const int64_t* ids, const float* embed, int64_t V, const float* w,
                            float* x, float* out, int64_t T, int64_t H, float eps, void* stream);
+
+/*
+ * The norms above writing the next int4 linear's activation fragments instead of fp32 rows
+ * (rmsnorm / add_rmsnorm_ / embedding + rmsnorm fused with Int4Linear's x * inv_act_scale,
+ * fused_ops.cpp:23-81 and quant.py:141): x' = (w * (x * inv)) * act_inv (act_inv nullable),
+ * written to `xfrag` (llmserve_int4_xfrag_bytes(T, H) bytes). The residual x is updated as
+ * by the plain kernels. H a multiple of 128.
+ */
+int llmserve_rmsnorm_xfrag(const float* x, const float* w, const float* act_inv, void* xfrag,
+                           int64_t T, int64_t H, float eps, void* stream);
+int llmserve_add_rmsnorm_xfrag(float* x, const float* r, const float* w, const float* act_inv,
+                               void* xfrag, int64_t T, int64_t H, float eps, void* stream);
+int llmserve_embed_rmsnorm_xfrag(const int64_t* ids, const float* embed, int64_t V,
+                                 const float* w, const float* act_inv, float* x, void* xfrag,
+                                 int64_t T, int64_t H, float eps, void* stream);
+
+/*
+ * silu(gate) * up (fused_ops.cpp:83-99) times the down projection's act_inv (nullable), as
+ * activation fragments of [T, I] (llmserve_int4_xfrag_bytes(T, I) bytes). I a multiple of 128.
+ */
+int llmserve_silu_mul_xfrag(const float* gate_up, const float* act_inv, void* xfrag, int64_t T,
+                            int64_t I, void* stream);
 
 /*
  * out[t, i] = gate / (1 + exp(-gate)) * up for a fused gate|up row (replaces silu_mul,

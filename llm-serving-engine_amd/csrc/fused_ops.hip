@@ -11,6 +11,7 @@
 // trees over the wavefront / workgroup in a fixed order.
 #include "common.h"
 #include "kv_quant.h"
+#include "xfrag.h"
 
 namespace {
 
@@ -79,6 +80,86 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_kernel(const float* __re
     const float g = gu[t * 2 * I + i], u = gu[t * 2 * I + I + i];
     out[e] = g / (1.f + expf(-g)) * u;
   }
+}
+
+// The norms above with the int4 linear's activation fragments as output (xfrag.h): the
+// first pass is rmsnorm_kernel's (same x update, same sum of squares, same inv); the second
+// computes h = w * (x * inv) as rmsnorm_kernel does, x' = h * act_inv (the next linear's AWQ
+// pre-scale, or h) and writes x' as bf16 hi / lo fragments and block sums, with 4 consecutive
+// channels per thread (32 threads per 128-channel block). One workgroup per fragment row:
+// rows past T write zeros. H is a multiple of 128.
+template <int MODE>
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_frag_kernel(
+    float* __restrict__ x, const float* __restrict__ r, const int64_t* __restrict__ ids, int64_t V,
+    const float* __restrict__ w, const float* __restrict__ act_inv, __bf16* __restrict__ xf,
+    float* __restrict__ xsum, int T, int H, int mp, float eps) {
+  __shared__ float red[kRowThreads / kWave];
+  const int t = blockIdx.x;
+  const int nblk = H / lsh::kFragBlk;
+  if (t >= T) {  // padding row of the last 16-row tile
+    for (int c0 = 4 * threadIdx.x; c0 < H; c0 += 4 * kRowThreads) {
+      const float z[4] = {0.f, 0.f, 0.f, 0.f};
+      lsh::frag_store<4>(xf, t, c0, nblk, z);
+      if (threadIdx.x % 32 == 0) xsum[static_cast<int64_t>(c0 / lsh::kFragBlk) * mp + t] = 0.f;
+    }
+    return;
+  }
+  float* xr = x + static_cast<int64_t>(t) * H;
+  const float* src = xr;
+  bool bad = false;
+  if (MODE == kNormGather) {
+    const int64_t id = ids[t];
+    bad = id < 0 || id >= V;
+    src = r + (bad ? 0 : id) * H;
+  }
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H; i += kRowThreads) {
+    float v = src[i];
+    if (MODE == kNormAdd) v += r[static_cast<int64_t>(t) * H + i];
+    if (MODE == kNormGather && bad) v = __builtin_nanf("");
+    if (MODE != kNormPlain) xr[i] = v;
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);  // its barriers also order the x writes above before the reads below
+  const float inv = 1.f / sqrtf(ss / static_cast<float>(H) + eps);
+  for (int c0 = 4 * threadIdx.x; c0 < H; c0 += 4 * kRowThreads) {
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float h = w[c0 + e] * (xr[c0 + e] * inv);
+      v[e] = act_inv ? __fmul_rn(h, act_inv[c0 + e]) : h;
+    }
+    lsh::frag_store<4>(xf, t, c0, nblk, v);
+    const float sblk = lsh::group_sum<32>(lsh::tree_sum<4>(v));
+    if (threadIdx.x % 32 == 0) xsum[static_cast<int64_t>(c0 / lsh::kFragBlk) * mp + t] = sblk;
+  }
+}
+
+// silu(gate) * up (silu_mul_kernel's arithmetic) times the next linear's AWQ pre-scale, as
+// fragments and block sums. One wavefront per (fragment row, block), two channels per lane;
+// rows past T write zeros.
+__global__ __launch_bounds__(kRowThreads) void silu_mul_frag_kernel(
+    const float* __restrict__ gu, const float* __restrict__ act_inv, __bf16* __restrict__ xf,
+    float* __restrict__ xsum, int T, int I, int mp) {
+  const int nblk = I / lsh::kFragBlk;
+  const int item = blockIdx.x * (kRowThreads / kWave) + threadIdx.x / kWave;
+  if (item >= mp * nblk) return;  // whole wavefront
+  const int t = item / nblk, b = item % nblk;
+  const int lane = threadIdx.x % kWave;
+  const int c = lsh::kFragBlk * b + 2 * lane;
+  float v[2] = {0.f, 0.f};
+  if (t < T) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float g = gu[static_cast<int64_t>(t) * 2 * I + c + e];
+      const float u = gu[static_cast<int64_t>(t) * 2 * I + I + c + e];
+      const float a = g / (1.f + expf(-g)) * u;
+      v[e] = act_inv ? __fmul_rn(a, act_inv[c + e]) : a;
+    }
+  }
+  lsh::frag_store<2>(xf, t, c, nblk, v);
+  const float sblk = lsh::group_sum<64>(lsh::tree_sum<2>(v));
+  if (lane == 0) xsum[static_cast<int64_t>(b) * mp + t] = sblk;
 }
 
 struct RopeArgs {
@@ -428,4 +509,85 @@ extern "C" int llmserve_argmax_advance(const float* logits, int64_t T, int64_t V
   lsh::launch(argmax_finish_kernel, dim3(static_cast<unsigned>(T)), dim3(kWave), 0, st, true,
               part_v, part_i, V, next_ids, context_lens);
   return lsh::launch_status("argmax_advance");
+}
+
+// ---- producers of the int4 linear's activation fragments -------------------------------------
+
+namespace {
+
+int launch_norm_frag(int mode, float* x, const float* r, const int64_t* ids, int64_t V,
+                     const float* w, const float* act_inv, void* xfrag, int64_t T, int64_t H,
+                     float eps, void* stream, const char* what) {
+  LSH_CHECK(T >= 0 && H >= lsh::kFragBlk && H % lsh::kFragBlk == 0 && T < (1LL << 24) &&
+                H < (1LL << 24),
+            "%s: T=%lld, H=%lld (H a multiple of 128)", what, (long long)T, (long long)H);
+  if (T == 0) return LLMSERVE_OK;
+  LSH_CHECK(x && w && xfrag && (mode != kNormAdd || r) && (mode != kNormGather || (ids && r)),
+            "%s: null pointer", what);
+  LSH_CHECK(lsh::aligned16(xfrag), "%s: the fragment buffer must be 16-byte aligned", what);
+  const int mp = static_cast<int>(lsh::frag_rows(T));
+  __bf16* xf = static_cast<__bf16*>(xfrag);
+  float* xsum = reinterpret_cast<float*>(xf + 2 * static_cast<int64_t>(mp) * H);
+  const dim3 grid(static_cast<unsigned>(mp)), block(kRowThreads);
+  hipStream_t st = lsh::as_stream(stream);
+  const int Ti = static_cast<int>(T), Hi = static_cast<int>(H);
+  switch (mode) {
+    case kNormAdd:
+      lsh::launch(rmsnorm_frag_kernel<kNormAdd>, grid, block, 0, st, true, x, r, ids, V, w, act_inv,
+                  xf, xsum, Ti, Hi, mp, eps);
+      break;
+    case kNormGather:
+      lsh::launch(rmsnorm_frag_kernel<kNormGather>, grid, block, 0, st, true, x, r, ids, V, w,
+                  act_inv, xf, xsum, Ti, Hi, mp, eps);
+      break;
+    default:
+      lsh::launch(rmsnorm_frag_kernel<kNormPlain>, grid, block, 0, st, true, x, r, ids, V, w,
+                  act_inv, xf, xsum, Ti, Hi, mp, eps);
+      break;
+  }
+  return lsh::launch_status(what);
+}
+
+}  // namespace
+
+extern "C" int llmserve_rmsnorm_xfrag(const float* x, const float* w, const float* act_inv,
+                                      void* xfrag, int64_t T, int64_t H, float eps,
+                                      void* stream) {
+  return launch_norm_frag(kNormPlain, const_cast<float*>(x), nullptr, nullptr, 0, w, act_inv, xfrag,
+                          T, H, eps, stream, "rmsnorm_xfrag");
+}
+
+extern "C" int llmserve_add_rmsnorm_xfrag(float* x, const float* r, const float* w,
+                                          const float* act_inv, void* xfrag, int64_t T, int64_t H,
+                                          float eps, void* stream) {
+  return launch_norm_frag(kNormAdd, x, r, nullptr, 0, w, act_inv, xfrag, T, H, eps, stream,
+                          "add_rmsnorm_xfrag");
+}
+
+extern "C" int llmserve_embed_rmsnorm_xfrag(const int64_t* ids, const float* embed, int64_t V,
+                                            const float* w, const float* act_inv, float* x,
+                                            void* xfrag, int64_t T, int64_t H, float eps,
+                                            void* stream) {
+  LSH_CHECK(V >= 1, "embed_rmsnorm_xfrag: empty embedding");
+  return launch_norm_frag(kNormGather, x, embed, ids, V, w, act_inv, xfrag, T, H, eps, stream,
+                          "embed_rmsnorm_xfrag");
+}
+
+extern "C" int llmserve_silu_mul_xfrag(const float* gate_up, const float* act_inv, void* xfrag,
+                                       int64_t T, int64_t I, void* stream) {
+  LSH_CHECK(T >= 0 && I >= lsh::kFragBlk && I % lsh::kFragBlk == 0 && T < (1LL << 24) &&
+                I < (1LL << 24),
+            "silu_mul_xfrag: T=%lld, I=%lld (I a multiple of 128)", (long long)T, (long long)I);
+  if (T == 0) return LLMSERVE_OK;
+  LSH_CHECK(gate_up && xfrag, "silu_mul_xfrag: null pointer");
+  LSH_CHECK(lsh::aligned16(xfrag), "silu_mul_xfrag: the fragment buffer must be 16-byte aligned");
+  const int mp = static_cast<int>(lsh::frag_rows(T));
+  __bf16* xf = static_cast<__bf16*>(xfrag);
+  float* xsum = reinterpret_cast<float*>(xf + 2 * static_cast<int64_t>(mp) * I);
+  const int64_t items = static_cast<int64_t>(mp) * (I / lsh::kFragBlk);
+  const int wpb = kRowThreads / kWave;
+  lsh::launch(silu_mul_frag_kernel, dim3(static_cast<unsigned>((items + wpb - 1) / wpb)),
+              dim3(kRowThreads), 0, lsh::as_stream(stream), true, gate_up, act_inv, xf, xsum,
+              static_cast<int>(T), static_cast<int>(I), mp);
+  return lsh::launch_status("silu_mul_xfrag");
 }

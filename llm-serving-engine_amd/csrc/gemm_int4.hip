@@ -29,6 +29,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "xfrag.h"
 
 namespace {
 
@@ -285,19 +286,17 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const float* __restric
   o[4 + u] = zz;
 }
 
-// x' = x * inv split into bf16 hi / lo fragments (packed layout above) and xsum[b, m]. One
-// workgroup per (row tile, block), wavefront q writing step q; rows past M are zeros. The
-// channel sums add the 8 values of a lane, then the 4 lanes of a row, then the 4 steps
-// (fixed order).
-__global__ __launch_bounds__(4 * kWave) void x_split_frag_kernel(
+// x' = x * inv split into bf16 hi / lo fragments (xfrag.h) and xsum[b, m]. One workgroup
+// per (row tile, block): thread (row fr, segment s) handles channels 8 s .. + 8 of row
+// 16 t + fr; rows past M are zeros. xsum is the pairwise tree of the block's 128 channels.
+__global__ __launch_bounds__(256) void x_split_frag_kernel(
     const float* __restrict__ x, const float* __restrict__ inv, __bf16* __restrict__ xf,
     float* __restrict__ xsum, int M, int K, int mp) {
-  __shared__ float part[4][16];
   const int nblk = K / kBlk;
   const int t = blockIdx.x / nblk, b = blockIdx.x % nblk;
-  const int q = threadIdx.x / kWave, lane = threadIdx.x % kWave, fr = lane % 16, fc = lane / 16;
+  const int fr = threadIdx.x / 16, seg = threadIdx.x % 16;
   const int m = 16 * t + fr;
-  const int c = kBlk * b + 32 * fc + 8 * q;
+  const int c = kBlk * b + 8 * seg;
   float v[8];
   if (m < M) {
     const f32x4 a0 = *reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(m) * K + c);
@@ -320,24 +319,9 @@ __global__ __launch_bounds__(4 * kWave) void x_split_frag_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = 0.f;
   }
-  bf16x8 hi, lo;
-  float s = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    hi[e] = static_cast<__bf16>(v[e]);
-    lo[e] = static_cast<__bf16>(v[e] - static_cast<float>(hi[e]));
-    s += v[e];
-  }
-  __bf16* f = xf + ((((static_cast<int64_t>(t) * nblk + b) * 4 + q) * 2) * kWave + lane) * 8;
-  *reinterpret_cast<bf16x8*>(f) = hi;
-  *reinterpret_cast<bf16x8*>(f + kPkFrag) = lo;
-  s += __shfl_xor(s, 16, kWave);
-  s += __shfl_xor(s, 32, kWave);
-  if (fc == 0) part[q][fr] = s;
-  __syncthreads();
-  if (threadIdx.x < 16)
-    xsum[static_cast<int64_t>(b) * mp + 16 * t + threadIdx.x] =
-        (part[0][threadIdx.x] + part[1][threadIdx.x]) + (part[2][threadIdx.x] + part[3][threadIdx.x]);
+  lsh::frag_store<8>(xf, m, c, nblk, v);
+  const float s = lsh::group_sum<16>(lsh::tree_sum<8>(v));
+  if (seg == 0) xsum[static_cast<int64_t>(b) * mp + m] = s;
 }
 
 // Decode-sized batches (up to a few 16-row tiles). The time goes to each CU's memory
@@ -567,7 +551,12 @@ extern "C" int llmserve_int4_gemm_pack(const uint8_t* nibbles, const float* g_sc
 
 extern "C" int64_t llmserve_int4_linear_gemm_packed_workspace_bytes(int64_t M, int64_t K) {
   if (M <= 0 || K <= 0) return 0;
-  return xsum_rows(M) * K * 4 + (K / kBlk) * xsum_rows(M) * 4;
+  return lsh::frag_bytes(M, K);
+}
+
+extern "C" int64_t llmserve_int4_xfrag_bytes(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0 || K % kBlk) return 0;
+  return lsh::frag_bytes(M, K);
 }
 
 extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv_act_scale,
@@ -598,8 +587,8 @@ extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv
   const int mp = static_cast<int>(xsum_rows(M));
   __bf16* xf = static_cast<__bf16*>(workspace);
   float* xsum = reinterpret_cast<float*>(xf + 2 * static_cast<int64_t>(mp) * K);
-  lsh::launch(x_split_frag_kernel, dim3(static_cast<unsigned>(mtiles * nb)), dim3(4 * kWave), 0, st,
-              false, x, inv_act_scale, xf, xsum, static_cast<int>(M), static_cast<int>(K), mp);
+  lsh::launch(x_split_frag_kernel, dim3(static_cast<unsigned>(mtiles * nb)), dim3(256), 0, st, false,
+              x, inv_act_scale, xf, xsum, static_cast<int>(M), static_cast<int>(K), mp);
   const uint8_t* wpk = static_cast<const uint8_t*>(packed);
   const float* spk = reinterpret_cast<const float*>(wpk + (pk_weight_bytes(N, K) + 255) / 256 * 256);
   Int4GemmArgs a{xf, nullptr, xsum, wpk, spk, nullptr, y, static_cast<int>(M),
@@ -607,4 +596,31 @@ extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv
                  static_cast<int>(group_size / kBlk), mp};
   launch_lat(a, pk_slabs(N), mtiles, nb, st);
   return lsh::launch_status("int4_linear_gemm_packed");
+}
+
+extern "C" int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* packed, float* y,
+                                               int64_t M, int64_t N, int64_t K,
+                                               int64_t group_size, void* stream) {
+  LSH_CHECK(M >= 0 && N >= 1 && K >= 1 && group_size >= 2, "int4_linear_gemm_xfrag: bad shape");
+  LSH_CHECK(K % kBlk == 0 && group_size % kBlk == 0 && K % group_size == 0,
+            "int4_linear_gemm_xfrag: K and group_size must be multiples of 128 (K %% group == 0)");
+  LSH_CHECK(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31) && M * K < (1LL << 40) &&
+                N * K < (1LL << 41),
+            "int4_linear_gemm_xfrag: shape too large");
+  if (M == 0) return LLMSERVE_OK;
+  LSH_CHECK(xfrag && packed && y, "int4_linear_gemm_xfrag: null pointer");
+  LSH_CHECK(lsh::aligned16(xfrag) && lsh::aligned16(packed),
+            "int4_linear_gemm_xfrag: the fragments and the packed weight must be 16-byte aligned");
+  const int nb = static_cast<int>(K / kBlk);
+  const int64_t mtiles = (M + kRows - 1) / kRows;
+  const int mp = static_cast<int>(lsh::frag_rows(M));
+  const __bf16* xf = static_cast<const __bf16*>(xfrag);
+  const float* xsum = reinterpret_cast<const float*>(xf + 2 * static_cast<int64_t>(mp) * K);
+  const uint8_t* wpk = static_cast<const uint8_t*>(packed);
+  const float* spk = reinterpret_cast<const float*>(wpk + (pk_weight_bytes(N, K) + 255) / 256 * 256);
+  Int4GemmArgs a{xf, nullptr, xsum, wpk, spk, nullptr, y, static_cast<int>(M),
+                 static_cast<int>(N), static_cast<int>(K), static_cast<int>(K / group_size),
+                 static_cast<int>(group_size / kBlk), mp};
+  launch_lat(a, pk_slabs(N), mtiles, nb, lsh::as_stream(stream));
+  return lsh::launch_status("int4_linear_gemm_xfrag");
 }

@@ -424,6 +424,94 @@ at::Tensor argmax_advance(const at::Tensor& logits, at::Tensor& context_lens) {
   return ids;
 }
 
+// ---- activation fragments of the packed int4 linear --------------------------------------------
+
+at::Tensor new_xfrag(const at::Tensor& like, int64_t T, int64_t K, const char* what) {
+  const int64_t bytes = llmserve_int4_xfrag_bytes(T, K);
+  TORCH_CHECK(bytes > 0, what, ": the channel count must be a multiple of 128");
+  return at::empty({bytes}, like.options().dtype(at::kByte));
+}
+
+void check_act_inv(const at::Tensor& x, const std::optional<at::Tensor>& act_inv, int64_t K,
+                   const char* what) {
+  if (!act_inv.has_value()) return;
+  check_device(x, {&*act_inv}, what);
+  TORCH_CHECK(act_inv->scalar_type() == at::kFloat && act_inv->is_contiguous() &&
+                  act_inv->numel() == K,
+              what, ": act_inv must be a contiguous float32 tensor with one entry per channel");
+}
+
+at::Tensor add_rmsnorm_xfrag_(at::Tensor& x, const at::Tensor& r, const at::Tensor& w,
+                              const std::optional<at::Tensor>& act_inv, double eps) {
+  check_f32(x, "x");
+  check_f32(r, "r");
+  check_f32(w, "w");
+  check_device(x, {&r, &w}, "add_rmsnorm_xfrag_");
+  TORCH_CHECK(x.sizes() == r.sizes() && x.dim() == 2, "add_rmsnorm_xfrag_: x, r [T, H]");
+  const int64_t T = x.size(0), H = x.size(1);
+  TORCH_CHECK(w.numel() == H, "add_rmsnorm_xfrag_: weight must have H entries");
+  check_act_inv(x, act_inv, H, "add_rmsnorm_xfrag_");
+  const c10::DeviceGuard guard(x.device());
+  auto xf = new_xfrag(x, T, H, "add_rmsnorm_xfrag_");
+  check_status(llmserve_add_rmsnorm_xfrag(x.data_ptr<float>(), r.data_ptr<float>(),
+                                          w.data_ptr<float>(), opt_ptr<float>(act_inv),
+                                          xf.data_ptr(), T, H, static_cast<float>(eps),
+                                          stream_of(x)));
+  return xf;
+}
+
+std::tuple<at::Tensor, at::Tensor> embed_rmsnorm_xfrag(const at::Tensor& ids,
+                                                       const at::Tensor& embed, const at::Tensor& w,
+                                                       const std::optional<at::Tensor>& act_inv,
+                                                       double eps) {
+  check_f32(embed, "embed");
+  check_f32(w, "w");
+  TORCH_CHECK(ids.scalar_type() == at::kLong && ids.is_contiguous() && ids.dim() == 1,
+              "embed_rmsnorm_xfrag: ids must be a contiguous int64 [T] tensor");
+  check_device(embed, {&ids, &w}, "embed_rmsnorm_xfrag");
+  TORCH_CHECK(embed.dim() == 2, "embed_rmsnorm_xfrag: embed must be [V, H]");
+  const int64_t T = ids.numel(), V = embed.size(0), H = embed.size(1);
+  TORCH_CHECK(w.numel() == H, "embed_rmsnorm_xfrag: weight must have H entries");
+  check_act_inv(embed, act_inv, H, "embed_rmsnorm_xfrag");
+  const c10::DeviceGuard guard(embed.device());
+  auto x = at::empty({T, H}, embed.options());
+  auto xf = new_xfrag(embed, T, H, "embed_rmsnorm_xfrag");
+  check_status(llmserve_embed_rmsnorm_xfrag(ids.data_ptr<int64_t>(), embed.data_ptr<float>(), V,
+                                            w.data_ptr<float>(), opt_ptr<float>(act_inv),
+                                            x.data_ptr<float>(), xf.data_ptr(), T, H,
+                                            static_cast<float>(eps), stream_of(embed)));
+  return {x, xf};
+}
+
+at::Tensor silu_mul_xfrag(const at::Tensor& gate_up, const std::optional<at::Tensor>& act_inv) {
+  check_f32(gate_up, "gate_up");
+  TORCH_CHECK(gate_up.dim() == 2 && gate_up.size(1) % 2 == 0, "silu_mul_xfrag: gate_up [T, 2I]");
+  const int64_t T = gate_up.size(0), I = gate_up.size(1) / 2;
+  check_act_inv(gate_up, act_inv, I, "silu_mul_xfrag");
+  const c10::DeviceGuard guard(gate_up.device());
+  auto xf = new_xfrag(gate_up, T, I, "silu_mul_xfrag");
+  check_status(llmserve_silu_mul_xfrag(gate_up.data_ptr<float>(), opt_ptr<float>(act_inv),
+                                       xf.data_ptr(), T, I, stream_of(gate_up)));
+  return xf;
+}
+
+at::Tensor int4_linear_gemm_xfrag(const at::Tensor& xfrag, const at::Tensor& packed, int64_t M,
+                                  int64_t N, int64_t K, int64_t group_size) {
+  TORCH_CHECK(xfrag.scalar_type() == at::kByte && xfrag.is_contiguous() &&
+                  xfrag.numel() == llmserve_int4_xfrag_bytes(M, K),
+              "int4_linear_gemm_xfrag: xfrag must hold the fragments of [M, K]");
+  TORCH_CHECK(packed.scalar_type() == at::kByte && packed.is_contiguous() &&
+                  packed.numel() == llmserve_int4_gemm_pack_bytes(N, K, group_size),
+              "int4_linear_gemm_xfrag: packed buffer does not match N, K, group_size");
+  check_device(xfrag, {&packed}, "int4_linear_gemm_xfrag");
+  const c10::DeviceGuard guard(xfrag.device());
+  auto y = at::empty({M, N}, xfrag.options().dtype(at::kFloat));
+  check_status(llmserve_int4_linear_gemm_xfrag(xfrag.data_ptr(), packed.data_ptr(),
+                                               y.data_ptr<float>(), M, N, K, group_size,
+                                               stream_of(xfrag)));
+  return y;
+}
+
 // ---- int8-KV paged decode -------------------------------------------------------------------
 
 at::Tensor paged_attention_decode_int8(const at::Tensor& q, const at::Tensor& k_cache,
@@ -498,6 +586,12 @@ TORCH_LIBRARY(llmserve_hip, m) {
   m.def("rmsnorm(Tensor x, Tensor w, float eps) -> Tensor");
   m.def("add_rmsnorm_(Tensor(a!) x, Tensor r, Tensor w, float eps) -> Tensor");
   m.def("embed_rmsnorm(Tensor ids, Tensor embed, Tensor w, float eps) -> (Tensor, Tensor)");
+  m.def("add_rmsnorm_xfrag_(Tensor(a!) x, Tensor r, Tensor w, Tensor? act_inv, float eps) -> Tensor");
+  m.def("embed_rmsnorm_xfrag(Tensor ids, Tensor embed, Tensor w, Tensor? act_inv, float eps)"
+        " -> (Tensor, Tensor)");
+  m.def("silu_mul_xfrag(Tensor gate_up, Tensor? act_inv) -> Tensor");
+  m.def("int4_linear_gemm_xfrag(Tensor xfrag, Tensor packed, int M, int N, int K, int group_size)"
+        " -> Tensor");
   m.def("silu_mul(Tensor gate_up) -> Tensor");
   m.def("rope_qk_(Tensor(a!) qkv, Tensor cos, Tensor sin, int n_q, int n_k, int head_dim,"
         " Tensor? q_w=None, Tensor? k_w=None, float eps=1e-6) -> ()");
@@ -524,6 +618,10 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("rmsnorm", &rmsnorm);
   m.impl("add_rmsnorm_", &add_rmsnorm_);
   m.impl("embed_rmsnorm", &embed_rmsnorm);
+  m.impl("add_rmsnorm_xfrag_", &add_rmsnorm_xfrag_);
+  m.impl("embed_rmsnorm_xfrag", &embed_rmsnorm_xfrag);
+  m.impl("silu_mul_xfrag", &silu_mul_xfrag);
+  m.impl("int4_linear_gemm_xfrag", &int4_linear_gemm_xfrag);
   m.impl("silu_mul", &silu_mul);
   m.impl("rope_qk_", &rope_qk_);
   m.impl("decode_qkv_kv", &decode_qkv_kv);

@@ -1,0 +1,74 @@
+// Activation fragments of the batched int4 linear (int4_gemm_lat): x' = x * inv_act_scale
+// split into bf16 hi = bf16(x') and lo = bf16(x' - hi), laid out in the order the matrix-core
+// wavefronts read them, plus the channel sums of x' over every 128-channel block.
+//
+//   fragments: [row tile t][block b][step q][hi, lo][lane][8 bf16]; lane = fr + 16 fc holds
+//              row 16 t + fr, channels 128 b + 32 fc + 8 q .. + 8 (rows past M are zero);
+//   xsum:      [block][mp] fp32 after the fragments, mp = M rounded up to 16.
+//
+// Every producer (the split pass of llmserve_int4_linear_gemm_packed, the fused norms and
+// silu * up) sums a block as the same pairwise tree over the 128 channels in index order, so
+// their outputs are bit-identical for the same x'.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace lsh {
+
+constexpr int kFragBlk = 128;       // channels of a block
+constexpr int kFragElems = 64 * 8;  // bf16 of one (step, hi / lo) fragment
+
+__host__ __device__ inline int64_t frag_rows(int64_t M) { return (M + 15) / 16 * 16; }
+
+// Bytes of fragments + channel sums for M rows and K channels (K a multiple of 128).
+inline int64_t frag_bytes(int64_t M, int64_t K) {
+  return frag_rows(M) * K * 4 + (K / kFragBlk) * frag_rows(M) * 4;
+}
+
+// Element offset of the hi value of x'[m, c] (the lo value is kFragElems further).
+__device__ __forceinline__ int64_t frag_offset(int m, int c, int nblk) {
+  const int t = m / 16, fr = m % 16, b = c / kFragBlk, cc = c % kFragBlk;
+  const int fc = cc / 32, q = (cc % 32) / 8, e = cc % 8;
+  return ((((static_cast<int64_t>(t) * nblk + b) * 4 + q) * 2) * 64 + fr + 16 * fc) * 8 + e;
+}
+
+// hi / lo bf16 split of an fp32 value (round to nearest even; hi + lo equals v to 2^-18).
+__device__ __forceinline__ void split_bf16(float v, __bf16& hi, __bf16& lo) {
+  hi = static_cast<__bf16>(v);
+  lo = static_cast<__bf16>(v - static_cast<float>(hi));
+}
+
+// Writes N consecutive channels c .. c + N - 1 (within one 8-channel group) of row m.
+template <int N>
+__device__ __forceinline__ void frag_store(__bf16* xf, int m, int c, int nblk, const float (&v)[N]) {
+  static_assert(N == 2 || N == 4 || N == 8, "frag_store: 2, 4 or 8 channels");
+  typedef __bf16 bfN __attribute__((ext_vector_type(N)));
+  bfN hi, lo;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    __bf16 h, l;
+    split_bf16(v[e], h, l);
+    hi[e] = h;
+    lo[e] = l;
+  }
+  __bf16* p = xf + frag_offset(m, c, nblk);
+  *reinterpret_cast<bfN*>(p) = hi;
+  *reinterpret_cast<bfN*>(p + kFragElems) = lo;
+}
+
+// Pairwise tree of N consecutive values in index order (the first levels of a block sum).
+template <int N>
+__device__ __forceinline__ float tree_sum(const float (&v)[N]) {
+  if constexpr (N == 2) {
+    return v[0] + v[1];
+  } else if constexpr (N == 4) {
+    return (v[0] + v[1]) + (v[2] + v[3]);
+  } else {
+    static_assert(N == 8, "tree_sum: 2, 4 or 8");
+    return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  }
+}
+
+}  // namespace lsh

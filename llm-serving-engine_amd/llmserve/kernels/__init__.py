@@ -22,7 +22,12 @@ objects expose the reference's function names and signatures:
   ``silu_mul(gate_up)`` and ``rope_qk_(qkv, cos, sin, n_q, n_k, head_dim, q_w=None, k_w=None,
   eps=1e-6)`` (fused_ops.cpp:129-137), plus the decode-step glue ``embed_rmsnorm(ids, embed,
   w, eps) -> (x, h)`` (embedding lookup + first input norm), ``decode_qkv_kv`` (q/k norm,
-  RoPE and the int8 KV-cache write in one launch) and ``argmax_advance`` (greedy next token).
+  RoPE and the int8 KV-cache write in one launch) and ``argmax_advance`` (greedy next token);
+  and the producers of the packed int4 linear's activation fragments, which fuse the next
+  linear's ``x * inv_act_scale`` and bf16 split into the norm / silu kernel:
+  ``add_rmsnorm_xfrag_(x, r, w, act_inv, eps)``, ``embed_rmsnorm_xfrag(ids, embed, w, act_inv,
+  eps) -> (x, xfrag)``, ``silu_mul_xfrag(gate_up, act_inv)``, consumed by
+  ``int4_linear_gemm_xfrag(xfrag, packed, M, N, K, group_size)``.
 
 The fp32-KV decode variants (``paged_attention_decode``, ``paged_attention_decode_v1``,
 ``set_simd``) are outside the quantized path and not provided.
@@ -76,6 +81,10 @@ def load_fused_ops() -> SimpleNamespace:
         rmsnorm=o.rmsnorm,
         add_rmsnorm_=o.add_rmsnorm_,
         embed_rmsnorm=o.embed_rmsnorm,
+        add_rmsnorm_xfrag_=o.add_rmsnorm_xfrag_,
+        embed_rmsnorm_xfrag=o.embed_rmsnorm_xfrag,
+        silu_mul_xfrag=o.silu_mul_xfrag,
+        int4_linear_gemm_xfrag=o.int4_linear_gemm_xfrag,
         silu_mul=o.silu_mul,
         rope_qk_=o.rope_qk_,
         decode_qkv_kv=o.decode_qkv_kv,

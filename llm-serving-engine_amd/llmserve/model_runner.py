@@ -52,7 +52,8 @@ class DecodeRunner:
         m = self.model
         h = m.forward_decode(self.ids, self.context_lens, self.block_tables, self.cache.layers,
                              self.block_size)
-        return m.compute_logits(h)
+        B = self.ids.numel()
+        return m.compute_logits(h, B if m._lm_frag(B) else None)
 
     def _step(self) -> None:
         self.logits = self.forward_logits()

@@ -145,9 +145,21 @@ class QuantCausalLM(nn.Module):
         self.register_buffer("rope_sin", sin.to(dev))
         self.scale = D ** -0.5
 
+    # Above the GEMV's row limit the norms and silu * up write the next linear's activation
+    # fragments directly (its x * inv_act_scale and bf16 split fused in), and the linears run
+    # the packed matrix-core kernel on them: one launch less per linear, same result bits.
+    fuse_xfrag = True
+
+    def _xfrag_ok(self, rows: int) -> bool:
+        lins = [m for L in self.layers for m in (L.qkv_proj, L.o_proj, L.gate_up_proj, L.down_proj)]
+        return (self.fuse_xfrag and all(m.kernel == "auto" and m.gemm_packed is not None
+                                        and rows > m.max_fused_rows and rows <= m.max_packed_rows
+                                        for m in lins))
+
     def forward_decode(self, ids: torch.Tensor, context_lens: torch.Tensor,
                        block_tables: torch.Tensor, kv_layers, block_size: int) -> torch.Tensor:
-        """Final hidden states [B, H] of one decode token per sequence.
+        """Final hidden states [B, H] of one decode token per sequence (or, when the int4 LM
+        head consumes it, its activation fragments: ``compute_logits`` takes either).
 
         ``ids`` [B] int64; ``context_lens`` [B] int64 counts the token being decoded (its
         position is ctx - 1); ``block_tables`` [B, max_blocks] int64 holds the blocks of every
@@ -156,25 +168,60 @@ class QuantCausalLM(nn.Module):
         cfg = self.cfg
         fo, pa = load_fused_ops(), load_paged_attention()
         nq, nk, D, eps = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rms_norm_eps
-        B = ids.shape[0]
-        x, h = fo.embed_rmsnorm(ids, self.embed, self.layers[0].input_layernorm, eps)
+        B, H, I = ids.shape[0], cfg.hidden_size, cfg.intermediate_size
         n = len(self.layers)
+        frag = self._xfrag_ok(B)
+
+        def gemm(xf, lin, K):
+            return fo.int4_linear_gemm_xfrag(xf, lin.gemm_packed, B, lin.out_features, K,
+                                             lin.group_size)
+
+        if frag:
+            x, h = fo.embed_rmsnorm_xfrag(ids, self.embed, self.layers[0].input_layernorm,
+                                          self.layers[0].qkv_proj.inv_act_scale, eps)
+        else:
+            x, h = fo.embed_rmsnorm(ids, self.embed, self.layers[0].input_layernorm, eps)
         for i, (L, (kc, vc)) in enumerate(zip(self.layers, kv_layers, strict=True)):
-            qkv = L.qkv_proj(h)
+            qkv = gemm(h, L.qkv_proj, H) if frag else L.qkv_proj(h)
             q = fo.decode_qkv_kv(qkv, self.rope_cos, self.rope_sin, context_lens, block_tables,
                                  block_size, L.q_norm, L.k_norm, eps, kc.smooth, kc.data, vc.data,
                                  kc.scale, vc.scale, nq, nk, D)
             o = pa.paged_attention_decode_int8(q, kc.data, vc.data, kc.scale, vc.scale,
                                                block_tables, context_lens, block_size,
                                                self.scale, 0, kc._q_mult)
-            h = fo.add_rmsnorm_(x, L.o_proj(o.view(B, nq * D)), L.post_attention_layernorm, eps)
-            down = L.down_proj(fo.silu_mul(L.gate_up_proj(h)))
-            nxt = self.layers[i + 1].input_layernorm if i + 1 < n else self.norm
-            h = fo.add_rmsnorm_(x, down, nxt, eps)
+            attn = L.o_proj(o.view(B, nq * D))
+            nxt = self.layers[i + 1] if i + 1 < n else None
+            nxt_w = nxt.input_layernorm if nxt is not None else self.norm
+            if frag:
+                h = fo.add_rmsnorm_xfrag_(x, attn, L.post_attention_layernorm,
+                                          L.gate_up_proj.inv_act_scale, eps)
+                a = fo.silu_mul_xfrag(gemm(h, L.gate_up_proj, H), L.down_proj.inv_act_scale)
+                down = gemm(a, L.down_proj, I)
+                if nxt is not None:
+                    h = fo.add_rmsnorm_xfrag_(x, down, nxt_w, nxt.qkv_proj.inv_act_scale, eps)
+                elif self._lm_frag(B):
+                    h = fo.add_rmsnorm_xfrag_(x, down, nxt_w, self.lm_head.inv_act_scale, eps)
+                else:
+                    h = fo.add_rmsnorm_(x, down, nxt_w, eps)
+            else:
+                h = fo.add_rmsnorm_(x, attn, L.post_attention_layernorm, eps)
+                down = L.down_proj(fo.silu_mul(L.gate_up_proj(h)))
+                h = fo.add_rmsnorm_(x, down, nxt_w, eps)
         return h
 
-    def compute_logits(self, hidden: torch.Tensor) -> torch.Tensor:
-        """lm_head (transformer.py:192-193): fp32 [B, V]."""
+    def _lm_frag(self, rows: int) -> bool:
+        m = self.lm_head
+        return (self._xfrag_ok(rows) and m is not None and m.kernel == "auto"
+                and m.gemm_packed is not None and m.max_fused_rows < rows <= m.max_packed_rows)
+
+    def compute_logits(self, hidden: torch.Tensor, rows: int | None = None) -> torch.Tensor:
+        """lm_head (transformer.py:192-193): fp32 [B, V]. ``hidden`` is the fp32 [B, H] final
+        norm output, or (``rows`` given) the int4 LM head's activation fragments."""
+        if rows is not None:
+            m = self.lm_head
+            return load_fused_ops().int4_linear_gemm_xfrag(hidden, m.gemm_packed, rows,
+                                                           m.out_features, m.in_features,
+                                                           m.group_size)
         if self.lm_head is not None:
             return self.lm_head(hidden)
         return torch.mm(hidden, self.lm_weight.t())

@@ -161,3 +161,65 @@ def test_argmax_small_vocab(gpu, V):
     c = cu.dev(np.zeros(4, np.int64))
     ids = fo().argmax_advance(cu.dev(logits), c).cpu().numpy()
     assert np.array_equal(ids, torch.from_numpy(logits).argmax(-1).numpy())
+
+
+# ---- producers of the packed int4 linear's activation fragments ------------------------------
+
+def _int4_packed(N, K, seed, awq=True):
+    from llmserve.kernels import load_int8_gemv, load_quant
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randn(N, K, device="cuda", generator=g) * 0.02
+    act = (torch.rand(K, device="cuda", generator=g) + 0.5) if awq else None
+    nib, gs, gz, inv = load_quant().int4_quantize(w, 128, act)
+    return load_int8_gemv().int4_gemm_pack(nib, gs, gz, 128), (inv if awq else None)
+
+
+@pytest.mark.parametrize("T", [17, 64, 70])
+@pytest.mark.parametrize("awq", [True, False])
+def test_xfrag_producers_equal_split_path(gpu, T, awq):
+    """Norm / silu kernels writing fragments + the fragment GEMM give the same bits as the
+    plain kernels followed by int4_linear_gemm_packed (its own split pass): the x' values,
+    their bf16 split and the block sums are computed the same way."""
+    from llmserve.kernels import load_int8_gemv
+
+    f, lin = fo(), load_int8_gemv()
+    H, I, N = 1024, 3072, 4096
+    rng = np.random.default_rng(T + awq)
+    x0 = rng.standard_normal((T, H)).astype(F32)
+    r = rng.standard_normal((T, H)).astype(F32)
+    w = (1 + 0.1 * rng.standard_normal(H)).astype(F32)
+    pk, inv = _int4_packed(N, H, 1, awq)
+    # add + rmsnorm
+    xa, xb = cu.dev(x0), cu.dev(x0)
+    h = f.add_rmsnorm_(xa, cu.dev(r), cu.dev(w), 1e-6)
+    ref = lin.int4_linear_gemm_packed(h, pk, N, 128, inv)
+    xf = f.add_rmsnorm_xfrag_(xb, cu.dev(r), cu.dev(w), inv, 1e-6)
+    got = f.int4_linear_gemm_xfrag(xf, pk, T, N, H, 128)
+    assert torch.equal(xa, xb) and torch.equal(got, ref)
+    # embedding + rmsnorm
+    V = 300
+    emb = rng.standard_normal((V, H)).astype(F32)
+    ids = cu.dev(rng.integers(0, V, T).astype(np.int64))
+    xe, he = f.embed_rmsnorm(ids, cu.dev(emb), cu.dev(w), 1e-6)
+    xe2, xfe = f.embed_rmsnorm_xfrag(ids, cu.dev(emb), cu.dev(w), inv, 1e-6)
+    assert torch.equal(xe, xe2)
+    assert torch.equal(f.int4_linear_gemm_xfrag(xfe, pk, T, N, H, 128),
+                       lin.int4_linear_gemm_packed(he, pk, N, 128, inv))
+    # silu * up -> down projection (K = 3072)
+    pkd, invd = _int4_packed(1024, I, 2, awq)
+    gu = cu.dev(rng.standard_normal((T, 2 * I)).astype(F32))
+    ref = lin.int4_linear_gemm_packed(f.silu_mul(gu), pkd, 1024, 128, invd)
+    got = f.int4_linear_gemm_xfrag(f.silu_mul_xfrag(gu, invd), pkd, T, 1024, I, 128)
+    assert torch.equal(got, ref)
+
+
+def test_xfrag_rejects_bad_shapes(gpu):
+    f = fo()
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        f.silu_mul_xfrag(torch.zeros(4, 2 * 100, device="cuda"), None)
+    pk, inv = _int4_packed(64, 256, 3)
+    xf = f.add_rmsnorm_xfrag_(torch.zeros(8, 256, device="cuda"), torch.zeros(8, 256, device="cuda"),
+                              torch.ones(256, device="cuda"), None, 1e-6)
+    with pytest.raises(RuntimeError, match="fragments"):
+        f.int4_linear_gemm_xfrag(xf, pk, 17, 64, 256, 128)  # buffer of one 16-row tile

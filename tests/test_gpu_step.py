@@ -146,6 +146,27 @@ def test_graph_replays_equal_eager_steps(gpu):
         assert torch.equal(v.data, vd) and torch.equal(v.scale, vs)
 
 
+@pytest.mark.parametrize("lm_int4", [False, True])
+def test_fragment_path_equals_plain_path(gpu, lm_int4):
+    """Above 16 rows the step fuses each linear's x * inv_act_scale and bf16 split into the
+    producing norm / silu kernel; the logits, tokens and caches equal the unfused step's bit
+    for bit."""
+    cfg = tiny_cfg()
+    ctx = list(range(20, 500, 20))
+    model, cache, runner, host, ids, ctx, bt = setup(cfg, ctx, 31, lm_int4)
+    start = runner.snapshot()
+    assert model._xfrag_ok(len(ids))
+    runner.step()
+    fused = (runner.logits.clone(), runner.ids.clone(), runner.snapshot()[2])
+    runner.restore(start)
+    model.fuse_xfrag = False
+    runner.step()
+    assert torch.equal(runner.logits, fused[0]) and torch.equal(runner.ids, fused[1])
+    for a, b in zip(runner.snapshot()[2], fused[2]):
+        for u, v in zip(a, b):
+            assert torch.equal(u, v)
+
+
 def test_embed_rmsnorm(gpu):
     from llmserve.kernels import load_fused_ops
     from oracle import fused_ops as ofo
