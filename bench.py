@@ -504,6 +504,20 @@ def profile_only(torch, dev, what: str) -> int:
         gemv = load_int8_gemv()
         for i in range(16):
             gemv.int8_linear_prefill(x, *qs[i % 2])
+    elif what == "gemm4":  # config 5's batched int4 linear: qkv 1024->4096 at 64 rows, packed
+        N, K = SHAPES["qkv"]
+        g = torch.Generator(device=dev).manual_seed(5)
+        gemv = load_int8_gemv()
+        packed = []
+        for _ in range(64):
+            nib, gs, gz, inv = load_quant().int4_quantize(
+                torch.randn(N, K, device=dev, generator=g) * 0.02, GROUP,
+                torch.rand(K, device=dev, generator=g) + 0.5)
+            packed.append((gemv.int4_gemm_pack(nib, gs, gz, GROUP), inv))
+        x = torch.randn(64, K, device=dev, generator=g)
+        for i in range(64):
+            pk, inv = packed[i]
+            gemv.int4_linear_gemm_packed(x, pk, N, GROUP, inv)
     elif what == "attention":
         copies, q, cl, qm, bs, D, _ = c4_inputs(torch, dev)
         pa = load_paged_attention()
@@ -527,7 +541,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
-    ap.add_argument("--only", choices=["gemv", "attention", "prefill", "copy"],
+    ap.add_argument("--only", choices=["gemv", "gemm4", "attention", "prefill", "copy"],
                     help="profiling run: only launch that kernel (64 times) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
