@@ -19,10 +19,12 @@ stream the kernel runs on — the per-dispatch interval a kernel-trace profiler 
 `cpu_baseline` times the reference's own CPU kernels (oracle/_ref, built from the reference
 sources) — or the oracle's C restatement where that build is absent — on the host cores, on
 the same quantized weights, for about 10 s.
-Extra fields report M = 4 / 16 steps and configs 1 (int8 GEMV), 3 (prefill int8 GEMM on the
-bf16 matrix cores, x conversion included), 4 (int8-KV decode) and 5 (the full greedy decode
-step of a random-init int4-AWQ Qwen3-0.6B at batch 64 over the int8 KV cache, one HIP graph
-replay per step: tokens/s, with the fp32 and the int4 LM head, and per-op times).
+Extra fields report M = 4 / 16 steps (the kernel Int4Linear runs at that batch: the GEMV up
+to 4 rows, the matrix-core kernel on the packed weight above) and configs 1 (int8 GEMV), 3
+(prefill int8 GEMM on the bf16 matrix cores, x conversion included), 4 (int8-KV decode) and
+5 (the full greedy decode step of a random-init int4-AWQ Qwen3-0.6B at batch 64 over the int8
+KV cache, one HIP graph replay per step: tokens/s, with the fp32 and the int4 LM head, and
+per-op times).
 """
 
 from __future__ import annotations
@@ -96,25 +98,40 @@ def make_inputs(torch, dev, calib, M: int):
     return {name: calib[name][:M].contiguous() for name in SHAPES}
 
 
-def capture_steps(torch, model, xs, gemv):
-    """One HIP graph per weight copy, each holding the 112 launches of one step."""
+GEMV_ROWS = 4  # Int4Linear.gemv_max_rows: the GEMV up to 4 rows, the matrix-core kernel above
+
+
+def pack_all(torch, model, gemv):
+    """The packed copy of every weight (Int4Linear keeps one for its matrix-core kernel)."""
+    return [[{n: gemv.int4_gemm_pack(*lin[n][:3], GROUP) for n in SHAPES} for lin in layers]
+            for layers in model]
+
+
+def capture_steps(torch, model, xs, gemv, packed=None):
+    """One HIP graph per weight copy, each holding the 112 launches of one step: the int4 GEMV
+    (M <= GEMV_ROWS) or, given the packed weights, the matrix-core kernel with its split pass,
+    as Int4Linear runs them."""
+    def launch(lin, pk, name):
+        nib, gs, gz, inv = lin[name]
+        if pk is None:
+            return gemv.int4_linear(xs[name], nib, gs, gz, GROUP, inv)
+        return gemv.int4_linear_gemm_packed(xs[name], pk[name], SHAPES[name][0], GROUP, inv)
+
     graphs, outs = [], []
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):  # warm the op (allocator) outside capture
         for name in SHAPES:
-            nib, gs, gz, inv = model[0][0][name]
-            gemv.int4_linear(xs[name], nib, gs, gz, GROUP, inv)
+            launch(model[0][0], None if packed is None else packed[0][0], name)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    for layers in model:
+    for c, layers in enumerate(model):
         g = torch.cuda.CUDAGraph()
         ys = []
         with torch.cuda.graph(g):
-            for lin in layers:
+            for li, lin in enumerate(layers):
                 for name in SHAPES:
-                    nib, gs, gz, inv = lin[name]
-                    ys.append(gemv.int4_linear(xs[name], nib, gs, gz, GROUP, inv))
+                    ys.append(launch(lin, None if packed is None else packed[c][li], name))
         graphs.append(g)
         outs.append(ys)
     torch.cuda.synchronize()
@@ -562,20 +579,26 @@ def main() -> int:
 
     by_rows = {}
     headline = None
+    packed = None
     for M in (1, 4, 16):
         xs = make_inputs(torch, dev, calib, M)
-        graphs, _ = capture_steps(torch, model, xs, gemv)
+        if M > GEMV_ROWS and packed is None:
+            packed = pack_all(torch, model, gemv)
+        graphs, _ = capture_steps(torch, model, xs, gemv, packed if M > GEMV_ROWS else None)
         steps = args.steps if M == 1 else max(20, args.steps // 4)
         wall, gpu = time_graphs(torch, graphs, steps, args.warmup)
         step_bytes = LAYERS * sum(int4_bytes(N, K, M) for N, K in SHAPES.values())
         gbs = step_bytes * steps / wall / 1e9
-        by_rows[str(M)] = {"GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+        by_rows[str(M)] = {"kernel": ("gemv" if M <= GEMV_ROWS else
+                                      "matrix-core on packed weight (split pass included)"),
+                           "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                            "ms_per_step": round(wall / steps * 1e3, 4),
                            "gpu_ms_per_step": round(gpu / steps * 1e3, 4), "bytes": step_bytes}
         if M == 1:
             headline = (gbs, wall / steps * 1e3, steps, step_bytes)
         del graphs
         log(f"[bench] M={M}: {by_rows[str(M)]}")
+    del packed
 
     # dominant kernel: the gate_up GEMV at M = 1
     N, K = SHAPES["gate_up"]

@@ -136,12 +136,15 @@ class Int4Linear(nn.Module):
     same fp32 ``x * inv_act_scale`` the reference computes.
     """
 
-    max_fused_rows = 16  # above this: the large-M path (reference quant.py:123)
+    max_fused_rows = 16  # the reference's GEMV limit (quant.py:123): above it, the large-M path
+    gemv_max_rows = 4  # the HIP GEMV's rows when the packed matrix-core kernel applies
     max_packed_rows = 256  # up to this: the decode-batch kernel on the packed weight
-    # "auto": the HIP GEMV up to max_fused_rows rows; above that the HIP matrix-core GEMM on
-    # the packed weight ("gemm", K and group multiples of 128) up to max_packed_rows rows, and
-    # the matrix-core GEMM on the reference layout ("gemm_ref", out also a multiple of 16)
-    # beyond; else dequantize + GEMM ("aten", the reference's large-M algorithm). Each name
+    # "auto": the HIP GEMV up to gemv_max_rows rows (its straight-line kernel; measured at the
+    # Qwen3-0.6B shapes, the matrix-core kernel ties it from 6 rows and is ~2x faster from 12),
+    # then the HIP matrix-core GEMM on the packed weight ("gemm", K and group multiples of 128)
+    # up to max_packed_rows rows; without a packed weight the GEMV up to max_fused_rows rows;
+    # beyond, the matrix-core GEMM on the reference layout ("gemm_ref", out also a multiple of
+    # 16), else dequantize + GEMM ("aten", the reference's large-M algorithm). Each name
     # forces its kernel for every batch.
     kernel = "auto"
 
@@ -188,6 +191,11 @@ class Int4Linear(nn.Module):
         w = (q - 8) * self.g_scale[..., None] + self.g_zero[..., None]
         return w.reshape(self.out_features, self.in_features)
 
+    def packed_path(self, rows: int) -> bool:
+        """``kernel="auto"`` runs the packed matrix-core kernel for ``rows`` activation rows."""
+        return (self.kernel == "auto" and self.gemm_packed is not None
+                and self.gemv_max_rows < rows <= self.max_packed_rows)
+
     def gemm_ok(self) -> bool:
         """Shapes the reference-layout matrix-core kernel (int4_linear_gemm) takes."""
         return (self.in_features % 128 == 0 and self.group_size % 128 == 0
@@ -198,9 +206,11 @@ class Int4Linear(nn.Module):
         x2 = x.reshape(-1, shape[-1])
         rows = x2.shape[0]
         if self.kernel == "auto":
-            if rows <= self.max_fused_rows:
+            if self.packed_path(rows):
+                path = "gemm"
+            elif rows <= self.max_fused_rows:
                 path = "gemv"
-            elif self.gemm_packed is not None and (rows <= self.max_packed_rows or not self.gemm_ok()):
+            elif self.gemm_packed is not None and not self.gemm_ok():
                 path = "gemm"
             else:
                 path = "gemm_ref" if self.gemm_ok() else "aten"

@@ -145,16 +145,15 @@ class QuantCausalLM(nn.Module):
         self.register_buffer("rope_sin", sin.to(dev))
         self.scale = D ** -0.5
 
-    # Above the GEMV's row limit the norms and silu * up write the next linear's activation
+    # Where the linears run the packed matrix-core kernel (above the GEMV's rows) the norms
+    # and silu * up write the next linear's activation
     # fragments directly (its x * inv_act_scale and bf16 split fused in), and the linears run
     # the packed matrix-core kernel on them: one launch less per linear, same result bits.
     fuse_xfrag = True
 
     def _xfrag_ok(self, rows: int) -> bool:
         lins = [m for L in self.layers for m in (L.qkv_proj, L.o_proj, L.gate_up_proj, L.down_proj)]
-        return (self.fuse_xfrag and all(m.kernel == "auto" and m.gemm_packed is not None
-                                        and rows > m.max_fused_rows and rows <= m.max_packed_rows
-                                        for m in lins))
+        return self.fuse_xfrag and all(m.packed_path(rows) for m in lins)
 
     def forward_decode(self, ids: torch.Tensor, context_lens: torch.Tensor,
                        block_tables: torch.Tensor, kv_layers, block_size: int) -> torch.Tensor:
@@ -211,8 +210,7 @@ class QuantCausalLM(nn.Module):
 
     def _lm_frag(self, rows: int) -> bool:
         m = self.lm_head
-        return (self._xfrag_ok(rows) and m is not None and m.kernel == "auto"
-                and m.gemm_packed is not None and m.max_fused_rows < rows <= m.max_packed_rows)
+        return self._xfrag_ok(rows) and m is not None and m.packed_path(rows)
 
     def compute_logits(self, hidden: torch.Tensor, rows: int | None = None) -> torch.Tensor:
         """lm_head (transformer.py:192-193): fp32 [B, V]. ``hidden`` is the fp32 [B, H] final
@@ -234,7 +232,7 @@ class QuantCausalLM(nn.Module):
 
         def lin_bytes(m: Int4Linear) -> int:
             inv = 0 if m.inv_act_scale is None else m.inv_act_scale.numel() * 4
-            if rows > m.max_fused_rows and m.gemm_packed is not None:
+            if m.packed_path(rows):
                 return m.gemm_packed.numel() + inv
             return (m.nibbles.numel() + (m.g_scale.numel() + m.g_zero.numel()) * 4) + inv
 

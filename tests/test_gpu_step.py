@@ -1,7 +1,7 @@
 """One greedy decode step of the quantized model (llmserve.transformer + llmserve.model_runner)
 against the decode-step oracle (oracle/decode_step.py), and graph replays against eager steps.
 
-Tolerances: logits max-abs <= 2e-5 x max|logits| with the GEMV linears (<= 16 rows: float32
+Tolerances: logits max-abs <= 2e-5 x max|logits| with the GEMV linears (<= 4 rows: float32
 through two layers, different reduction orders) and <= 1e-4 with the matrix-core linears (the
 bf16 hi/lo split of x is exact to 2^-18 per element; 1e-4 is the reference's fused-vs-plain
 bar, tests/test_fused_ops.py:40); the oracle reads the K/V rows the HIP step wrote, so a
@@ -25,7 +25,7 @@ BS = 16
 
 
 def tol(rows: int) -> float:
-    return 2e-5 if rows <= 16 else 1e-4
+    return 2e-5 if rows <= 4 else 1e-4  # the GEMV up to 4 rows, the matrix-core kernel above
 
 
 def tiny_cfg(vocab=512):
@@ -111,8 +111,9 @@ def check_step(cfg, model, cache, runner, host, ids, ctx, bt):
 
 
 @pytest.mark.parametrize("ctx,lm_int4,smooth", [
-    ([1, 16, 17, 300, 77], False, True),     # 5 rows: the GEMV linears
-    ([1, 16, 17, 300, 77], True, False),     # int4 LM head
+    ([1, 16, 17, 300, 77], False, True),     # 5 rows: the matrix-core linears
+    ([1, 16, 17, 300], True, False),         # 4 rows: the GEMV linears, int4 LM head
+    ([9, 300], False, True),                 # 2 rows
     (list(range(20, 500, 20)), False, True),  # 24 rows: the matrix-core linears
     (list(range(20, 500, 20)), True, True),
 ])
