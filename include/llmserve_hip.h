@@ -315,6 +315,23 @@ int llmserve_paged_attention_decode_int8(
     int64_t block_size, float scale, int64_t partition_size, const float* q_mult /* nullable */,
     void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * llmserve_paged_attention_decode_int8 whose merge also writes the next linear's input: the
+ * attention output [B, Hq*D] times act_inv (nullable; the o_proj's inv_act_scale) as
+ * activation fragments (llmserve_int4_xfrag_bytes(B, Hq*D) bytes at xfrag, 16-byte aligned)
+ * for llmserve_int4_linear_gemm_xfrag. `out` is written as by the plain entry; the fragments
+ * equal what llmserve_rmsnorm_xfrag-style producers write for the same x' (same rounding and
+ * block-sum order). D = 128 or 256. No counterpart in the reference: it fuses Int4Linear's
+ * `x * inv_act_scale` (quant.py:141) of o_proj into the attention's last kernel.
+ */
+int llmserve_paged_attention_decode_int8_xfrag(
+    const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
+    const float* v_scale, const int64_t* block_tables, const int64_t* context_lens, float* out,
+    const float* act_inv /* nullable */, void* xfrag, int64_t B, int64_t Hq, int64_t Hk, int64_t D,
+    int64_t num_slots, int64_t max_blocks, int64_t block_size, float scale,
+    int64_t partition_size, const float* q_mult /* nullable */, void* workspace,
+    int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -117,7 +117,9 @@ __device__ __forceinline__ float group_max(float v) {
 }
 
 // Sum / max over the lanes that share lane % LO (LO a power of two <= 64): the "columns"
-// of a wave laid out as rows of LO lanes. Every lane gets its column's result.
+// of a wave laid out as rows of LO lanes. Every lane gets its column's result; for LO <= 4
+// the two row rotations pair the partial sums differently in different lanes, so the sum may
+// differ in its last bit between lanes (group_sum<64> gives every lane the same bits).
 template <int LO>
 __device__ __forceinline__ float wave_sum_from(float v) {
   if constexpr (LO <= 1) v += dpp<kQuadXor1>(v);

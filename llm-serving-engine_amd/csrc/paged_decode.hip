@@ -39,6 +39,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "xfrag.h"
 
 namespace {
 
@@ -532,13 +533,126 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_kernel
       }
     }
   }
-  L = lsh::wave_sum_from<1>(L);
+  L = lsh::group_sum<kWave>(L);  // the same bits in every lane (xor / mirror steps)
   const float inv = 1.f / L;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int d = lane + i * kWave;
     if (d < D) out[d] = o[i] * inv;
   }
+}
+
+// Merge writing the o_proj input fragments as well (decode step): one wavefront per (row m,
+// q head) over the mp = 16-row-padded rows, each lane holding CPL = D / 64 consecutive
+// channels of the output row. A split (b, head) is merged as paged_decode_merge_kernel does
+// (same operations in the same order, so the same bits); a whole one is read back from out;
+// a zero context is NaN; rows m >= B are zero. Every row then goes out as
+// x' = out * act_inv (act_inv nullable) in the activation-fragment layout of the batched int4
+// linear (xfrag.h), and each 128-channel block's sum of x' as the same pairwise tree in
+// channel order that the other fragment producers use.
+template <int D>
+__global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_frag_kernel(
+    DecodeArgs a, const float* __restrict__ act_inv, __bf16* __restrict__ xf,
+    float* __restrict__ xsum, int mp) {
+  static_assert(D == 128 || D == 256, "fragment merge: D = 128 or 256");
+  constexpr int CPL = D / kWave;              // channels per lane: 2 or 4
+  constexpr int LPB = lsh::kFragBlk / CPL;    // lanes per 128-channel block: 64 or 32
+  const int lane = threadIdx.x % kWave;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kMergeWaves +
+                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  if (item >= static_cast<int64_t>(mp) * a.Hq) return;
+  const int b = static_cast<int>(item / a.Hq), hq = static_cast<int>(item % a.Hq);
+  const int nblk = a.Hq * D / lsh::kFragBlk;
+  const int c0 = hq * D + lane * CPL;  // first channel of this lane in the [B, Hq * D] row
+  float x[CPL];
+  if (b >= a.B) {
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) x[e] = 0.f;
+  } else {
+    const int G = a.Hq / a.Hk;
+    const int h = hq / G, g = hq % G;
+    float* out = a.out + item * D + lane * CPL;
+    int64_t tot = 0, pre = 0, cb = 0;
+    for (int b0 = 0; b0 < a.B; b0 += kWave) {
+      const int bb = b0 + lane;
+      const int64_t c = bb < a.B ? seq_ctx(a, bb) : 0;
+      tot += c;
+      pre += bb < b ? c : 0;
+      cb += bb == b ? c : 0;
+    }
+    tot = uniform64(wave_sum_i64(tot));
+    pre = uniform64(wave_sum_i64(pre));
+    const int64_t ctx = uniform64(wave_sum_i64(cb));
+    const int64_t T = tot * a.NHG;
+    int64_t Q = a.range > 0 ? a.range : (T + a.W - 1) / a.W;
+    if (Q < 1) Q = 1;
+    const int hg = h / a.HB;
+    const int64_t g0 = pre * a.NHG + hg * ctx;
+    const int64_t j0 = ctx > 0 ? g0 / Q : 0, j1 = ctx > 0 ? (g0 + ctx - 1) / Q : 0;
+    if (ctx == 0) {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        x[e] = __builtin_nanf("");
+        out[e] = x[e];
+      }
+    } else if (j0 == j1) {  // written whole by the decode kernel
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) x[e] = out[e];
+    } else {
+      const int64_t base = ((static_cast<int64_t>(b) * a.NHG + hg) + j0) * a.HB + h % a.HB;
+      const int np = static_cast<int>(j1 - j0 + 1);
+      auto ml = [&](int p) {
+        return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2;
+      };
+      float M = kNegBig;
+      for (int p = lane; p < np; p += kWave) M = fmaxf(M, ml(p)[0]);
+      M = lsh::wave_max_from<1>(M);
+      float L = 0.f, o[CPL];
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) o[e] = 0.f;
+      for (int p0 = 0; p0 < np; p0 += kWave) {
+        float w = 0.f;
+        if (p0 + lane < np) {
+          const float* pm = ml(p0 + lane);
+          const float lp = pm[1];
+          w = lp == 0.f ? 0.f : __builtin_amdgcn_exp2f(pm[0] - M);
+          L += w * lp;
+        }
+        const int n = np - p0 < kWave ? np - p0 : kWave;
+        for (int j0b = 0; j0b < n; j0b += kMergeBatch) {
+          float v[kMergeBatch][CPL];
+#pragma unroll
+          for (int j = 0; j < kMergeBatch; ++j) {
+            const int jj = j0b + j < n ? j0b + j : n - 1;  // in-bounds row; weight zeroed below
+            const float* src = a.part_acc +
+                               ((base + static_cast<int64_t>(p0 + jj) * a.HB) * G + g) * D + lane * CPL;
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) v[j][e] = src[e];
+          }
+#pragma unroll
+          for (int j = 0; j < kMergeBatch; ++j) {
+            const float wj = j0b + j < n ? __shfl(w, j0b + j, kWave) : 0.f;
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) o[e] += wj * v[j][e];
+          }
+        }
+      }
+      L = lsh::group_sum<kWave>(L);  // the same bits in every lane (xor / mirror steps)
+      const float inv = 1.f / L;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        x[e] = o[e] * inv;
+        out[e] = x[e];
+      }
+    }
+    if (act_inv) {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) x[e] = __fmul_rn(x[e], act_inv[c0 + e]);
+    }
+  }
+  lsh::frag_store<CPL>(xf, b, c0, nblk, x);
+  const float sum = lsh::group_sum<LPB>(lsh::tree_sum<CPL>(x));
+  if (lane % LPB == 0) xsum[static_cast<int64_t>(c0 / lsh::kFragBlk) * mp + b] = sum;
 }
 
 // Resident workgroups of `waves` wavefronts of a kernel on the current device: CUs x blocks
@@ -583,8 +697,14 @@ int decode_blocks(bool scalar, int off32, int hb) {
   return off32 > 0 ? w32 : (off32 == 0 ? w64 : (w32 > w64 ? w32 : w64));
 }
 
+// Fragment output of the merge (nullptr: the plain merge writes out only).
+struct FragOut {
+  const float* act_inv;
+  void* xfrag;
+};
+
 template <int D, int G>
-void launch_decode(const DecodeArgs& a, bool scalar, bool off32, hipStream_t st) {
+void launch_decode(const DecodeArgs& a, bool scalar, bool off32, const FragOut& fo, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.W)), block(a.HB * kWave);
   if (scalar && off32)
     lsh::launch(paged_decode_int8_kernel<D, G, true, true>, grid, block, 0, st, false, a);
@@ -592,6 +712,19 @@ void launch_decode(const DecodeArgs& a, bool scalar, bool off32, hipStream_t st)
     lsh::launch(paged_decode_int8_kernel<D, G, true, false>, grid, block, 0, st, false, a);
   else
     lsh::launch(paged_decode_int8_kernel<D, G, false, false>, grid, block, 0, st, false, a);
+  if constexpr (D == 128 || D == 256) {
+    if (fo.xfrag != nullptr) {
+      const int mp = static_cast<int>(lsh::frag_rows(a.B));
+      const int64_t K = static_cast<int64_t>(a.Hq) * D;
+      __bf16* xf = static_cast<__bf16*>(fo.xfrag);
+      float* xsum = reinterpret_cast<float*>(xf + static_cast<int64_t>(mp) * K * 2);
+      const int64_t items = static_cast<int64_t>(mp) * a.Hq;
+      lsh::launch(paged_decode_merge_frag_kernel<D>,
+                  dim3(static_cast<unsigned>((items + kMergeWaves - 1) / kMergeWaves)),
+                  dim3(kMergeWaves * kWave), 0, st, true, a, fo.act_inv, xf, xsum, mp);
+      return;
+    }
+  }
   const int64_t items = static_cast<int64_t>(a.B) * a.Hq;
   lsh::launch(paged_decode_merge_kernel<D>,
               dim3(static_cast<unsigned>((items + kMergeWaves - 1) / kMergeWaves)),
@@ -659,12 +792,14 @@ extern "C" int64_t llmserve_paged_attention_workspace_bytes(int64_t B, int64_t H
   return slots * G * (D + 2) * static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int llmserve_paged_attention_decode_int8(
-    const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
-    const float* v_scale, const int64_t* block_tables, const int64_t* context_lens, float* out,
-    int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots, int64_t max_blocks,
-    int64_t block_size, float scale, int64_t partition_size, const float* q_mult, void* workspace,
-    int64_t workspace_bytes, void* stream) {
+namespace {
+
+int decode_int8(const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
+                const float* v_scale, const int64_t* block_tables, const int64_t* context_lens,
+                float* out, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots,
+                int64_t max_blocks, int64_t block_size, float scale, int64_t partition_size,
+                const float* q_mult, const FragOut& fo, void* workspace, int64_t workspace_bytes,
+                void* stream) {
   LSH_CHECK(B >= 0 && Hq >= 1 && Hk >= 1 && D >= 1, "paged_attention: bad shape");
   LSH_CHECK(Hq % Hk == 0, "Hq must be a multiple of Hk");
   LSH_CHECK(block_size >= 1 && max_blocks >= 0 && num_slots >= 0, "paged_attention: bad cache shape");
@@ -724,7 +859,38 @@ extern "C" int llmserve_paged_attention_decode_int8(
   LSH_CHECK(a.W >= 1, "paged_attention: no resident workgroups");
   hipStream_t st = lsh::as_stream(stream);
   const bool ok =
-      with_shape(D, G, [&]<int Dv, int Gv>() { launch_decode<Dv, Gv>(a, scalar, off32, st); });
+      with_shape(D, G, [&]<int Dv, int Gv>() { launch_decode<Dv, Gv>(a, scalar, off32, fo, st); });
   LSH_CHECK(ok, "paged_attention: unsupported G=%lld", (long long)G);
   return lsh::launch_status("paged_attention_decode_int8");
+}
+
+}  // namespace
+
+extern "C" int llmserve_paged_attention_decode_int8(
+    const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
+    const float* v_scale, const int64_t* block_tables, const int64_t* context_lens, float* out,
+    int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots, int64_t max_blocks,
+    int64_t block_size, float scale, int64_t partition_size, const float* q_mult, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+  return decode_int8(q, k_cache, v_cache, k_scale, v_scale, block_tables, context_lens, out, B, Hq,
+                     Hk, D, num_slots, max_blocks, block_size, scale, partition_size, q_mult,
+                     FragOut{nullptr, nullptr}, workspace, workspace_bytes, stream);
+}
+
+extern "C" int llmserve_paged_attention_decode_int8_xfrag(
+    const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
+    const float* v_scale, const int64_t* block_tables, const int64_t* context_lens, float* out,
+    const float* act_inv, void* xfrag, int64_t B, int64_t Hq, int64_t Hk, int64_t D,
+    int64_t num_slots, int64_t max_blocks, int64_t block_size, float scale,
+    int64_t partition_size, const float* q_mult, void* workspace, int64_t workspace_bytes,
+    void* stream) {
+  LSH_CHECK(D == 128 || D == 256,
+            "paged_attention_decode_int8_xfrag: head_dim %lld not 128 or 256", (long long)D);
+  LSH_CHECK(B >= 0 && Hq >= 1 && B * Hq * D < (1LL << 31),
+            "paged_attention_decode_int8_xfrag: bad or too large shape");
+  LSH_CHECK(B == 0 || (xfrag != nullptr && lsh::aligned16(xfrag)),
+            "paged_attention_decode_int8_xfrag: xfrag must be a 16-byte aligned buffer");
+  return decode_int8(q, k_cache, v_cache, k_scale, v_scale, block_tables, context_lens, out, B, Hq,
+                     Hk, D, num_slots, max_blocks, block_size, scale, partition_size, q_mult,
+                     FragOut{act_inv, xfrag}, workspace, workspace_bytes, stream);
 }

@@ -514,12 +514,11 @@ at::Tensor int4_linear_gemm_xfrag(const at::Tensor& xfrag, const at::Tensor& pac
 
 // ---- int8-KV paged decode -------------------------------------------------------------------
 
-at::Tensor paged_attention_decode_int8(const at::Tensor& q, const at::Tensor& k_cache,
-                                       const at::Tensor& v_cache, const at::Tensor& k_scale,
-                                       const at::Tensor& v_scale, const at::Tensor& block_tables,
-                                       const at::Tensor& context_lens, int64_t block_size,
-                                       double scale, int64_t partition_size,
-                                       const std::optional<at::Tensor>& q_mult) {
+// Checks of the paged decode's tensors (dtypes, shapes, devices, contiguity).
+void check_paged(const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
+                 const at::Tensor& k_scale, const at::Tensor& v_scale,
+                 const at::Tensor& block_tables, const at::Tensor& context_lens,
+                 const std::optional<at::Tensor>& q_mult) {
   TORCH_CHECK(k_cache.scalar_type() == at::kChar && v_cache.scalar_type() == at::kChar,
               "paged_attention_decode_int8: int8 cache");
   TORCH_CHECK(k_scale.scalar_type() == at::kFloat && v_scale.scalar_type() == at::kFloat &&
@@ -549,14 +548,34 @@ at::Tensor paged_attention_decode_int8(const at::Tensor& q, const at::Tensor& k_
                     q_mult->numel() == Hq * D,
                 "paged_attention_decode_int8: q_mult must be a contiguous float32 [Hq, D] tensor");
   }
+}
+
+at::Tensor paged_workspace(const at::Tensor& q, const at::Tensor& k_cache,
+                           const at::Tensor& block_tables, int64_t block_size,
+                           int64_t partition_size, int64_t& ws_bytes) {
+  ws_bytes = llmserve_paged_attention_workspace_bytes(q.size(0), q.size(1), k_cache.size(1),
+                                                      q.size(2), block_tables.size(1), block_size,
+                                                      partition_size);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes / 4}, q.options());
+  return ws;
+}
+
+at::Tensor paged_attention_decode_int8(const at::Tensor& q, const at::Tensor& k_cache,
+                                       const at::Tensor& v_cache, const at::Tensor& k_scale,
+                                       const at::Tensor& v_scale, const at::Tensor& block_tables,
+                                       const at::Tensor& context_lens, int64_t block_size,
+                                       double scale, int64_t partition_size,
+                                       const std::optional<at::Tensor>& q_mult) {
+  check_paged(q, k_cache, v_cache, k_scale, v_scale, block_tables, context_lens, q_mult);
+  const int64_t B = q.size(0), Hq = q.size(1), D = q.size(2);
+  const int64_t num_slots = k_cache.size(0), Hk = k_cache.size(1);
   const c10::DeviceGuard guard(q.device());
   auto out = at::empty_like(q);
   if (B == 0) return out;
   const int64_t max_blocks = block_tables.size(1);
-  const int64_t ws_bytes = llmserve_paged_attention_workspace_bytes(B, Hq, Hk, D, max_blocks,
-                                                                    block_size, partition_size);
-  at::Tensor ws;
-  if (ws_bytes > 0) ws = at::empty({ws_bytes / 4}, q.options());
+  int64_t ws_bytes = 0;
+  at::Tensor ws = paged_workspace(q, k_cache, block_tables, block_size, partition_size, ws_bytes);
   check_status(llmserve_paged_attention_decode_int8(
       q.data_ptr<float>(), k_cache.data_ptr<int8_t>(), v_cache.data_ptr<int8_t>(),
       k_scale.data_ptr<float>(), v_scale.data_ptr<float>(), block_tables.data_ptr<int64_t>(),
@@ -564,6 +583,32 @@ at::Tensor paged_attention_decode_int8(const at::Tensor& q, const at::Tensor& k_
       max_blocks, block_size, static_cast<float>(scale), partition_size, opt_ptr<float>(q_mult),
       ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q)));
   return out;
+}
+
+std::tuple<at::Tensor, at::Tensor> paged_attention_decode_int8_xfrag(
+    const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
+    const at::Tensor& k_scale, const at::Tensor& v_scale, const at::Tensor& block_tables,
+    const at::Tensor& context_lens, int64_t block_size, double scale, int64_t partition_size,
+    const std::optional<at::Tensor>& q_mult, const std::optional<at::Tensor>& act_inv) {
+  check_paged(q, k_cache, v_cache, k_scale, v_scale, block_tables, context_lens, q_mult);
+  const int64_t B = q.size(0), Hq = q.size(1), D = q.size(2);
+  const int64_t num_slots = k_cache.size(0), Hk = k_cache.size(1);
+  TORCH_CHECK(D == 128 || D == 256, "paged_attention_decode_int8_xfrag: head_dim 128 or 256");
+  check_act_inv(q, act_inv, Hq * D, "paged_attention_decode_int8_xfrag");
+  const c10::DeviceGuard guard(q.device());
+  auto out = at::empty_like(q);
+  auto xf = new_xfrag(q, B, Hq * D, "paged_attention_decode_int8_xfrag");
+  if (B == 0) return {out, xf};
+  int64_t ws_bytes = 0;
+  at::Tensor ws = paged_workspace(q, k_cache, block_tables, block_size, partition_size, ws_bytes);
+  check_status(llmserve_paged_attention_decode_int8_xfrag(
+      q.data_ptr<float>(), k_cache.data_ptr<int8_t>(), v_cache.data_ptr<int8_t>(),
+      k_scale.data_ptr<float>(), v_scale.data_ptr<float>(), block_tables.data_ptr<int64_t>(),
+      context_lens.data_ptr<int64_t>(), out.data_ptr<float>(), opt_ptr<float>(act_inv),
+      xf.data_ptr(), B, Hq, Hk, D, num_slots, block_tables.size(1), block_size,
+      static_cast<float>(scale), partition_size, opt_ptr<float>(q_mult),
+      ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q)));
+  return {out, xf};
 }
 
 }  // namespace
@@ -603,6 +648,10 @@ TORCH_LIBRARY(llmserve_hip, m) {
   m.def("paged_attention_decode_int8(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale,"
         " Tensor v_scale, Tensor block_tables, Tensor context_lens, int block_size, float scale,"
         " int partition_size=0, Tensor? q_mult=None) -> Tensor");
+  m.def("paged_attention_decode_int8_xfrag(Tensor q, Tensor k_cache, Tensor v_cache,"
+        " Tensor k_scale, Tensor v_scale, Tensor block_tables, Tensor context_lens,"
+        " int block_size, float scale, int partition_size=0, Tensor? q_mult=None,"
+        " Tensor? act_inv=None) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
@@ -627,4 +676,5 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("decode_qkv_kv", &decode_qkv_kv);
   m.impl("argmax_advance", &argmax_advance);
   m.impl("paged_attention_decode_int8", &paged_attention_decode_int8);
+  m.impl("paged_attention_decode_int8_xfrag", &paged_attention_decode_int8_xfrag);
 }

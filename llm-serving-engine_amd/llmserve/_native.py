@@ -82,6 +82,10 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
         _I32,
         [_P] * 8 + [_I64] * 7 + [_F32, _I64, _P, _P, _I64, _P],
     ),
+    "llmserve_paged_attention_decode_int8_xfrag": (
+        _I32,
+        [_P] * 10 + [_I64] * 7 + [_F32, _I64, _P, _P, _I64, _P],
+    ),
 }
 
 

@@ -59,7 +59,8 @@ def load_int8_gemv() -> SimpleNamespace:
 def load_paged_attention() -> SimpleNamespace:
     """int8-KV paged decode attention (HIP, gfx950)."""
     o = ops()
-    return SimpleNamespace(paged_attention_decode_int8=o.paged_attention_decode_int8)
+    return SimpleNamespace(paged_attention_decode_int8=o.paged_attention_decode_int8,
+                           paged_attention_decode_int8_xfrag=o.paged_attention_decode_int8_xfrag)
 
 
 @functools.cache

@@ -153,7 +153,9 @@ class QuantCausalLM(nn.Module):
 
     def _xfrag_ok(self, rows: int) -> bool:
         lins = [m for L in self.layers for m in (L.qkv_proj, L.o_proj, L.gate_up_proj, L.down_proj)]
-        return self.fuse_xfrag and all(m.packed_path(rows) for m in lins)
+        # the attention merge writes fragments of whole 128-channel blocks: head_dim 128 or 256
+        return (self.fuse_xfrag and self.cfg.head_dim in (128, 256)
+                and all(m.packed_path(rows) for m in lins))
 
     def forward_decode(self, ids: torch.Tensor, context_lens: torch.Tensor,
                        block_tables: torch.Tensor, kv_layers, block_size: int) -> torch.Tensor:
@@ -185,10 +187,16 @@ class QuantCausalLM(nn.Module):
             q = fo.decode_qkv_kv(qkv, self.rope_cos, self.rope_sin, context_lens, block_tables,
                                  block_size, L.q_norm, L.k_norm, eps, kc.smooth, kc.data, vc.data,
                                  kc.scale, vc.scale, nq, nk, D)
-            o = pa.paged_attention_decode_int8(q, kc.data, vc.data, kc.scale, vc.scale,
-                                               block_tables, context_lens, block_size,
-                                               self.scale, 0, kc._q_mult)
-            attn = L.o_proj(o.view(B, nq * D))
+            if frag:  # the attention merge writes o_proj's input fragments
+                _, xo = pa.paged_attention_decode_int8_xfrag(
+                    q, kc.data, vc.data, kc.scale, vc.scale, block_tables, context_lens,
+                    block_size, self.scale, 0, kc._q_mult, L.o_proj.inv_act_scale)
+                attn = gemm(xo, L.o_proj, nq * D)
+            else:
+                o = pa.paged_attention_decode_int8(q, kc.data, vc.data, kc.scale, vc.scale,
+                                                   block_tables, context_lens, block_size,
+                                                   self.scale, 0, kc._q_mult)
+                attn = L.o_proj(o.view(B, nq * D))
             nxt = self.layers[i + 1] if i + 1 < n else None
             nxt_w = nxt.input_layernorm if nxt is not None else self.norm
             if frag:

@@ -126,6 +126,44 @@ def paged_decode_int8(q, kc, vc, ks, vs, bt, cl, block_size, scale, partition_si
     return out
 
 
+def paged_decode_int8_xfrag(q, kc, vc, ks, vs, bt, cl, block_size, scale, partition_size=0,
+                            q_mult=None, act_inv=None):
+    """The decode whose merge also writes the [B, Hq*D] output times act_inv as activation
+    fragments: (out, fragment bytes)."""
+    B, Hq, D = q.shape
+    num_slots, Hk = kc.shape[0], kc.shape[1]
+    max_blocks = bt.shape[1]
+    out = torch.empty_like(q)
+    L = capi()
+    nbytes = L.llmserve_paged_attention_workspace_bytes(B, Hq, Hk, D, max_blocks, block_size,
+                                                        partition_size)
+    ws = torch.empty(max(nbytes, 4) // 4 + 4, dtype=torch.float32, device=q.device)
+    nx = L.llmserve_int4_xfrag_bytes(B, Hq * D)
+    xf = torch.empty(max(nx, 16), dtype=torch.uint8, device=q.device)
+    check(L.llmserve_paged_attention_decode_int8_xfrag(
+        _p(q), _p(kc), _p(vc), _p(ks), _p(vs), _p(bt), _p(cl), _p(out), _p(act_inv), _p(xf), B,
+        Hq, Hk, D, num_slots, max_blocks, block_size, float(scale), partition_size, _p(q_mult),
+        _p(ws), nbytes, _stream()))
+    return out, xf[:nx]
+
+
+def split_fragments(x, inv=None):
+    """The activation fragments of x * inv that llmserve_int4_linear_gemm_packed's split pass
+    leaves at the start of its workspace (run against a small packed weight)."""
+    M, K = x.shape
+    dev = x.device
+    nib = torch.zeros(64, K // 2, dtype=torch.uint8, device=dev)
+    gs = torch.ones(64, K // 128, dtype=torch.float32, device=dev)
+    packed = int4_gemm_pack(nib, gs, torch.zeros_like(gs), 128)
+    L = capi()
+    nbytes = L.llmserve_int4_linear_gemm_packed_workspace_bytes(M, K)
+    ws = torch.zeros(max(nbytes, 16) // 16 * 16 + 16, dtype=torch.uint8, device=dev)
+    y = torch.empty(M, 64, dtype=torch.float32, device=dev)
+    check(L.llmserve_int4_linear_gemm_packed(_p(x), _p(inv), _p(packed), _p(y), M, 64, K, 128,
+                                             _p(ws), nbytes, _stream()))
+    return ws[:L.llmserve_int4_xfrag_bytes(M, K)]
+
+
 def assert_rel_close(got, ref, tol: float, what: str = ""):
     """max|got - ref| <= tol * max|ref| and ||got - ref|| / ||ref|| <= tol."""
     g = np.asarray(got.detach().cpu() if isinstance(got, torch.Tensor) else got, np.float64)

@@ -158,6 +158,38 @@ def test_edge_contexts(gpu):
         assert np.isfinite(out[2]).all()
 
 
+@pytest.mark.parametrize("B,Hq,Hk,D,bs,part,with_inv,zero_ctx", [
+    (5, 4, 2, 128, 16, 0, True, False),     # 16-row padding of the fragments
+    (20, 8, 4, 256, 16, 0, False, False),   # two 128-channel blocks per head
+    (17, 16, 8, 128, 16, 64, True, False),  # fixed ranges: whole and split sequences
+    (6, 4, 2, 128, 8, 0, True, True),       # a zero context: NaN rows
+])
+def test_merge_writes_oproj_fragments(gpu, B, Hq, Hk, D, bs, part, with_inv, zero_ctx):
+    """The decode whose merge writes o_proj's input fragments: its output equals the plain
+    decode's bit for bit, and its fragments (x' = out * inv_act_scale, bf16 hi / lo, block
+    sums) equal those the packed int4 linear's split pass makes of that output."""
+    c = make_case(B * 7 + D, B, Hq, Hk, D, bs, 1, 700)
+    if zero_ctx:
+        c["cl"][1] = 0
+    args = [cu.dev(c[k]) for k in ("q", "kq", "vq", "ks", "vs", "bt", "cl")]
+    qm = cu.dev(c["q_mult"])
+    rng = np.random.default_rng(B)
+    inv = cu.dev((0.5 + rng.random(Hq * D)).astype(F32)) if with_inv else None
+    ref = cu.paged_decode_int8(*args, bs, D ** -0.5, part, qm)
+    out, xf = cu.paged_decode_int8_xfrag(*args, bs, D ** -0.5, part, qm, inv)
+    assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
+    if zero_ctx:
+        assert torch.isnan(out[1]).all() and torch.isfinite(out[0]).all()
+    assert torch.equal(xf, cu.split_fragments(ref.view(B, Hq * D), inv))
+
+
+def test_merge_fragments_reject_bad_head_dim(gpu):
+    c = make_case(3, 2, 4, 2, 64, 16, 1, 50)
+    args = [cu.dev(c[k]) for k in ("q", "kq", "vq", "ks", "vs", "bt", "cl")]
+    with pytest.raises(RuntimeError, match="128 or 256"):
+        cu.paged_decode_int8_xfrag(*args, 16, 0.125)
+
+
 def test_invalid_block_ids_are_skipped(gpu):
     c = make_case(6, 2, 8, 2, 32, 4, 12, 12, outlier=False)
     bt = c["bt"].copy()
