@@ -407,20 +407,29 @@ def c5_per_op(torch, dev, model, lm4, cache, runner) -> dict:
     kv_read = int(nk * (2 * D + 8) * ctx.double().sum().item())
     lay = model.layers
 
-    def frag_gemm(name, attr, N, K):
+    kc0, vc0 = cache.layers[0]
+    frags = {H: fo.add_rmsnorm_xfrag_(resid.clone(), x[H], lay[0].input_layernorm, None, eps),
+             I: fo.silu_mul_xfrag(gu, None),
+             nq * D: pa.paged_attention_decode_int8_xfrag(
+                 q, kc0.data, vc0.data, kc0.scale, vc0.scale, bt, ctx, bs, D ** -0.5, 0,
+                 kc0._q_mult, None)[1]}
+
+    def frag_gemm(name, lin_of, N, K, per_step=L):
         """the step's GEMM on activation fragments (their producer timed on its own)"""
-        xf = fo.add_rmsnorm_xfrag_(resid.clone(), x[H], lay[0].input_layernorm, None, eps) \
-            if K == H else fo.silu_mul_xfrag(gu, None)
+        xf = frags[K]
 
         def launch(i):
-            m = getattr(lay[i % L], attr)
-            fo.int4_linear_gemm_xfrag(xf, m.gemm_packed, B, N, K, GROUP)
-        return name, launch, int4_bytes(N, K, B), 2.0 * B * N * K, L
+            fo.int4_linear_gemm_xfrag(xf, lin_of(i).gemm_packed, B, N, K, GROUP)
+        return name, launch, int4_bytes(N, K, B), 2.0 * B * N * K, per_step
+
+    def lin(attr):
+        return lambda i: getattr(lay[i % L], attr)
 
     def attn(i):
         kc, vc = cache.layers[i % L]
-        pa.paged_attention_decode_int8(q, kc.data, vc.data, kc.scale, vc.scale, bt, ctx, bs,
-                                       D ** -0.5, 0, kc._q_mult)
+        pa.paged_attention_decode_int8_xfrag(q, kc.data, vc.data, kc.scale, vc.scale, bt, ctx, bs,
+                                             D ** -0.5, 0, kc._q_mult,
+                                             lay[i % L].o_proj.inv_act_scale)
 
     def qkv_kv(i):
         kc, vc = cache.layers[i % L]
@@ -428,30 +437,29 @@ def c5_per_op(torch, dev, model, lm4, cache, runner) -> dict:
                          lay[i % L].k_norm, eps, kc.smooth, kc.data, vc.data, kc.scale, vc.scale,
                          nq, nk, D)
 
-    def o_proj(i):
-        lay[i % L].o_proj(x[nq * D])
-
     ctx_save = ctx.clone()
     norm_bytes = 4 * B * H * 3 + 4 * B * H  # x read + written, r read, fragments (hi + lo)
     entries = [
-        frag_gemm("qkv_proj (int4 GEMM on fragments, 1024->4096)", "qkv_proj", (nq + 2 * nk) * D, H),
+        frag_gemm("qkv_proj (int4 GEMM on fragments, 1024->4096)", lin("qkv_proj"),
+                  (nq + 2 * nk) * D, H),
         ("decode_qkv_kv (norm + RoPE + KV write)", qkv_kv, 4 * B * (nq + 2 * nk) * D + 4 * B * nq * D
          + 2 * B * nk * (D + 4), 0.0, L),
-        ("paged_attention_decode_int8 (+ merge)", attn, kv_read + 8 * B * nq * D, 0.0, L),
-        ("o_proj (split pass + int4 GEMM, 2048->1024)", o_proj, int4_bytes(H, nq * D, B),
-         2.0 * B * H * nq * D, L),
+        ("paged_attention_decode_int8_xfrag (+ merge writing o_proj's fragments)", attn,
+         kv_read + 8 * B * nq * D + 4 * B * nq * D, 0.0, L),
+        frag_gemm("o_proj (int4 GEMM on fragments, 2048->1024)", lin("o_proj"), H, nq * D),
         ("add_rmsnorm_xfrag_ (residual + norm + next split)",
          lambda i: fo.add_rmsnorm_xfrag_(resid, x[H], lay[i % L].input_layernorm,
                                          lay[i % L].gate_up_proj.inv_act_scale, eps),
          norm_bytes, 0.0, 2 * L),
-        frag_gemm("gate_up_proj (int4 GEMM on fragments, 1024->6144)", "gate_up_proj", 2 * I, H),
+        frag_gemm("gate_up_proj (int4 GEMM on fragments, 1024->6144)", lin("gate_up_proj"),
+                  2 * I, H),
         ("silu_mul_xfrag (silu * up + down's split)",
          lambda i: fo.silu_mul_xfrag(gu, lay[i % L].down_proj.inv_act_scale), 4 * B * 3 * I, 0.0, L),
-        frag_gemm("down_proj (int4 GEMM on fragments, 3072->1024)", "down_proj", H, I),
+        frag_gemm("down_proj (int4 GEMM on fragments, 3072->1024)", lin("down_proj"), H, I),
         ("lm_head fp32 (hipBLASLt)", lambda i: model.compute_logits(x[H]),
          model.embed.numel() * 4 + 4 * B * (H + cfg.vocab_size), 2.0 * B * cfg.vocab_size * H, 1),
-        ("lm_head int4 (split pass + GEMM)", lambda i: lm4(x[H]), int4_bytes(cfg.vocab_size, H, B),
-         2.0 * B * cfg.vocab_size * H, 1),
+        frag_gemm("lm_head int4 (GEMM on fragments, 1024->151936)", lambda i: lm4,
+                  cfg.vocab_size, H, 1),
         ("argmax_advance", lambda i: fo.argmax_advance(logits, ctx), 4 * B * cfg.vocab_size, 0.0, 1),
     ]
     res = {}
