@@ -456,7 +456,10 @@ def c5_per_op(torch, dev, model, lm4, cache, runner) -> dict:
         ("silu_mul_xfrag (silu * up + down's split)",
          lambda i: fo.silu_mul_xfrag(gu, lay[i % L].down_proj.inv_act_scale), 4 * B * 3 * I, 0.0, L),
         frag_gemm("down_proj (int4 GEMM on fragments, 3072->1024)", lin("down_proj"), H, I),
-        ("lm_head fp32 (hipBLASLt)", lambda i: model.compute_logits(x[H]),
+        ("lm_head fp32 (hipBLASLt, torch.mm)", lambda i: torch.mm(x[H], model.lm_weight.t()),
+         model.embed.numel() * 4 + 4 * B * (H + cfg.vocab_size), 2.0 * B * cfg.vocab_size * H, 1),
+        ("lm_head fp32 (split-bf16 matrix cores on fragments: the step's)",
+         lambda i: fo.lm_head_f32_xfrag(frags[H], model.lm_weight, B),
          model.embed.numel() * 4 + 4 * B * (H + cfg.vocab_size), 2.0 * B * cfg.vocab_size * H, 1),
         frag_gemm("lm_head int4 (GEMM on fragments, 1024->151936)", lambda i: lm4,
                   cfg.vocab_size, H, 1),

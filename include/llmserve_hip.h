@@ -284,6 +284,17 @@ int llmserve_argmax_advance(const float* logits, int64_t T, int64_t V, int64_t* 
                             int64_t* context_lens, void* workspace, int64_t workspace_bytes,
                             void* stream);
 
+/*
+ * fp32 LM head on activation fragments (replaces the tied-embedding lm_head,
+ * models/transformer.py:192-193): y[M, V] = x[M, K] . w[V, K]^T with w fp32 row-major and x
+ * given as llmserve_int4_xfrag_bytes(M, K) bytes of fragments (written, e.g., by
+ * llmserve_add_rmsnorm_xfrag with act_inv = NULL). Split-bf16 matrix-core products (x and w
+ * each as bf16 hi + lo, four products, fp32 accumulation): within a few 1e-6 relative of
+ * fp32. K a multiple of 128; xfrag, w and y 16-byte aligned.
+ */
+int llmserve_lm_head_f32_xfrag(const void* xfrag, const float* w, float* y, int64_t M, int64_t V,
+                               int64_t K, void* stream);
+
 /* ---- int8-KV paged decode attention ------------------------------------------------------ */
 
 /*

@@ -1,0 +1,233 @@
+// fp32 LM head of the decode step on activation fragments (replaces the tied-embedding
+// lm_head of models/transformer.py:192-193, F.linear(h, embed.weight)):
+//   y[m, v] = sum_k x[m, k] * W[v, k]      W fp32 [V, K] row-major (the embedding matrix)
+// x arrives as the bf16 hi / lo fragments of xfrag.h (x = xh + xl to 2^-16 relative); each W
+// value is split the same way in registers (W = wh + wl), and the four products
+// wh*xh + wh*xl + wl*xh + wl*xl go through v_mfma_f32_16x16x32_bf16 (each product of two bf16
+// values is exact in fp32) with fp32 accumulation. Only the two split residuals are lost:
+// each product is within ~2^-15 of fp32, the sums within a few 1e-6 relative.
+//
+// The kernel streams W once (622 MB at Qwen3-0.6B: HBM-bound). A workgroup of 4 wavefronts
+// (one per resident slot, looping over vocab tiles) owns 64 vocab rows at a time (16 per wavefront, the matrix-core A operand: lane l holds row l % 16,
+// channels 32 (l / 16) .. + 32 of each 128-channel block, 128 contiguous bytes) and up to 4
+// row tiles of x (64 rows, the B operand, straight from the fragment layout). Per block of
+// 128 channels the x fragments (8 KB per row tile) are staged in LDS, double-buffered, for all
+// 4 wavefronts; W (8 KB per wavefront and block) is loaded two blocks ahead and x one block
+// ahead, before the current block's 64 MFMAs. The output lane holds vocab
+// rows 4 (l / 16) .. + 4 of batch row l % 16: one 16-byte store.
+#include "common.h"
+#include "xfrag.h"
+
+namespace {
+
+using lsh::kWave;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;                 // wavefronts per workgroup
+constexpr int kVRows = 16 * kWaves;       // vocab rows per workgroup
+constexpr int kMaxTiles = 4;              // 16-row tiles of x per pass (64 rows)
+constexpr int kTilePieces = 512;          // 16-byte pieces of one (row tile, block) fragment
+constexpr int kBlkElems = 4 * 2 * kWave * 8;  // bf16 of one (row tile, block) fragment
+
+struct LmArgs {
+  const __bf16* xf;  // fragments of x [mp, K]
+  const float* w;    // [V, K]
+  float* y;          // [M, V]
+  int M, V, K, nblk;
+};
+
+// W row chunk -> bf16 hi / lo A operands of step q (8 channels).
+__device__ __forceinline__ void split_w(const u32x4& p0, const u32x4& p1, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = __builtin_bit_cast(float, e < 4 ? p0[e] : p1[e - 4]);
+    __bf16 h, l;
+    lsh::split_bf16(v, h, l);
+    hi[e] = h;
+    lo[e] = l;
+  }
+}
+
+// T: row tiles of this pass (blockIdx.y selects which). Workgroup g runs the vocab tiles
+// g, g + gridDim.x, ... as one stream of (tile, block) steps, so the loads ahead run across
+// tile boundaries; a tile's logits are stored after its last block.
+template <int T>
+__global__ __launch_bounds__(kWaves * kWave) void lm_head_f32_kernel(LmArgs a) {
+  __shared__ u32x4 xs[2][T * kTilePieces];
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int tile0 = blockIdx.y * kMaxTiles;
+  const int ntiles = (a.V + kVRows - 1) / kVRows;
+  const int mine = (ntiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
+                   static_cast<int>(gridDim.x);  // >= 1: the host launches at most ntiles
+  const int nsteps = mine * a.nblk;
+  const int lastw = nsteps - 1;
+  const u32x4* xg = reinterpret_cast<const u32x4*>(a.xf);
+
+  // W rows of step s: vocab tile blockIdx.x + (s / nblk) gridDim.x, block s % nblk
+  auto vtile = [&](int s) { return static_cast<int>(blockIdx.x) + (s / a.nblk) * static_cast<int>(gridDim.x); };
+
+  // x staging: piece p = tid + 256 i of the T (row tile, block) fragments
+  constexpr int kPer = T * kTilePieces / (kWaves * kWave);
+  auto load_x = [&](int b, u32x4 (&r)[kPer]) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int p = tid + i * kWaves * kWave;
+      const int t = p / kTilePieces, within = p % kTilePieces;
+      r[i] = xg[(static_cast<int64_t>(tile0 + t) * a.nblk + b) * kTilePieces + within];
+    }
+  };
+  auto store_x = [&](int buf, const u32x4 (&r)[kPer]) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) xs[buf][tid + i * kWaves * kWave] = r[i];
+  };
+  // a lane's 128 contiguous bytes of its W row in the block (kept in L1 over the 8 loads)
+  auto load_w = [&](int s, u32x4 (&r)[8]) {
+    const int v = vtile(s) * kVRows + wave * 16 + lane % 16;
+    const int vr = v < a.V ? v : a.V - 1;  // loads stay in bounds
+    const u32x4* p = reinterpret_cast<const u32x4*>(a.w + static_cast<int64_t>(vr) * a.K +
+                                                    (s % a.nblk) * lsh::kFragBlk + 32 * (lane / 16));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = p[i];
+  };
+
+  f32x4 acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // lane: vocab rows 4 (lane / 16) .. + 4 of the wavefront's 16, batch row 16 t + lane % 16
+  auto store_tile = [&](int s) {
+    const int vo = vtile(s) * kVRows + wave * 16 + 4 * (lane / 16);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int m = 16 * (tile0 + t) + lane % 16;
+      if (m < a.M) {
+        float* yo = a.y + static_cast<int64_t>(m) * a.V + vo;
+        if (vo + 3 < a.V && (a.V & 3) == 0) {
+          *reinterpret_cast<f32x4*>(yo) = acc[t];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (vo + r < a.V) yo[r] = acc[t][r];
+        }
+      }
+      acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  // W runs two steps ahead in three register sets used in turn (a copy from one set to
+  // another would wait for the loads); x runs one step ahead through the LDS buffers.
+  u32x4 w0[8], w1[8], w2[8], xn[kPer];
+  load_w(0, w0);
+  load_x(0, xn);
+  load_w(lastw < 1 ? lastw : 1, w1);
+  store_x(0, xn);
+  __syncthreads();
+  auto step = [&](int s, const u32x4 (&wc)[8], u32x4 (&wn)[8]) {
+    const int cur = s & 1;
+    const int sx = s + 1 < lastw ? s + 1 : lastw;  // past the end: reload the last (unused)
+    const int sw = s + 2 < lastw ? s + 2 : lastw;
+    // The loads ahead go out before this step's products: x first, so that its LDS store
+    // after the products waits for x (and the older W) only -- vmcnt counts in issue order --
+    // and W of step s + 2 stays in flight over the barrier; the scheduling barriers keep
+    // that order and keep the loads from sinking.
+    load_x(sx % a.nblk, xn);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(sw, wn);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bf16x8 wh, wl;
+      split_w(wc[2 * q], wc[2 * q + 1], wh, wl);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const bf16x8 xh = __builtin_bit_cast(bf16x8, xs[cur][t * kTilePieces + (q * 2) * kWave + lane]);
+        const bf16x8 xl = __builtin_bit_cast(bf16x8, xs[cur][t * kTilePieces + (q * 2 + 1) * kWave + lane]);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, xh, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, xl, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wl, xh, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wl, xl, acc[t], 0, 0, 0);
+      }
+    }
+    if (s % a.nblk == a.nblk - 1) store_tile(s);
+    store_x(cur ^ 1, xn);  // every wavefront finished reading this buffer before the last barrier
+    __syncthreads();
+  };
+  int s = 0;
+  for (; s + 2 < nsteps; s += 3) {
+    step(s, w0, w2);
+    step(s + 1, w1, w0);
+    step(s + 2, w2, w1);
+  }
+  if (s < nsteps) step(s, w0, w2);
+  if (s + 1 < nsteps) step(s + 1, w1, w0);
+}
+
+// Resident workgroups of the kernel on the current device (cached per device).
+template <int T>
+int lm_resident() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, lm_head_f32_kernel<T>, kWaves * kWave, 0) !=
+            hipSuccess || per < 1)
+      per = 1;
+    cached[dev] = cus * per;
+  }
+  return cached[dev];
+}
+
+template <int T>
+void launch_lm(const LmArgs& a, int passes, bool last, hipStream_t st) {
+  const int ntiles = (a.V + kVRows - 1) / kVRows;
+  const int res = lm_resident<T>();
+  const int g = ntiles < res ? ntiles : res;
+  lsh::launch(lm_head_f32_kernel<T>, dim3(static_cast<unsigned>(g), static_cast<unsigned>(passes)),
+              dim3(kWaves * kWave), 0, st, last, a);
+}
+
+}  // namespace
+
+extern "C" int llmserve_lm_head_f32_xfrag(const void* xfrag, const float* w, float* y, int64_t M,
+                                          int64_t V, int64_t K, void* stream) {
+  LSH_CHECK(M >= 0 && V >= 1 && K >= 1, "lm_head_f32_xfrag: bad shape");
+  LSH_CHECK(K % lsh::kFragBlk == 0, "lm_head_f32_xfrag: K must be a multiple of 128");
+  LSH_CHECK(M < (1LL << 24) && V < (1LL << 31) && V * K < (1LL << 40) && M * V < (1LL << 40),
+            "lm_head_f32_xfrag: shape too large");
+  if (M == 0) return LLMSERVE_OK;
+  LSH_CHECK(xfrag && w && y, "lm_head_f32_xfrag: null pointer");
+  LSH_CHECK(lsh::aligned16(xfrag) && lsh::aligned16(w) && lsh::aligned16(y),
+            "lm_head_f32_xfrag: xfrag, w and y must be 16-byte aligned");
+  LmArgs a{static_cast<const __bf16*>(xfrag), w, y, static_cast<int>(M), static_cast<int>(V),
+           static_cast<int>(K), static_cast<int>(K / lsh::kFragBlk)};
+  const int64_t tiles = lsh::frag_rows(M) / 16;
+  hipStream_t st = lsh::as_stream(stream);
+  if (tiles >= kMaxTiles) {
+    // full passes of 4 row tiles; a remainder of 1-3 tiles runs as one more launch
+    const int full = static_cast<int>(tiles / kMaxTiles);
+    const int rem = static_cast<int>(tiles % kMaxTiles);
+    launch_lm<kMaxTiles>(a, full, rem == 0, st);
+    if (rem > 0) {
+      LmArgs r = a;
+      const int64_t off_tiles = static_cast<int64_t>(full) * kMaxTiles;
+      r.xf = a.xf + off_tiles * a.nblk * kBlkElems;
+      r.y = a.y + off_tiles * 16 * V;
+      r.M = static_cast<int>(M - off_tiles * 16);
+      if (rem == 1) launch_lm<1>(r, 1, true, st);
+      else if (rem == 2) launch_lm<2>(r, 1, true, st);
+      else launch_lm<3>(r, 1, true, st);
+    }
+  } else if (tiles == 1) {
+    launch_lm<1>(a, 1, true, st);
+  } else if (tiles == 2) {
+    launch_lm<2>(a, 1, true, st);
+  } else {
+    launch_lm<3>(a, 1, true, st);
+  }
+  return lsh::launch_status("lm_head_f32_xfrag");
+}

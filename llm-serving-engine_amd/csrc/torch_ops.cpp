@@ -514,6 +514,22 @@ at::Tensor int4_linear_gemm_xfrag(const at::Tensor& xfrag, const at::Tensor& pac
 
 // ---- int8-KV paged decode -------------------------------------------------------------------
 
+at::Tensor lm_head_f32_xfrag(const at::Tensor& xfrag, const at::Tensor& w, int64_t M) {
+  TORCH_CHECK(xfrag.scalar_type() == at::kByte && xfrag.is_contiguous(),
+              "lm_head_f32_xfrag: xfrag must be a contiguous uint8 fragment buffer");
+  TORCH_CHECK(w.scalar_type() == at::kFloat && w.is_contiguous() && w.dim() == 2,
+              "lm_head_f32_xfrag: w must be a contiguous float32 [V, K] tensor");
+  check_device(w, {&xfrag}, "lm_head_f32_xfrag");
+  const int64_t V = w.size(0), K = w.size(1);
+  TORCH_CHECK(M >= 0 && xfrag.numel() >= llmserve_int4_xfrag_bytes(M, K),
+              "lm_head_f32_xfrag: xfrag holds fewer than M rows of K channels");
+  const c10::DeviceGuard guard(w.device());
+  auto y = at::empty({M, V}, w.options());
+  check_status(llmserve_lm_head_f32_xfrag(xfrag.data_ptr(), w.data_ptr<float>(),
+                                          y.data_ptr<float>(), M, V, K, stream_of(w)));
+  return y;
+}
+
 // Checks of the paged decode's tensors (dtypes, shapes, devices, contiguity).
 void check_paged(const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
                  const at::Tensor& k_scale, const at::Tensor& v_scale,
@@ -638,6 +654,7 @@ TORCH_LIBRARY(llmserve_hip, m) {
   m.def("int4_linear_gemm_xfrag(Tensor xfrag, Tensor packed, int M, int N, int K, int group_size)"
         " -> Tensor");
   m.def("silu_mul(Tensor gate_up) -> Tensor");
+  m.def("lm_head_f32_xfrag(Tensor xfrag, Tensor w, int M) -> Tensor");
   m.def("rope_qk_(Tensor(a!) qkv, Tensor cos, Tensor sin, int n_q, int n_k, int head_dim,"
         " Tensor? q_w=None, Tensor? k_w=None, float eps=1e-6) -> ()");
   m.def("decode_qkv_kv(Tensor qkv, Tensor cos_table, Tensor sin_table, Tensor context_lens,"
@@ -672,6 +689,7 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("silu_mul_xfrag", &silu_mul_xfrag);
   m.impl("int4_linear_gemm_xfrag", &int4_linear_gemm_xfrag);
   m.impl("silu_mul", &silu_mul);
+  m.impl("lm_head_f32_xfrag", &lm_head_f32_xfrag);
   m.impl("rope_qk_", &rope_qk_);
   m.impl("decode_qkv_kv", &decode_qkv_kv);
   m.impl("argmax_advance", &argmax_advance);

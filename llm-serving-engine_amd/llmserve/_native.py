@@ -77,6 +77,7 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
     ),
     "llmserve_argmax_advance_workspace_bytes": (_I64, [_I64]),
     "llmserve_argmax_advance": (_I32, [_P, _I64, _I64, _P, _P, _P, _I64, _P]),
+    "llmserve_lm_head_f32_xfrag": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "llmserve_paged_attention_workspace_bytes": (_I64, [_I64] * 7),
     "llmserve_paged_attention_decode_int8": (
         _I32,

@@ -86,6 +86,7 @@ def load_fused_ops() -> SimpleNamespace:
         embed_rmsnorm_xfrag=o.embed_rmsnorm_xfrag,
         silu_mul_xfrag=o.silu_mul_xfrag,
         int4_linear_gemm_xfrag=o.int4_linear_gemm_xfrag,
+        lm_head_f32_xfrag=o.lm_head_f32_xfrag,
         silu_mul=o.silu_mul,
         rope_qk_=o.rope_qk_,
         decode_qkv_kv=o.decode_qkv_kv,

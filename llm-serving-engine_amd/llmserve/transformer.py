@@ -145,11 +145,14 @@ class QuantCausalLM(nn.Module):
         self.register_buffer("rope_sin", sin.to(dev))
         self.scale = D ** -0.5
 
-    # Where the linears run the packed matrix-core kernel (above the GEMV's rows) the norms
-    # and silu * up write the next linear's activation
-    # fragments directly (its x * inv_act_scale and bf16 split fused in), and the linears run
-    # the packed matrix-core kernel on them: one launch less per linear, same result bits.
+    # Where the linears run the packed matrix-core kernel (above the GEMV's rows) the norms,
+    # silu * up and the attention merge write the next linear's activation fragments directly
+    # (its x * inv_act_scale and bf16 split fused in), and the linears run the packed
+    # matrix-core kernel on them: one launch less per linear, same result bits.
     fuse_xfrag = True
+    # With fragments, the fp32 LM head runs the split-bf16 matrix-core kernel
+    # (lm_head_f32_xfrag, within a few 1e-6 of fp32) instead of torch.mm (hipBLASLt).
+    fp32_head_kernel = True
 
     def _xfrag_ok(self, rows: int) -> bool:
         lins = [m for L in self.layers for m in (L.qkv_proj, L.o_proj, L.gate_up_proj, L.down_proj)]
@@ -207,7 +210,8 @@ class QuantCausalLM(nn.Module):
                 if nxt is not None:
                     h = fo.add_rmsnorm_xfrag_(x, down, nxt_w, nxt.qkv_proj.inv_act_scale, eps)
                 elif self._lm_frag(B):
-                    h = fo.add_rmsnorm_xfrag_(x, down, nxt_w, self.lm_head.inv_act_scale, eps)
+                    inv = self.lm_head.inv_act_scale if self.lm_head is not None else None
+                    h = fo.add_rmsnorm_xfrag_(x, down, nxt_w, inv, eps)
                 else:
                     h = fo.add_rmsnorm_(x, down, nxt_w, eps)
             else:
@@ -217,14 +221,22 @@ class QuantCausalLM(nn.Module):
         return h
 
     def _lm_frag(self, rows: int) -> bool:
+        """The LM head reads the final norm's activation fragments: the int4 head on its packed
+        weight, or the fp32 head's split-bf16 matrix-core kernel (``fp32_head_kernel``)."""
         m = self.lm_head
-        return self._xfrag_ok(rows) and m is not None and m.packed_path(rows)
+        if not self._xfrag_ok(rows):
+            return False
+        if m is not None:
+            return m.packed_path(rows)
+        return self.fp32_head_kernel and self.cfg.hidden_size % 128 == 0
 
     def compute_logits(self, hidden: torch.Tensor, rows: int | None = None) -> torch.Tensor:
         """lm_head (transformer.py:192-193): fp32 [B, V]. ``hidden`` is the fp32 [B, H] final
         norm output, or (``rows`` given) the int4 LM head's activation fragments."""
         if rows is not None:
             m = self.lm_head
+            if m is None:
+                return load_fused_ops().lm_head_f32_xfrag(hidden, self.lm_weight, rows)
             return load_fused_ops().int4_linear_gemm_xfrag(hidden, m.gemm_packed, rows,
                                                            m.out_features, m.in_features,
                                                            m.group_size)

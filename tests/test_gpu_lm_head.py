@@ -1,0 +1,56 @@
+"""fp32 LM head on activation fragments (llmserve_lm_head_f32_xfrag) against float64.
+
+x and W are each split into bf16 hi + lo (exact to ~2^-16 relative) and the four products
+accumulate in fp32, so the logits are within a few 1e-6 of fp32; the bound here is
+max-abs <= 2e-5 * max|ref| and rel-L2 <= 2e-5 against x . W^T in float64. Shapes cover a
+partial row tile (rows past M are zero fragments and are not stored), several 64-row passes
+plus a remainder, and vocab sizes that are not multiples of 64 or 4 (clamped loads, scalar
+stores). The decode step's use of it is checked against the step oracle in test_gpu_step.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import capi_util as cu
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-5
+
+
+def _lm_head(xf, w, M):
+    V, K = w.shape
+    y = torch.empty(M, V, dtype=torch.float32, device=w.device)
+    cu.check(cu.capi().llmserve_lm_head_f32_xfrag(cu._p(xf), cu._p(w), cu._p(y), M, V, K,
+                                                   cu._stream()))
+    return y
+
+
+@pytest.mark.parametrize("M,V,K", [(5, 1000, 256), (64, 4096, 1024), (70, 777, 512),
+                                   (130, 2050, 384), (16, 4099, 128)])
+def test_lm_head_f32_matches_f64(gpu, M, V, K):
+    rng = np.random.default_rng(M * 7 + V)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (0.02 * rng.standard_normal((V, K))).astype(np.float32)
+    xd, wd = cu.dev(x), cu.dev(w)
+    y = _lm_head(cu.split_fragments(xd), wd, M)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    cu.assert_rel_close(y, ref, TOL, f"M{M} V{V} K{K}")
+
+
+def test_lm_head_op_and_rejects(gpu):
+    from llmserve.kernels import load_fused_ops
+
+    fo = load_fused_ops()
+    rng = np.random.default_rng(3)
+    x = cu.dev(rng.standard_normal((20, 256)).astype(np.float32))
+    w = cu.dev(rng.standard_normal((300, 256)).astype(np.float32))
+    xf = cu.split_fragments(x)
+    y = fo.lm_head_f32_xfrag(xf, w, 20)
+    assert torch.equal(y, _lm_head(xf, w, 20))
+    with pytest.raises(RuntimeError, match="fewer than M rows"):
+        fo.lm_head_f32_xfrag(xf[:100], w, 20)
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        _lm_head(xf, cu.dev(np.zeros((300, 200), np.float32)), 20)
