@@ -7,14 +7,16 @@
 // values is exact in fp32) with fp32 accumulation. Only the two split residuals are lost:
 // each product is within ~2^-15 of fp32, the sums within a few 1e-6 relative.
 //
-// The kernel streams W once (622 MB at Qwen3-0.6B: HBM-bound). A workgroup of 4 wavefronts
-// (one per resident slot, looping over vocab tiles) owns 64 vocab rows at a time (16 per wavefront, the matrix-core A operand: lane l holds row l % 16,
-// channels 32 (l / 16) .. + 32 of each 128-channel block, 128 contiguous bytes) and up to 4
-// row tiles of x (64 rows, the B operand, straight from the fragment layout). Per block of
-// 128 channels the x fragments (8 KB per row tile) are staged in LDS, double-buffered, for all
-// 4 wavefronts; W (8 KB per wavefront and block) is loaded two blocks ahead and x one block
-// ahead, before the current block's 64 MFMAs. The output lane holds vocab
-// rows 4 (l / 16) .. + 4 of batch row l % 16: one 16-byte store.
+// The kernel streams W once (622 MB at Qwen3-0.6B: HBM-bound). A workgroup of 8 wavefronts
+// (about one per CU, looping over vocab tiles) owns 128 vocab rows at a time, 16 per
+// wavefront, and up to 4 row tiles of x (64 rows, the B operand, straight from the fragment
+// layout). Per block of 128 channels:
+//   * x (8 KB per row tile) is staged in LDS for all wavefronts, double-buffered, one block
+//     ahead;
+//   * each lane loads its A operand directly: row l % 16, channels 32 (l / 16) .. + 32, one
+//     128-byte line kept in L1 over its 8 loads, two blocks ahead (8 KB per wavefront);
+//   * 4 steps x 4 row tiles x 4 products = 64 MFMAs.
+// The output lane holds vocab rows 4 (l / 16) .. + 4 of batch row l % 16: one 16-byte store.
 #include "common.h"
 #include "xfrag.h"
 
