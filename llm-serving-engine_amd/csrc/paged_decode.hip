@@ -457,6 +457,68 @@ __global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_int8_k
 // per lane), then their acc rows, kMergeBatch partials at a time with all loads in flight.
 constexpr int kMergeBatch = 16;
 
+// Combines np >= 1 partials of one (sequence, q head) into this lane's N output elements:
+//   M = max_j m_j;  w_j = exp2(m_j - M) (0 where l_j = 0);  o[e] = sum_j w_j acc_j[e] in j
+//   order;  returns L = sum_j w_j l_j (the same bits in every lane).
+// ml(p) points at (m, l) of partial p; row(p) at this lane's first accumulator element of
+// partial p, its N elements STEP floats apart. The (m, l) of the first 64 partials and the
+// accumulator rows of the first kMergeBatch go out together: they do not depend on each other.
+template <int N, int STEP, typename ML, typename ROW>
+__device__ __forceinline__ float merge_partials(int np, ML ml, ROW row, float (&o)[N]) {
+  const int lane = threadIdx.x % kWave;
+  float v0[kMergeBatch][N];
+#pragma unroll
+  for (int j = 0; j < kMergeBatch; ++j) {
+    const float* src = row(j < np ? j : np - 1);  // in-bounds row; its weight is zeroed below
+#pragma unroll
+    for (int e = 0; e < N; ++e) v0[j][e] = src[e * STEP];
+  }
+  float m0 = kNegBig, l0 = 0.f;
+  if (lane < np) {
+    m0 = ml(lane)[0];
+    l0 = ml(lane)[1];
+  }
+  float M = m0;
+  for (int p = lane + kWave; p < np; p += kWave) M = fmaxf(M, ml(p)[0]);
+  M = lsh::wave_max_from<1>(M);
+  float L = 0.f;
+#pragma unroll
+  for (int e = 0; e < N; ++e) o[e] = 0.f;
+  for (int p0 = 0; p0 < np; p0 += kWave) {
+    float w = 0.f;
+    if (p0 + lane < np) {
+      const float mp = p0 == 0 ? m0 : ml(p0 + lane)[0];
+      const float lp = p0 == 0 ? l0 : ml(p0 + lane)[1];
+      w = lp == 0.f ? 0.f : __builtin_amdgcn_exp2f(mp - M);
+      L += w * lp;
+    }
+    const int n = np - p0 < kWave ? np - p0 : kWave;
+    for (int j0b = 0; j0b < n; j0b += kMergeBatch) {
+      float v[kMergeBatch][N];
+      if (p0 == 0 && j0b == 0) {
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j)
+#pragma unroll
+          for (int e = 0; e < N; ++e) v[j][e] = v0[j][e];
+      } else {
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+          const float* src = row(p0 + (j0b + j < n ? j0b + j : n - 1));
+#pragma unroll
+          for (int e = 0; e < N; ++e) v[j][e] = src[e * STEP];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        const float wj = j0b + j < n ? __shfl(w, j0b + j, kWave) : 0.f;
+#pragma unroll
+        for (int e = 0; e < N; ++e) o[e] += wj * v[j][e];
+      }
+    }
+  }
+  return lsh::group_sum<kWave>(L);  // the same bits in every lane (xor / mirror steps)
+}
+
 template <int D>
 __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int PER = (D + kWave - 1) / kWave;
@@ -493,47 +555,15 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_kernel
   const int64_t g0 = pre * a.NHG + hg * ctx;
   const int64_t j0 = g0 / Q, j1 = (g0 + ctx - 1) / Q;
   if (j0 == j1) return;
-  // partial of range j0 + p: slot base + p * HB
+  // partial of range j0 + p: slot base + p * HB; lane holds dims lane + 64 i
   const int64_t base = ((static_cast<int64_t>(b) * a.NHG + hg) + j0) * a.HB + h % a.HB;
   const int np = static_cast<int>(j1 - j0 + 1);
-  auto ml = [&](int p) { return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2; };
-  float M = kNegBig;
-  for (int p = lane; p < np; p += kWave) M = fmaxf(M, ml(p)[0]);
-  M = lsh::wave_max_from<1>(M);
-  float L = 0.f, o[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) o[i] = 0.f;
-  for (int p0 = 0; p0 < np; p0 += kWave) {
-    float w = 0.f;
-    if (p0 + lane < np) {
-      const float* pm = ml(p0 + lane);
-      const float lp = pm[1];
-      w = lp == 0.f ? 0.f : __builtin_amdgcn_exp2f(pm[0] - M);
-      L += w * lp;
-    }
-    const int n = np - p0 < kWave ? np - p0 : kWave;
-    for (int j0b = 0; j0b < n; j0b += kMergeBatch) {
-      float v[kMergeBatch][PER];
-#pragma unroll
-      for (int j = 0; j < kMergeBatch; ++j) {
-        const int jj = j0b + j < n ? j0b + j : n - 1;  // in-bounds row; its weight is zeroed below
-        const float* src =
-            a.part_acc + ((base + static_cast<int64_t>(p0 + jj) * a.HB) * G + g) * D;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-          const int d = lane + i * kWave;
-          v[j][i] = d < D ? src[d] : 0.f;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kMergeBatch; ++j) {
-        const float wj = j0b + j < n ? __shfl(w, j0b + j, kWave) : 0.f;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) o[i] += wj * v[j][i];
-      }
-    }
-  }
-  L = lsh::group_sum<kWave>(L);  // the same bits in every lane (xor / mirror steps)
+  const int dl = lane < D ? lane : 0;  // D < 64: lanes past D read dim 0 and write nothing
+  float o[PER];
+  const float L = merge_partials<PER, kWave>(
+      np, [&](int p) { return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2; },
+      [&](int p) { return a.part_acc + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * D + dl; },
+      o);
   const float inv = 1.f / L;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -601,43 +631,13 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_frag_k
     } else {
       const int64_t base = ((static_cast<int64_t>(b) * a.NHG + hg) + j0) * a.HB + h % a.HB;
       const int np = static_cast<int>(j1 - j0 + 1);
-      auto ml = [&](int p) {
-        return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2;
-      };
-      float M = kNegBig;
-      for (int p = lane; p < np; p += kWave) M = fmaxf(M, ml(p)[0]);
-      M = lsh::wave_max_from<1>(M);
-      float L = 0.f, o[CPL];
-#pragma unroll
-      for (int e = 0; e < CPL; ++e) o[e] = 0.f;
-      for (int p0 = 0; p0 < np; p0 += kWave) {
-        float w = 0.f;
-        if (p0 + lane < np) {
-          const float* pm = ml(p0 + lane);
-          const float lp = pm[1];
-          w = lp == 0.f ? 0.f : __builtin_amdgcn_exp2f(pm[0] - M);
-          L += w * lp;
-        }
-        const int n = np - p0 < kWave ? np - p0 : kWave;
-        for (int j0b = 0; j0b < n; j0b += kMergeBatch) {
-          float v[kMergeBatch][CPL];
-#pragma unroll
-          for (int j = 0; j < kMergeBatch; ++j) {
-            const int jj = j0b + j < n ? j0b + j : n - 1;  // in-bounds row; weight zeroed below
-            const float* src = a.part_acc +
-                               ((base + static_cast<int64_t>(p0 + jj) * a.HB) * G + g) * D + lane * CPL;
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) v[j][e] = src[e];
-          }
-#pragma unroll
-          for (int j = 0; j < kMergeBatch; ++j) {
-            const float wj = j0b + j < n ? __shfl(w, j0b + j, kWave) : 0.f;
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) o[e] += wj * v[j][e];
-          }
-        }
-      }
-      L = lsh::group_sum<kWave>(L);  // the same bits in every lane (xor / mirror steps)
+      float o[CPL];
+      const float L = merge_partials<CPL, 1>(
+          np, [&](int p) { return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2; },
+          [&](int p) {
+            return a.part_acc + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * D + lane * CPL;
+          },
+          o);
       const float inv = 1.f / L;
 #pragma unroll
       for (int e = 0; e < CPL; ++e) {
