@@ -552,6 +552,18 @@ def profile_only(torch, dev, what: str) -> int:
         for i in range(64):
             kq, vq, ks, vs, bt = copies[i % len(copies)]
             pa.paged_attention_decode_int8(q, kq, vq, ks, vs, bt, cl, bs, D ** -0.5, 0, qm)
+    elif what == "lmhead":  # config 5's fp32 LM head 1024 -> 151936 at 64 rows, 2 weight copies
+        from llmserve.kernels import load_fused_ops
+
+        fo = load_fused_ops()
+        V, H, B = 151936, 1024, 64
+        g = torch.Generator(device=dev).manual_seed(6)
+        ws = [torch.randn(V, H, device=dev, generator=g) * 0.02 for _ in range(2)]
+        r = torch.randn(B, H, device=dev, generator=g)
+        xf = fo.add_rmsnorm_xfrag_(torch.randn(B, H, device=dev, generator=g), r,
+                                   torch.ones(H, device=dev), None, 1e-6)
+        for i in range(32):
+            fo.lm_head_f32_xfrag(xf, ws[i % 2], B)
     else:  # copy of 256 MiB: the reference for scaling FETCH_SIZE / WRITE_SIZE
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).random_(0, 255)
         dst = torch.empty_like(src)
@@ -569,7 +581,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
-    ap.add_argument("--only", choices=["gemv", "gemm4", "attention", "prefill", "copy"],
+    ap.add_argument("--only", choices=["gemv", "gemm4", "attention", "prefill", "lmhead", "copy"],
                     help="profiling run: only launch that kernel (64 times) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
