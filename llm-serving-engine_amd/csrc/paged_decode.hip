@@ -655,17 +655,17 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_frag_k
   if (lane % LPB == 0) xsum[static_cast<int64_t>(c0 / lsh::kFragBlk) * mp + b] = sum;
 }
 
-// Resident workgroups of `waves` wavefronts of a kernel on the current device: CUs x blocks
-// per CU (cached per kernel, device and workgroup size).
-template <typename K>
-int resident_blocks(K kernel, int waves) {
+// Resident workgroups of `waves` wavefronts of `Kernel` on the current device: CUs x blocks
+// per CU (cached per kernel -- one instantiation each --, device and workgroup size).
+template <auto Kernel>
+int resident_blocks(int waves) {
   static int cached[64][kMaxHeadsPerBlock + 1] = {};  // [device][waves]
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   if (cached[dev][waves] == 0) {
     int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, waves * kWave, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, Kernel, waves * kWave, 0) != hipSuccess ||
         per < 1)
       per = 1;
     cached[dev][waves] = cus * per;
@@ -691,9 +691,9 @@ bool scalar_blocks(int64_t D, int64_t block_size) {
 // cache size).
 template <int D, int G>
 int decode_blocks(bool scalar, int off32, int hb) {
-  if (!scalar) return resident_blocks(paged_decode_int8_kernel<D, G, false, false>, hb);
-  const int w32 = resident_blocks(paged_decode_int8_kernel<D, G, true, true>, hb);
-  const int w64 = resident_blocks(paged_decode_int8_kernel<D, G, true, false>, hb);
+  if (!scalar) return resident_blocks<paged_decode_int8_kernel<D, G, false, false>>(hb);
+  const int w32 = resident_blocks<paged_decode_int8_kernel<D, G, true, true>>(hb);
+  const int w64 = resident_blocks<paged_decode_int8_kernel<D, G, true, false>>(hb);
   return off32 > 0 ? w32 : (off32 == 0 ? w64 : (w32 > w64 ? w32 : w64));
 }
 
