@@ -5,9 +5,10 @@
 // (reference quant.py:71-72, dequantize :78-79: x @ (q * scale[:, None]).T) with the
 // per-channel scale moved to the epilogue.
 //
-// Tiling: a 256-thread workgroup owns a 256 x 256 output tile (or, split-K, one K range of
-// it); its four wavefronts (one per SIMD, 512 registers each) own 128 x 128 quadrants, each a
-// grid of 8 x 8 v_mfma_f32_16x16x32_bf16 tiles (256 fp32 accumulators per lane, in AGPRs). K advances 64 per stage:
+// Tiling: a 512-thread workgroup owns a 256 x 256 output tile (or, split-K, one K range of
+// it); its eight wavefronts (two per SIMD, so one waits for LDS or a barrier while the other
+// issues MFMAs) own 128 x 64 parts, each a grid of 8 x 4 v_mfma_f32_16x16x32_bf16 tiles (128
+// fp32 accumulators per lane, in AGPRs). K advances 64 per stage:
 // A = 256 rows x 64 bf16 of x, B = 256 rows x 64 weights widened int8 -> fp32 -> bf16 on the
 // way into LDS. Two LDS buffers: the global loads of stage s + 1 are in flight (in registers)
 // while the 128 MFMAs per wavefront of stage s run from LDS, then go to the other buffer.
@@ -29,7 +30,7 @@ namespace {
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kMaxSplits = 4;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kXcds = 8;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -79,10 +80,10 @@ struct GemmArgs {
   int tiles_m, tiles_n, splits, k_split;  // k_split = K per split (multiple of kBK)
 };
 
-// One stage of global data held in registers: A (8 x 16 B: rows t / 8 + 32 i, chunk t % 8)
-// and B (4 x 16 B int8: rows t / 4 + 64 i, bytes 16 (t % 4) .. + 16).
+// One stage of global data held in registers: A (4 x 16 B: rows t / 8 + 64 i, chunk t % 8)
+// and B (2 x 16 B int8: rows t / 4 + 128 i, bytes 16 (t % 4) .. + 16).
 struct Stage {
-  u32x4 a[8], b[4];
+  u32x4 a[4], b[2];
 };
 
 __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
@@ -110,72 +111,72 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
 
   const int t = threadIdx.x;
   const int lane = t % 64, wave = t / 64;
-  const int wm = wave / 2, wn = wave % 2;  // 128 x 128 quadrant
+  const int wm = wave / 4, wn = wave % 4;  // 128 x 64 part of the tile
   const int K = a.K;
 
   // Global loads: a lane-constant byte offset, the stage's k (and the row block i) in the
-  // scalar offset. A: rows t / 8 + 32 i, chunk t % 8; B: rows t / 4 + 64 i, 16 bytes t % 4.
+  // scalar offset. A: rows t / 8 + 64 i, chunk t % 8; B: rows t / 4 + 128 i, 16 bytes t % 4.
   const auto ra = rsrc(a.xb, static_cast<int64_t>(a.M) * K * 2);
   const auto rb = rsrc(a.q, static_cast<int64_t>(a.N) * K);
   const int ga_off = ((m0 + t / 8) * K + 8 * (t % 8)) * 2;
   const int gb_off = (n0 + t / 4) * K + 16 * (t % 4);
   auto load_stage = [&](Stage& g, int k0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      g.a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             ra, ga_off, (k0 + i * 32 * K) * 2, 0));
-#pragma unroll
     for (int i = 0; i < 4; ++i)
+      g.a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             ra, ga_off, (k0 + i * 64 * K) * 2, 0));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
       g.b[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rb, gb_off, k0 + i * 64 * K, 0));
+                                             rb, gb_off, k0 + i * 128 * K, 0));
   };
-  // LDS stores: the swizzle of rows t / 8 + 32 i (A) and t / 4 + 64 i (B) depends on t only.
+  // LDS stores: the swizzle of rows t / 8 + 64 i (A) and t / 4 + 128 i (B) depends on t only.
   const int sa_off = (t / 8) * 128 + swz(t / 8, t % 8) * 16;
   const int sb_off0 = (t / 4) * 128 + swz(t / 4, 2 * (t % 4)) * 16;
   const int sb_off1 = (t / 4) * 128 + swz(t / 4, 2 * (t % 4) + 1) * 16;
   auto store_stage = [&](const Stage& g, int buf) {
     char* base = lds + buf * kBufBytes;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(base + sa_off + i * 32 * 128) = g.a[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(base + sa_off + i * 64 * 128) = g.a[i];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
       u32x4 lo, hi;
       widen16(g.b[i], lo, hi);
-      *reinterpret_cast<u32x4*>(base + kBOff + sb_off0 + i * 64 * 128) = lo;
-      *reinterpret_cast<u32x4*>(base + kBOff + sb_off1 + i * 64 * 128) = hi;
+      *reinterpret_cast<u32x4*>(base + kBOff + sb_off0 + i * 128 * 128) = lo;
+      *reinterpret_cast<u32x4*>(base + kBOff + sb_off1 + i * 128 * 128) = hi;
     }
   };
 
-  f32x4 acc[8][8];
+  f32x4 acc[8][4];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Fragment reads: rows wm * 128 + 16 i + fr (A) and wn * 128 + 16 j + fr (B); the swizzle
+  // Fragment reads: rows wm * 128 + 16 i + fr (A) and wn * 64 + 16 j + fr (B); the swizzle
   // of such a row depends on fr only, so each substep has one lane offset per operand.
   const int fr = lane % 16, fc = lane / 16;
   int fa_off[kBK / 32], fb_off[kBK / 32];
 #pragma unroll
   for (int sub = 0; sub < kBK / 32; ++sub) {
     fa_off[sub] = (wm * 128 + fr) * 128 + swz(fr, 4 * sub + fc) * 16;
-    fb_off[sub] = kBOff + (wn * 128 + fr) * 128 + swz(fr, 4 * sub + fc) * 16;
+    fb_off[sub] = kBOff + (wn * 64 + fr) * 128 + swz(fr, 4 * sub + fc) * 16;
   }
   auto compute = [&](int buf) {
     const char* base = lds + buf * kBufBytes;
 #pragma unroll
     for (int sub = 0; sub < kBK / 32; ++sub) {
-      bf16x8 fa[8], fb[8];
+      bf16x8 fa[8], fb[4];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         fa[i] = *reinterpret_cast<const bf16x8*>(base + fa_off[sub] + i * 16 * 128);
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < 4; ++j)
         fb[j] = *reinterpret_cast<const bf16x8*>(base + fb_off[sub] + j * 16 * 128);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
   };
@@ -197,8 +198,8 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
   // epilogue: lane holds rows 4 (lane / 16) + r, column lane % 16 of each 16 x 16 tile
   float* dst = a.splits > 1 ? a.part + static_cast<int64_t>(split) * a.M * a.N : a.y;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int nn = n0 + wn * 128 + 16 * j + fr;
+  for (int j = 0; j < 4; ++j) {
+    const int nn = n0 + wn * 64 + 16 * j + fr;
     if (nn >= a.N) continue;
     const float sc = a.splits > 1 ? 1.f : a.scale[nn];
 #pragma unroll
