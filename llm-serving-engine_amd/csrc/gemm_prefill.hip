@@ -80,12 +80,6 @@ struct GemmArgs {
   int tiles_m, tiles_n, splits, k_split;  // k_split = K per split (multiple of kBK)
 };
 
-// One stage of global data held in registers: A (4 x 16 B: rows t / 8 + 64 i, chunk t % 8)
-// and B (2 x 16 B int8: rows t / 4 + 128 i, bytes 16 (t % 4) .. + 16).
-struct Stage {
-  u32x4 a[4], b[2];
-};
-
 __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
   // [buf][row][8 chunks of 16 B]; A and B halves of one LDS stage
   __shared__ __attribute__((aligned(16))) char lds[2 * 2 * kBM * 128];
@@ -120,28 +114,30 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
   const auto rb = rsrc(a.q, static_cast<int64_t>(a.N) * K);
   const int ga_off = ((m0 + t / 8) * K + 8 * (t % 8)) * 2;
   const int gb_off = (n0 + t / 4) * K + 16 * (t % 4);
-  auto load_stage = [&](Stage& g, int k0) {
+  auto load_a = [&](u32x4 (&ga)[4], int k0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      g.a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             ra, ga_off, (k0 + i * 64 * K) * 2, 0));
+      ga[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            ra, ga_off, (k0 + i * 64 * K) * 2, 0));
+  };
+  auto load_b = [&](u32x4 (&gb)[2], int k0) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      g.b[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rb, gb_off, k0 + i * 128 * K, 0));
+      gb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rb, gb_off, k0 + i * 128 * K, 0));
   };
   // LDS stores: the swizzle of rows t / 8 + 64 i (A) and t / 4 + 128 i (B) depends on t only.
   const int sa_off = (t / 8) * 128 + swz(t / 8, t % 8) * 16;
   const int sb_off0 = (t / 4) * 128 + swz(t / 4, 2 * (t % 4)) * 16;
   const int sb_off1 = (t / 4) * 128 + swz(t / 4, 2 * (t % 4) + 1) * 16;
-  auto store_stage = [&](const Stage& g, int buf) {
+  auto store_stage = [&](const u32x4 (&ga)[4], const u32x4 (&gb)[2], int buf) {
     char* base = lds + buf * kBufBytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(base + sa_off + i * 64 * 128) = g.a[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(base + sa_off + i * 64 * 128) = ga[i];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       u32x4 lo, hi;
-      widen16(g.b[i], lo, hi);
+      widen16(gb[i], lo, hi);
       *reinterpret_cast<u32x4*>(base + kBOff + sb_off0 + i * 128 * 128) = lo;
       *reinterpret_cast<u32x4*>(base + kBOff + sb_off1 + i * 128 * 128) = hi;
     }
@@ -181,19 +177,35 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
     }
   };
 
-  // stage s + 1 is loaded into registers while stage s is computed from LDS, then stored to
-  // the other LDS buffer; one barrier per stage
+  // While stage s is computed from LDS, A of stage s + 1 and B (the weights, the loads that
+  // miss in L2) of stage s + 2 are loaded into registers; then A of s + 1 and B of s + 1
+  // (loaded one stage earlier; two B register sets used in turn) go to the other LDS buffer.
+  // The loads are unconditional (past the end they reload stage n - 1, unused): a load under a
+  // branch makes the waits count conservatively; vmcnt counts in issue order, so waiting for
+  // A of s + 1 leaves B of s + 2 in flight. One barrier per stage.
   const int n = a.k_split / kBK;
-  Stage g;
-  load_stage(g, kbeg);
-  store_stage(g, 0);
+  auto kofs = [&](int st) { return kbeg + (st < n ? st : n - 1) * kBK; };
+  u32x4 ga[4], gb0[2], gb1[2];
+  load_a(ga, kofs(0));
+  load_b(gb0, kofs(0));
+  load_b(gb1, kofs(1));
+  store_stage(ga, gb0, 0);
   __syncthreads();
-  for (int kt = 0; kt < n; ++kt) {
-    if (kt + 1 < n) load_stage(g, kbeg + (kt + 1) * kBK);
+  auto step = [&](int kt, const u32x4 (&nxtb)[2], u32x4 (&farb)[2]) {
+    load_a(ga, kofs(kt + 1));
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(farb, kofs(kt + 2));
+    __builtin_amdgcn_sched_barrier(0);
     compute(kt & 1);
-    if (kt + 1 < n) store_stage(g, (kt + 1) & 1);
+    store_stage(ga, nxtb, (kt + 1) & 1);
     __syncthreads();
+  };
+  int kt = 0;
+  for (; kt + 1 < n; kt += 2) {
+    step(kt, gb1, gb0);
+    step(kt + 1, gb0, gb1);
   }
+  if (kt < n) step(kt, gb1, gb0);
 
   // epilogue: lane holds rows 4 (lane / 16) + r, column lane % 16 of each 16 x 16 tile
   float* dst = a.splits > 1 ? a.part + static_cast<int64_t>(split) * a.M * a.N : a.y;
