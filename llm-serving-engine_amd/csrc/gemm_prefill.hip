@@ -28,7 +28,7 @@
 
 namespace {
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBM = 256, kBN = 256, kBK = 64;  // kBN: the widest tile (B rows per stage)
 constexpr int kMaxSplits = 4;
 constexpr int kThreads = 512;
 constexpr int kXcds = 8;
@@ -80,7 +80,11 @@ struct GemmArgs {
   int tiles_m, tiles_n, splits, k_split;  // k_split = K per split (multiple of kBK)
 };
 
+// BN: output columns per tile, 256 or 192 (for outputs whose 256-wide tiles would leave CUs
+// idle); a stage always stages kBN weight rows (rows past the tile are never read).
+template <int BN>
 __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
+  constexpr int NJ = BN / 64;  // 16-column MFMA tiles per wavefront (4 wavefront columns)
   // [buf][row][8 chunks of 16 B]; A and B halves of one LDS stage
   __shared__ __attribute__((aligned(16))) char lds[2 * 2 * kBM * 128];
   constexpr int kBufBytes = 2 * kBM * 128;  // one stage: A (32 KB) then B (32 KB)
@@ -100,12 +104,12 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
     col = b / a.tiles_m;
   }
   const int tn = col / a.splits, split = col % a.splits;
-  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int m0 = tm * kBM, n0 = tn * BN;
   const int kbeg = split * a.k_split;
 
   const int t = threadIdx.x;
   const int lane = t % 64, wave = t / 64;
-  const int wm = wave / 4, wn = wave % 4;  // 128 x 64 part of the tile
+  const int wm = wave / 4, wn = wave % 4;  // 128 x 16 NJ part of the tile
   const int K = a.K;
 
   // Global loads: a lane-constant byte offset, the stage's k (and the row block i) in the
@@ -143,36 +147,36 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
     }
   };
 
-  f32x4 acc[8][4];
+  f32x4 acc[8][NJ];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Fragment reads: rows wm * 128 + 16 i + fr (A) and wn * 64 + 16 j + fr (B); the swizzle
+  // Fragment reads: rows wm * 128 + 16 i + fr (A) and wn * 16 NJ + 16 j + fr (B); the swizzle
   // of such a row depends on fr only, so each substep has one lane offset per operand.
   const int fr = lane % 16, fc = lane / 16;
   int fa_off[kBK / 32], fb_off[kBK / 32];
 #pragma unroll
   for (int sub = 0; sub < kBK / 32; ++sub) {
     fa_off[sub] = (wm * 128 + fr) * 128 + swz(fr, 4 * sub + fc) * 16;
-    fb_off[sub] = kBOff + (wn * 64 + fr) * 128 + swz(fr, 4 * sub + fc) * 16;
+    fb_off[sub] = kBOff + (wn * 16 * NJ + fr) * 128 + swz(fr, 4 * sub + fc) * 16;
   }
   auto compute = [&](int buf) {
     const char* base = lds + buf * kBufBytes;
 #pragma unroll
     for (int sub = 0; sub < kBK / 32; ++sub) {
-      bf16x8 fa[8], fb[4];
+      bf16x8 fa[8], fb[NJ];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         fa[i] = *reinterpret_cast<const bf16x8*>(base + fa_off[sub] + i * 16 * 128);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
         fb[j] = *reinterpret_cast<const bf16x8*>(base + fb_off[sub] + j * 16 * 128);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
   };
@@ -210,8 +214,8 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_bf16(GemmArgs a) {
   // epilogue: lane holds rows 4 (lane / 16) + r, column lane % 16 of each 16 x 16 tile
   float* dst = a.splits > 1 ? a.part + static_cast<int64_t>(split) * a.M * a.N : a.y;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int nn = n0 + wn * 64 + 16 * j + fr;
+  for (int j = 0; j < NJ; ++j) {
+    const int nn = n0 + wn * 16 * NJ + 16 * j + fr;
     if (nn >= a.N) continue;
     const float sc = a.splits > 1 ? 1.f : a.scale[nn];
 #pragma unroll
@@ -240,14 +244,27 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ p
 
 // K splits for an M x N x K problem: enough (tile, split) units to give every CU one, at most
 // kMaxSplits, each split a multiple of kBK.
-int prefill_splits(int64_t M, int64_t N, int64_t K) {
+int device_cus() {
   int cus = 256, dev = 0;
   if (hipGetDevice(&dev) == hipSuccess) {
     int c = 0;
     if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
       cus = c;
   }
-  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  return cus;
+}
+
+// Tile width: 192 when 256-wide tiles leave CUs idle and 192-wide ones fill between 3/4 and
+// all of them (qkv at config 3: 192 -> 256 tiles), else 256.
+int pick_bn(int64_t M, int64_t N) {
+  const int64_t cus = device_cus(), tm = (M + kBM - 1) / kBM;
+  const int64_t t256 = tm * ((N + 255) / 256), t192 = tm * ((N + 191) / 192);
+  return (t256 < cus && 4 * t192 > 3 * cus && t192 <= cus) ? 192 : 256;
+}
+
+int prefill_splits(int64_t M, int64_t N, int64_t K) {
+  const int cus = device_cus();
+  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + pick_bn(M, N) - 1) / pick_bn(M, N));
   int s = 1;
   while (s < kMaxSplits && tiles * s * 2 <= cus && K % (static_cast<int64_t>(2 * s) * kBK) == 0) s *= 2;
   return s;
@@ -298,13 +315,18 @@ extern "C" int llmserve_int8_linear_prefill(const float* x, const int8_t* qweigh
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
   a.tiles_m = static_cast<int>((M + kBM - 1) / kBM);
-  a.tiles_n = static_cast<int>((N + kBN - 1) / kBN);
+  const int bn = pick_bn(M, N);
+  a.tiles_n = static_cast<int>((N + bn - 1) / bn);
   a.splits = splits;
   a.k_split = static_cast<int>(K / splits);
   const int64_t units = static_cast<int64_t>(a.tiles_m) * a.tiles_n * splits;
   LSH_CHECK(units < (1LL << 31), "int8_linear_prefill: too many tiles");
-  lsh::launch(int8_gemm_bf16, dim3(static_cast<unsigned>(units)), dim3(kThreads), 0, st,
-              splits == 1, a);
+  if (bn == 192)
+    lsh::launch(int8_gemm_bf16<192>, dim3(static_cast<unsigned>(units)), dim3(kThreads), 0, st,
+                splits == 1, a);
+  else
+    lsh::launch(int8_gemm_bf16<256>, dim3(static_cast<unsigned>(units)), dim3(kThreads), 0, st,
+                splits == 1, a);
   if (splits > 1) {
     const int64_t MN = M * N;
     const int64_t rgrid = (MN + 255) / 256 < 8192 ? (MN + 255) / 256 : 8192;

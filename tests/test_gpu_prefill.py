@@ -49,7 +49,8 @@ def make(seed, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 64), (37, 100, 64), (256, 256, 128), (300, 520, 192),
-                                   (513, 257, 320), (64, 2048, 1024), (200, 300, 4096)])
+                                   (513, 257, 320), (64, 2048, 1024), (200, 300, 4096),
+                                   (2048, 6000, 128)])  # 192-wide tiles, a 48-column last one
 def test_shapes(gpu, M, N, K):
     x, q, s = make(M * 7 + N, M, N, K)
     y = cu.int8_linear_prefill(cu.dev(x), cu.dev(q), cu.dev(s))
