@@ -343,6 +343,64 @@ int llmserve_paged_attention_decode_int8_xfrag(
     int64_t partition_size, const float* q_mult /* nullable */, void* workspace,
     int64_t workspace_bytes, void* stream);
 
+/*
+ * The same split-context paged decode over a float32 KV cache (replaces
+ * paged_attention_decode -> pa2::decode<float>, paged_attention.cpp:350-359, :141-346):
+ *   s_t = scale * (q_g . k_cache[slot_t,h,:]);  out_g = sum_t softmax(s)_t * v_cache[slot_t,h,:]
+ * k/v_cache fp32 [num_slots,Hk,D]; everything else, the split and the workspace
+ * (llmserve_paged_attention_workspace_bytes) as llmserve_paged_attention_decode_int8.
+ */
+int llmserve_paged_attention_decode(const float* q, const float* k_cache, const float* v_cache,
+                                    const int64_t* block_tables, const int64_t* context_lens,
+                                    float* out, int64_t B, int64_t Hq, int64_t Hk, int64_t D,
+                                    int64_t num_slots, int64_t max_blocks, int64_t block_size,
+                                    float scale, int64_t partition_size, void* workspace,
+                                    int64_t workspace_bytes, void* stream);
+
+/*
+ * Paged attention for the query rows of a ragged batch, decode and prefill alike (replaces
+ * paged_attention's prefill loop and decode branch, attention.py:249-307, over the cache of
+ * attention.py:241-246): query row r attends, with the paged decode's split and merge, to the
+ * first row_context[r] tokens of block-table row row_table[r] (0 <= row_table[r] < table_rows;
+ * a row outside gives NaN, as a zero context does). A prefill token at position p is a row
+ * with context p + 1, which is the causal mask of the reference's SDPA call
+ * (attention.py:114-124). llmserve_attention_metadata writes row_table / row_context for a
+ * step. q fp32 [R,Hq,D] (times q_mult [Hq,D] when non-NULL: key smoothing); block_tables int64
+ * [table_rows,max_blocks]; out fp32 [R,Hq,D]; the workspace holds
+ * llmserve_paged_attention_workspace_bytes(R, Hq, Hk, D, max_blocks, block_size, 0) bytes.
+ */
+int llmserve_paged_attention_rows_int8(const float* q, const int8_t* k_cache,
+                                       const int8_t* v_cache, const float* k_scale,
+                                       const float* v_scale, const int64_t* block_tables,
+                                       int64_t table_rows, const int64_t* row_table,
+                                       const int64_t* row_context, float* out, int64_t R,
+                                       int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots,
+                                       int64_t max_blocks, int64_t block_size, float scale,
+                                       const float* q_mult /* nullable */, void* workspace,
+                                       int64_t workspace_bytes, void* stream);
+int llmserve_paged_attention_rows_f32(const float* q, const float* k_cache, const float* v_cache,
+                                      const int64_t* block_tables, int64_t table_rows,
+                                      const int64_t* row_table, const int64_t* row_context,
+                                      float* out, int64_t R, int64_t Hq, int64_t Hk, int64_t D,
+                                      int64_t num_slots, int64_t max_blocks, int64_t block_size,
+                                      float scale, const float* q_mult /* nullable */,
+                                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Attention metadata of one step on the device (replaces the host loops of
+ * AttentionMetadata.build, attention.py:61-112): S sequences, sequence s with q_len new tokens
+ * at the end of its ctx_len-token context, its blocks in row s of block_tables int64
+ * [S,max_blocks]. seq_info int64 [3,S] holds q_lens, ctx_lens and q_start (the exclusive
+ * prefix sums of q_lens); T = sum of q_lens. For token t of sequence s at position p:
+ *   slot_mapping[t] = block_tables[s, p / block_size] * block_size + p % block_size
+ *                     (-1 when the block is past the table or its id is negative)
+ *   row_table[t] = s;  row_context[t] = p + 1.
+ */
+int llmserve_attention_metadata(const int64_t* seq_info, const int64_t* block_tables, int64_t S,
+                                int64_t max_blocks, int64_t block_size, int64_t T,
+                                int64_t* slot_mapping, int64_t* row_table, int64_t* row_context,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,7 @@ HIP_SOURCES = [
     "gemm_int4.hip",
     "fused_ops.hip",
     "paged_decode.hip",
+    "attn_meta.hip",
     "lm_head.hip",
 ]
 

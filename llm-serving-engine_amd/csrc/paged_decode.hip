@@ -50,9 +50,13 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1e30f;        // the reference's initial running max
 constexpr float kLazy2 = 8.0f * kLog2e;  // lazy running-max headroom (log2 units: e^8)
 constexpr int kWin = 64;                 // block ids of a window, one per lane
-// steps of K/V loads in flight per wavefront (fewer for wide GQA groups: register budget)
-template <int G>
-constexpr int ring_depth() { return G <= 2 ? 4 : (G <= 4 ? 3 : 2); }
+// steps of K/V loads in flight per wavefront (fewer for wide GQA groups and fp32 rows, which
+// hold four times the bytes per lane: register budget)
+template <int G, bool kF32>
+constexpr int ring_depth() {
+  if constexpr (kF32) return G <= 2 ? 2 : 1;
+  return G <= 2 ? 4 : (G <= 4 ? 3 : 2);
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -64,7 +68,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t b
                                            0x00020000);
 }
 
-__device__ __forceinline__ void unpack_i8x16(const u32x4& w, float (&f)[16]) {
+__device__ __forceinline__ void unpack16(const u32x4& w, float (&f)[16]) {  // 16 int8 values
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -72,13 +76,27 @@ __device__ __forceinline__ void unpack_i8x16(const u32x4& w, float (&f)[16]) {
       f[4 * i + b] = static_cast<float>(static_cast<int8_t>((w[i] >> (8 * b)) & 0xffu));
 }
 
+// 16 floats. The element goes through a named temporary: this compiler's __builtin_bit_cast of
+// a vector element expression (w[i][b]) reads element 0 whatever the subscript.
+__device__ __forceinline__ void unpack16(const u32x4 (&w)[4], float (&f)[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t u = w[i][b];
+      f[4 * i + b] = __builtin_bit_cast(float, u);
+    }
+}
+
 struct DecodeArgs {
   const float* q;
-  const int8_t* kc;
-  const int8_t* vc;
-  const float* ks;
+  const void* kc;  // int8 or float32 [num_slots, Hk, D]
+  const void* vc;
+  const float* ks;  // [num_slots, Hk] (int8 caches only)
   const float* vs;
   const int64_t* bt;
+  const int64_t* row_tab;  // nullable [B]: block-table row of query row b (else b)
+  int64_t tab_rows;        // rows of bt when row_tab is given
   const int64_t* cl;
   const float* q_mult;
   float* out;
@@ -99,10 +117,15 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Context length of sequence b, clamped to [0, max_blocks * block_size].
+// Context length of query row b, clamped to [0, max_blocks * block_size]; 0 for a row whose
+// block-table row (row map) is outside the table.
 __device__ __forceinline__ int64_t seq_ctx(const DecodeArgs& a, int b) {
   const int64_t cap = static_cast<int64_t>(a.max_blocks) * a.bs;
   const int64_t c = a.cl[b];
+  if (a.row_tab != nullptr) {
+    const int64_t t = a.row_tab[b];
+    if (t < 0 || t >= a.tab_rows) return 0;
+  }
   return c < 0 ? 0 : (c > cap ? cap : c);
 }
 
@@ -166,23 +189,45 @@ __device__ SeqPos locate(const DecodeArgs& a, int64_t g) {
   return {a.B, uniform64(base), 0};
 }
 
-// One token step of one lane: its 16 K and V bytes and the row's two scales.
-struct Tok {
+// One token step of one lane: its 16 K and V elements and the row's two scales (1 for an
+// fp32 cache).
+template <typename E>
+struct Tok;
+template <>
+struct Tok<int8_t> {
   u32x4 k, v;
   float ks, vs;
   bool valid;  // this lane's token is in the segment and its block id is inside the cache
 };
+template <>
+struct Tok<float> {
+  u32x4 k[4], v[4];
+  float ks, vs;
+  bool valid;
+};
+
+// An opaque use of a ring entry's registers (see the ring loop).
+__device__ __forceinline__ void pin(Tok<int8_t>& c) {
+  asm volatile("" : "+v"(c.k), "+v"(c.v), "+v"(c.ks), "+v"(c.vs));
+}
+__device__ __forceinline__ void pin(Tok<float>& c) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(c.k[i]), "+v"(c.v[i]));
+}
 
 // Runs tokens [t0, t1) of (b, h) and writes the output rows (whole) or partial `slot`.
 // kOff32: the K / V caches and their scales are each under 4 GB, so one buffer resource per
 // tensor (built once) with the step's slot offset in the scalar offset register addresses a
 // step; else the resources are rebuilt per step from 64-bit bases.
-template <int D, int G, bool kScalarBlk, bool kOff32>
+template <typename E, int D, int G, bool kScalarBlk, bool kOff32>
 __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h, int t0, int t1,
                                                bool whole, int64_t slot) {
+  constexpr bool kF32 = std::is_same_v<E, float>;
+  constexpr int kEB = sizeof(E);    // bytes per cache element
   constexpr int LPR = D / 16;       // lanes per token row
   constexpr int RPW = kWave / LPR;  // row slots per wavefront
-  constexpr int kRing = ring_depth<G>();
+  constexpr int kRing = ring_depth<G, kF32>();
+  const int64_t tab_row = a.row_tab ? uniform64(a.row_tab[b]) : b;
   const int lane = threadIdx.x % kWave;
   const int r = lane / LPR, seg = lane % LPR;
   const int bs = a.bs;
@@ -221,11 +266,13 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
     for (int i = 0; i < 16; ++i) acc[g][i] = 0.f;
   }
 
-  const int64_t row_stride = static_cast<int64_t>(a.Hk) * D;  // bytes between slots
+  const int64_t row_stride = static_cast<int64_t>(a.Hk) * D * kEB;  // bytes between slots
   // Per-lane offsets inside a step: row slot r, head h, dims of segment seg.
-  const uint32_t kv_lane = static_cast<uint32_t>(r * row_stride + h * D + seg * 16);
+  const uint32_t kv_lane = static_cast<uint32_t>(r * row_stride + (h * D + seg * 16) * kEB);
   const uint32_t sc_lane = static_cast<uint32_t>((r * a.Hk + h) * sizeof(float));
-  const int64_t head_off = static_cast<int64_t>(h) * D + seg * 16;
+  const int64_t head_off = (static_cast<int64_t>(h) * D + seg * 16) * kEB;
+  const char* kc = static_cast<const char*>(a.kc);
+  const char* vc = static_cast<const char*>(a.vc);
   const uint32_t step_bytes = static_cast<uint32_t>(RPW * row_stride);
   const uint32_t sc_bytes = static_cast<uint32_t>(RPW * a.Hk * sizeof(float));
   // kOff32 resources over whole tensors (the byte counts fit 32 bits by the host's choice)
@@ -243,7 +290,7 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
     {
       const int nwin = (we - wb * bs + bs - 1) / bs;
       if (lane < nwin) {
-        const int64_t id = a.bt[static_cast<int64_t>(b) * a.max_blocks + wb + lane];
+        const int64_t id = a.bt[tab_row * a.max_blocks + wb + lane];
         my_blk = (id >= 0 && id < a.num_slots / bs) ? static_cast<int>(id) : -1;
       }
     }
@@ -256,7 +303,7 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
     // (in bounds, masked). The loads are unconditional on purpose: with a predicated load
     // the compiler folds the consumer's byte unpacking into the load's block and waits for
     // the data right there, which serialises the ring of in-flight steps.
-    auto fetch = [&](int k, Tok& o) {
+    auto fetch = [&](int k, Tok<E>& o) {
       const int tk = k * RPW;
       const int t = tk + r;
       if constexpr (kScalarBlk) {
@@ -267,20 +314,40 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
         o.valid = id >= 0 && t >= ws && t < we;
         if constexpr (kOff32) {
           const uint32_t sb = static_cast<uint32_t>(id >= 0 ? id : 0) * bs + (tk & (bs - 1));
-          o.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, kv_lane, sb * rs32, kNT));
-          o.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, kv_lane, sb * rs32, kNT));
-          o.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, sc_lane, sb * hk4, 0));
-          o.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, sc_lane, sb * hk4, 0));
+          if constexpr (kF32) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              o.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rk, kv_lane + 16 * i, sb * rs32, kNT));
+              o.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rv, kv_lane + 16 * i, sb * rs32, kNT));
+            }
+            o.ks = o.vs = 1.f;
+          } else {
+            o.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, kv_lane, sb * rs32, kNT));
+            o.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, kv_lane, sb * rs32, kNT));
+            o.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, sc_lane, sb * hk4, 0));
+            o.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, sc_lane, sb * hk4, 0));
+          }
         } else {
           const int64_t sb = static_cast<int64_t>(id >= 0 ? id : 0) * bs + (tk & (bs - 1));
-          o.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              rsrc(a.kc + sb * row_stride, step_bytes), kv_lane, 0, kNT));
-          o.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              rsrc(a.vc + sb * row_stride, step_bytes), kv_lane, 0, kNT));
-          o.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                               rsrc(a.ks + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
-          o.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                               rsrc(a.vs + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
+          const __amdgpu_buffer_rsrc_t sk = rsrc(kc + sb * row_stride, step_bytes);
+          const __amdgpu_buffer_rsrc_t sv = rsrc(vc + sb * row_stride, step_bytes);
+          if constexpr (kF32) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              o.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sk, kv_lane + 16 * i, 0, kNT));
+              o.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sv, kv_lane + 16 * i, 0, kNT));
+            }
+            o.ks = o.vs = 1.f;
+          } else {
+            o.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sk, kv_lane, 0, kNT));
+            o.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sv, kv_lane, 0, kNT));
+            o.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 rsrc(a.ks + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
+            o.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 rsrc(a.vs + sb * a.Hk, sc_bytes), sc_lane, 0, 0));
+          }
         }
       } else {
         // every lane takes part in the shuffle (a lane's block id is read even when that
@@ -291,20 +358,29 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
         o.valid = id >= 0 && t >= ws && t < we;
         const int off = a.bs_shift >= 0 ? t & (bs - 1) : t % bs;
         const int64_t sl = o.valid ? static_cast<int64_t>(id) * bs + off : 0;
-        o.k = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(a.kc + sl * row_stride + head_off));
-        o.v = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(a.vc + sl * row_stride + head_off));
-        o.ks = a.ks[sl * a.Hk + h];
-        o.vs = a.vs[sl * a.Hk + h];
+        const u32x4* kp = reinterpret_cast<const u32x4*>(kc + sl * row_stride + head_off);
+        const u32x4* vp = reinterpret_cast<const u32x4*>(vc + sl * row_stride + head_off);
+        if constexpr (kF32) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            o.k[i] = __builtin_nontemporal_load(kp + i);
+            o.v[i] = __builtin_nontemporal_load(vp + i);
+          }
+          o.ks = o.vs = 1.f;
+        } else {
+          o.k = __builtin_nontemporal_load(kp);
+          o.v = __builtin_nontemporal_load(vp);
+          o.ks = a.ks[sl * a.Hk + h];
+          o.vs = a.vs[sl * a.Hk + h];
+        }
       }
     };
 
     // One step. A row outside the segment or the cache gets the score -inf (p = 0, and it
     // never raises the max) and the value scale 0 (its bytes, whatever they hold, add 0).
-    auto consume = [&](const Tok& c) {
+    auto consume = [&](const Tok<E>& c) {
       float kf[16];
-      unpack_i8x16(c.k, kf);
+      unpack16(c.k, kf);
       float s[G];
       bool raise = false;
 #pragma unroll
@@ -329,7 +405,7 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
         }
       }
       float vf[16];
-      unpack_i8x16(c.v, vf);
+      unpack16(c.v, vf);
       const float vsc = c.valid ? c.vs : 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -342,18 +418,18 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
     };
 
     const int k0 = ws / RPW, k1 = (we + RPW - 1) / RPW;
-    Tok ring[kRing];
+    Tok<E> ring[kRing];
 #pragma unroll
     for (int u = 0; u < kRing; ++u) fetch(k0 + u, ring[u]);
     // Whole rounds of kRing steps; steps past the window are fully masked.
     for (int k = k0; k < k1; k += kRing) {
 #pragma unroll
       for (int u = 0; u < kRing; ++u) {
-        Tok& c = ring[u];
+        Tok<E>& c = ring[u];
         // Consume the ring entry here and not earlier: an opaque use stops the compiler from
         // folding the unpacking into the loop latch, where it would wait for loads issued
         // only this round (vmcnt counts in issue order).
-        asm volatile("" : "+v"(c.k), "+v"(c.v), "+v"(c.ks), "+v"(c.vs));
+        pin(c);
         consume(c);
         fetch(k + u + kRing, c);
       }
@@ -411,8 +487,8 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
 // Decode kernel: workgroup w runs work ranges w, w + W, ... (one range each with the
 // balanced default); its wavefront i takes kv head hg * HB + i. Waves proceed independently
 // (no barriers).
-template <int D, int G, bool kScalarBlk, bool kOff32>
-__global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_int8_kernel(DecodeArgs a) {
+template <typename E, int D, int G, bool kScalarBlk, bool kOff32>
+__global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_kernel(DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const Ranges rg = work_ranges(a);
   for (int64_t j = blockIdx.x; j < rg.R; j += a.W) {
@@ -433,8 +509,8 @@ __global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_int8_k
       const int h = hg * a.HB + wave;
       const bool whole = t0 == 0 && t1 == ctx;
       const int64_t slot = ((static_cast<int64_t>(b) * a.NHG + hg) + j) * a.HB + wave;
-      decode_segment<D, G, kScalarBlk, kOff32>(a, b, h, static_cast<int>(t0), static_cast<int>(t1), whole,
-                                       slot);
+      decode_segment<E, D, G, kScalarBlk, kOff32>(a, b, h, static_cast<int>(t0),
+                                                  static_cast<int>(t1), whole, slot);
       g = send;
       if (g >= ge) break;
       if (hg + 1 == a.NHG) {  // next sequence with a non-empty context
@@ -689,11 +765,11 @@ bool scalar_blocks(int64_t D, int64_t block_size) {
 // Workgroups of the decode grid (all resident at once) of the variant that runs; off32 < 0:
 // the larger of the two scalar-block variants (the workspace bound, which does not know the
 // cache size).
-template <int D, int G>
+template <typename E, int D, int G>
 int decode_blocks(bool scalar, int off32, int hb) {
-  if (!scalar) return resident_blocks<paged_decode_int8_kernel<D, G, false, false>>(hb);
-  const int w32 = resident_blocks<paged_decode_int8_kernel<D, G, true, true>>(hb);
-  const int w64 = resident_blocks<paged_decode_int8_kernel<D, G, true, false>>(hb);
+  if (!scalar) return resident_blocks<paged_decode_kernel<E, D, G, false, false>>(hb);
+  const int w32 = resident_blocks<paged_decode_kernel<E, D, G, true, true>>(hb);
+  const int w64 = resident_blocks<paged_decode_kernel<E, D, G, true, false>>(hb);
   return off32 > 0 ? w32 : (off32 == 0 ? w64 : (w32 > w64 ? w32 : w64));
 }
 
@@ -703,15 +779,15 @@ struct FragOut {
   void* xfrag;
 };
 
-template <int D, int G>
+template <typename E, int D, int G>
 void launch_decode(const DecodeArgs& a, bool scalar, bool off32, const FragOut& fo, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.W)), block(a.HB * kWave);
   if (scalar && off32)
-    lsh::launch(paged_decode_int8_kernel<D, G, true, true>, grid, block, 0, st, false, a);
+    lsh::launch(paged_decode_kernel<E, D, G, true, true>, grid, block, 0, st, false, a);
   else if (scalar)
-    lsh::launch(paged_decode_int8_kernel<D, G, true, false>, grid, block, 0, st, false, a);
+    lsh::launch(paged_decode_kernel<E, D, G, true, false>, grid, block, 0, st, false, a);
   else
-    lsh::launch(paged_decode_int8_kernel<D, G, false, false>, grid, block, 0, st, false, a);
+    lsh::launch(paged_decode_kernel<E, D, G, false, false>, grid, block, 0, st, false, a);
   if constexpr (D == 128 || D == 256) {
     if (fo.xfrag != nullptr) {
       const int mp = static_cast<int>(lsh::frag_rows(a.B));
@@ -758,12 +834,18 @@ bool with_shape(int64_t D, int64_t G, F&& f) {
   }
 }
 
-int grid_blocks(int64_t D, int64_t G, int64_t Hk, int64_t block_size, int off32 = -1) {
-  int w = 0;
+// Decode workgroups for a cache of `elem_bytes`-byte elements (1: int8, 4: fp32; 0: the
+// larger of the two, for workspace bounds that do not know the cache type).
+int grid_blocks(int64_t D, int64_t G, int64_t Hk, int64_t block_size, int off32 = -1,
+                int elem_bytes = 0) {
+  int w8 = 0, w32 = 0;
   const bool scalar = scalar_blocks(D, block_size);
   const int hb = heads_per_block(Hk);
-  with_shape(D, G, [&]<int Dv, int Gv>() { w = decode_blocks<Dv, Gv>(scalar, off32, hb); });
-  return w;
+  with_shape(D, G, [&]<int Dv, int Gv>() {
+    if (elem_bytes != 4) w8 = decode_blocks<int8_t, Dv, Gv>(scalar, off32, hb);
+    if (elem_bytes != 1) w32 = decode_blocks<float, Dv, Gv>(scalar, off32, hb);
+  });
+  return w8 > w32 ? w8 : w32;
 }
 
 // Partial slots the workspace holds: HB per (b, head group) plus HB per work range (the
@@ -794,12 +876,26 @@ extern "C" int64_t llmserve_paged_attention_workspace_bytes(int64_t B, int64_t H
 
 namespace {
 
-int decode_int8(const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
-                const float* v_scale, const int64_t* block_tables, const int64_t* context_lens,
-                float* out, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots,
-                int64_t max_blocks, int64_t block_size, float scale, int64_t partition_size,
-                const float* q_mult, const FragOut& fo, void* workspace, int64_t workspace_bytes,
-                void* stream) {
+// The cache a call attends over: int8 with per-(slot, head) scales, or fp32 (no scales).
+struct CacheView {
+  const void* k;
+  const void* v;
+  const float* k_scale;  // int8 only
+  const float* v_scale;
+  int elem_bytes;  // 1 or 4
+};
+
+// Query rows -> block-table rows (nullable: row b uses table row b).
+struct RowMap {
+  const int64_t* row_table;
+  int64_t table_rows;
+};
+
+int decode_paged(const float* q, const CacheView& c, const int64_t* block_tables,
+                 const RowMap& rows, const int64_t* context_lens, float* out, int64_t B,
+                 int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots, int64_t max_blocks,
+                 int64_t block_size, float scale, int64_t partition_size, const float* q_mult,
+                 const FragOut& fo, void* workspace, int64_t workspace_bytes, void* stream) {
   LSH_CHECK(B >= 0 && Hq >= 1 && Hk >= 1 && D >= 1, "paged_attention: bad shape");
   LSH_CHECK(Hq % Hk == 0, "Hq must be a multiple of Hk");
   LSH_CHECK(block_size >= 1 && max_blocks >= 0 && num_slots >= 0, "paged_attention: bad cache shape");
@@ -807,16 +903,20 @@ int decode_int8(const float* q, const int8_t* k_cache, const int8_t* v_cache, co
   LSH_CHECK(max_blocks >= 1 && num_slots >= block_size,
             "paged_attention: empty block table or cache");
   const int64_t G = Hq / Hk;
-  LSH_CHECK(G <= 8, "paged_attention_decode_int8: at most 8 query heads per kv head (got %lld)",
-            (long long)G);
+  LSH_CHECK(G <= 8, "paged_attention: at most 8 query heads per kv head (got %lld)", (long long)G);
   LSH_CHECK(D == 16 || D == 32 || D == 64 || D == 128 || D == 256,
-            "paged_attention_decode_int8: head_dim %lld not in {16, 32, 64, 128, 256}", (long long)D);
+            "paged_attention: head_dim %lld not in {16, 32, 64, 128, 256}", (long long)D);
   LSH_CHECK(B < (1LL << 24) && Hk <= 4096, "paged_attention: batch or kv heads too large");
   LSH_CHECK(max_blocks * block_size < (1LL << 31) && num_slots * Hk < (1LL << 31),
             "paged_attention: context or cache too long");
-  LSH_CHECK(q && k_cache && v_cache && k_scale && v_scale && block_tables && context_lens && out,
+  const bool int8 = c.elem_bytes == 1;
+  LSH_CHECK(c.elem_bytes == 1 || c.elem_bytes == 4, "paged_attention: cache of int8 or float32");
+  LSH_CHECK(q && c.k && c.v && block_tables && context_lens && out &&
+                (!int8 || (c.k_scale && c.v_scale)),
             "paged_attention: null pointer");
-  LSH_CHECK(lsh::aligned16(q) && lsh::aligned16(k_cache) && lsh::aligned16(v_cache) &&
+  LSH_CHECK(rows.row_table == nullptr || rows.table_rows >= 1,
+            "paged_attention: a row map needs a non-empty block table");
+  LSH_CHECK(lsh::aligned16(q) && lsh::aligned16(c.k) && lsh::aligned16(c.v) &&
                 lsh::aligned16(out) && (q_mult == nullptr || lsh::aligned16(q_mult)),
             "paged_attention: q, caches, out and q_mult must be 16-byte aligned");
   const int64_t slots = partial_slots(B, Hk, D, G, max_blocks, block_size, partition_size);
@@ -829,11 +929,13 @@ int decode_int8(const float* q, const int8_t* k_cache, const int8_t* v_cache, co
   const bool scalar = scalar_blocks(D, block_size);
   DecodeArgs a{};
   a.q = q;
-  a.kc = k_cache;
-  a.vc = v_cache;
-  a.ks = k_scale;
-  a.vs = v_scale;
+  a.kc = c.k;
+  a.vc = c.v;
+  a.ks = c.k_scale;
+  a.vs = c.v_scale;
   a.bt = block_tables;
+  a.row_tab = rows.row_table;
+  a.tab_rows = rows.table_rows;
   a.cl = context_lens;
   a.q_mult = q_mult;
   a.out = out;
@@ -853,15 +955,31 @@ int decode_int8(const float* q, const int8_t* k_cache, const int8_t* v_cache, co
   a.HB = heads_per_block(Hk);
   a.NHG = static_cast<int>(Hk / a.HB);
   // one buffer resource per cache tensor when each is addressable with 32-bit offsets
-  const bool off32 = num_slots * Hk * D <= static_cast<int64_t>(0xffffffffu);
-  a.W = grid_blocks(D, G, Hk, block_size, off32 ? 1 : 0);
+  const bool off32 = num_slots * Hk * D * c.elem_bytes <= static_cast<int64_t>(0xffffffffu);
+  a.W = grid_blocks(D, G, Hk, block_size, off32 ? 1 : 0, c.elem_bytes);
   a.qscale = scale * kLog2e;
   LSH_CHECK(a.W >= 1, "paged_attention: no resident workgroups");
   hipStream_t st = lsh::as_stream(stream);
-  const bool ok =
-      with_shape(D, G, [&]<int Dv, int Gv>() { launch_decode<Dv, Gv>(a, scalar, off32, fo, st); });
+  const bool ok = with_shape(D, G, [&]<int Dv, int Gv>() {
+    if (int8)
+      launch_decode<int8_t, Dv, Gv>(a, scalar, off32, fo, st);
+    else
+      launch_decode<float, Dv, Gv>(a, scalar, off32, fo, st);
+  });
   LSH_CHECK(ok, "paged_attention: unsupported G=%lld", (long long)G);
-  return lsh::launch_status("paged_attention_decode_int8");
+  return lsh::launch_status(int8 ? "paged_attention_decode_int8" : "paged_attention_decode");
+}
+
+int decode_int8(const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
+                const float* v_scale, const int64_t* block_tables, const int64_t* context_lens,
+                float* out, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots,
+                int64_t max_blocks, int64_t block_size, float scale, int64_t partition_size,
+                const float* q_mult, const FragOut& fo, void* workspace, int64_t workspace_bytes,
+                void* stream) {
+  return decode_paged(q, CacheView{k_cache, v_cache, k_scale, v_scale, 1}, block_tables,
+                      RowMap{nullptr, 0}, context_lens, out, B, Hq, Hk, D, num_slots, max_blocks,
+                      block_size, scale, partition_size, q_mult, fo, workspace, workspace_bytes,
+                      stream);
 }
 
 }  // namespace
@@ -893,4 +1011,41 @@ extern "C" int llmserve_paged_attention_decode_int8_xfrag(
   return decode_int8(q, k_cache, v_cache, k_scale, v_scale, block_tables, context_lens, out, B, Hq,
                      Hk, D, num_slots, max_blocks, block_size, scale, partition_size, q_mult,
                      FragOut{act_inv, xfrag}, workspace, workspace_bytes, stream);
+}
+
+extern "C" int llmserve_paged_attention_decode(
+    const float* q, const float* k_cache, const float* v_cache, const int64_t* block_tables,
+    const int64_t* context_lens, float* out, int64_t B, int64_t Hq, int64_t Hk, int64_t D,
+    int64_t num_slots, int64_t max_blocks, int64_t block_size, float scale,
+    int64_t partition_size, void* workspace, int64_t workspace_bytes, void* stream) {
+  return decode_paged(q, CacheView{k_cache, v_cache, nullptr, nullptr, 4}, block_tables,
+                      RowMap{nullptr, 0}, context_lens, out, B, Hq, Hk, D, num_slots, max_blocks,
+                      block_size, scale, partition_size, nullptr, FragOut{nullptr, nullptr},
+                      workspace, workspace_bytes, stream);
+}
+
+extern "C" int llmserve_paged_attention_rows_int8(
+    const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
+    const float* v_scale, const int64_t* block_tables, int64_t table_rows,
+    const int64_t* row_table, const int64_t* row_context, float* out, int64_t R, int64_t Hq,
+    int64_t Hk, int64_t D, int64_t num_slots, int64_t max_blocks, int64_t block_size,
+    float scale, const float* q_mult, void* workspace, int64_t workspace_bytes, void* stream) {
+  LSH_CHECK(row_table != nullptr || R == 0, "paged_attention_rows_int8: row_table is required");
+  return decode_paged(q, CacheView{k_cache, v_cache, k_scale, v_scale, 1}, block_tables,
+                      RowMap{row_table, table_rows}, row_context, out, R, Hq, Hk, D, num_slots,
+                      max_blocks, block_size, scale, 0, q_mult, FragOut{nullptr, nullptr},
+                      workspace, workspace_bytes, stream);
+}
+
+extern "C" int llmserve_paged_attention_rows_f32(
+    const float* q, const float* k_cache, const float* v_cache, const int64_t* block_tables,
+    int64_t table_rows, const int64_t* row_table, const int64_t* row_context, float* out,
+    int64_t R, int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots, int64_t max_blocks,
+    int64_t block_size, float scale, const float* q_mult, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+  LSH_CHECK(row_table != nullptr || R == 0, "paged_attention_rows_f32: row_table is required");
+  return decode_paged(q, CacheView{k_cache, v_cache, nullptr, nullptr, 4}, block_tables,
+                      RowMap{row_table, table_rows}, row_context, out, R, Hq, Hk, D, num_slots,
+                      max_blocks, block_size, scale, 0, q_mult, FragOut{nullptr, nullptr},
+                      workspace, workspace_bytes, stream);
 }

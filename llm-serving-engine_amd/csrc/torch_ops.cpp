@@ -392,6 +392,13 @@ at::Tensor decode_qkv_kv(const at::Tensor& qkv, const at::Tensor& cos_table,
       check_f32(**w, "weight");
       check_device(qkv, {&**w}, "decode_qkv_kv");
     }
+  TORCH_CHECK((!q_w.has_value() || q_w->numel() == head_dim) &&
+                  (!k_w.has_value() || k_w->numel() == head_dim),
+              "decode_qkv_kv: q/k norm weights must have head_dim entries");
+  TORCH_CHECK(!k_smooth.has_value() || k_smooth->numel() == n_k * head_dim,
+              "decode_qkv_kv: k_smooth must be [n_k, head_dim]");
+  TORCH_CHECK(qkv.size(1) >= (n_q + 2 * n_k) * head_dim,
+              "decode_qkv_kv: qkv rows hold fewer than (n_q + 2 n_k) * head_dim values");
   const c10::DeviceGuard guard(qkv.device());
   auto q_out = at::empty({T, n_q, head_dim}, qkv.options());
   check_status(llmserve_decode_qkv_kv(
@@ -627,6 +634,129 @@ std::tuple<at::Tensor, at::Tensor> paged_attention_decode_int8_xfrag(
   return {out, xf};
 }
 
+// The reference's fp32-cache decode (paged_attention.cpp:350-359, :386-390).
+at::Tensor paged_attention_decode(const at::Tensor& q, const at::Tensor& k_cache,
+                                  const at::Tensor& v_cache, const at::Tensor& block_tables,
+                                  const at::Tensor& context_lens, int64_t block_size, double scale,
+                                  int64_t partition_size) {
+  TORCH_CHECK(k_cache.scalar_type() == at::kFloat && v_cache.scalar_type() == at::kFloat,
+              "paged_attention_decode: float32 cache");
+  TORCH_CHECK(q.scalar_type() == at::kFloat, "paged_attention: q must be float32");
+  TORCH_CHECK(block_tables.scalar_type() == at::kLong && context_lens.scalar_type() == at::kLong,
+              "paged_attention_decode: int64 block tables / context lens");
+  TORCH_CHECK(q.is_contiguous() && k_cache.is_contiguous() && v_cache.is_contiguous() &&
+                  block_tables.is_contiguous() && context_lens.is_contiguous(),
+              "paged_attention_decode: inputs must be contiguous");
+  TORCH_CHECK(q.dim() == 3 && k_cache.dim() == 3 && v_cache.sizes() == k_cache.sizes() &&
+                  k_cache.size(2) == q.size(2),
+              "paged_attention: q [B, Hq, D], caches [num_slots, Hk, D]");
+  TORCH_CHECK(block_tables.dim() == 2 && context_lens.dim() == 1 &&
+                  block_tables.size(0) == q.size(0) && context_lens.size(0) == q.size(0),
+              "paged_attention: block_tables [B, max_blocks], context_lens [B]");
+  check_device(q, {&k_cache, &v_cache, &block_tables, &context_lens}, "paged_attention_decode");
+  const int64_t B = q.size(0), Hq = q.size(1), D = q.size(2);
+  const c10::DeviceGuard guard(q.device());
+  auto out = at::empty_like(q);
+  if (B == 0) return out;
+  int64_t ws_bytes = 0;
+  at::Tensor ws = paged_workspace(q, k_cache, block_tables, block_size, partition_size, ws_bytes);
+  check_status(llmserve_paged_attention_decode(
+      q.data_ptr<float>(), k_cache.data_ptr<float>(), v_cache.data_ptr<float>(),
+      block_tables.data_ptr<int64_t>(), context_lens.data_ptr<int64_t>(), out.data_ptr<float>(),
+      B, Hq, k_cache.size(1), D, k_cache.size(0), block_tables.size(1), block_size,
+      static_cast<float>(scale), partition_size, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+      stream_of(q)));
+  return out;
+}
+
+// Attention over the query rows of a ragged batch (decode and prefill rows alike) for an int8
+// (k_scale / v_scale given) or float32 (no scales) cache.
+at::Tensor paged_attention_rows(const at::Tensor& q, const at::Tensor& k_cache,
+                                const at::Tensor& v_cache, const std::optional<at::Tensor>& k_scale,
+                                const std::optional<at::Tensor>& v_scale,
+                                const at::Tensor& block_tables, const at::Tensor& row_table,
+                                const at::Tensor& row_context, int64_t block_size, double scale,
+                                const std::optional<at::Tensor>& q_mult) {
+  const bool int8 = k_cache.scalar_type() == at::kChar;
+  TORCH_CHECK(int8 || k_cache.scalar_type() == at::kFloat,
+              "paged_attention_rows: int8 or float32 cache");
+  TORCH_CHECK(v_cache.scalar_type() == k_cache.scalar_type() && v_cache.sizes() == k_cache.sizes(),
+              "paged_attention_rows: K and V caches of one type and shape");
+  TORCH_CHECK(int8 == (k_scale.has_value() && v_scale.has_value()),
+              "paged_attention_rows: an int8 cache takes k_scale and v_scale, a float32 one none");
+  TORCH_CHECK(q.scalar_type() == at::kFloat && q.dim() == 3 && q.is_contiguous(),
+              "paged_attention_rows: q must be a contiguous float32 [R, Hq, D] tensor");
+  TORCH_CHECK(k_cache.dim() == 3 && k_cache.size(2) == q.size(2) && k_cache.is_contiguous() &&
+                  v_cache.is_contiguous(),
+              "paged_attention_rows: caches must be contiguous [num_slots, Hk, D]");
+  for (const at::Tensor* t : {&block_tables, &row_table, &row_context})
+    TORCH_CHECK(t->scalar_type() == at::kLong && t->is_contiguous(),
+                "paged_attention_rows: int64 contiguous tables");
+  TORCH_CHECK(block_tables.dim() == 2 && row_table.numel() == q.size(0) &&
+                  row_context.numel() == q.size(0),
+              "paged_attention_rows: block_tables [S, max_blocks], one table row and context per "
+              "query row");
+  check_device(q, {&k_cache, &v_cache, &block_tables, &row_table, &row_context},
+               "paged_attention_rows");
+  const int64_t R = q.size(0), Hq = q.size(1), D = q.size(2);
+  const int64_t num_slots = k_cache.size(0), Hk = k_cache.size(1);
+  if (int8) {
+    check_device(q, {&*k_scale, &*v_scale}, "paged_attention_rows");
+    TORCH_CHECK(k_scale->scalar_type() == at::kFloat && v_scale->scalar_type() == at::kFloat &&
+                    k_scale->is_contiguous() && v_scale->is_contiguous() &&
+                    k_scale->numel() == num_slots * Hk && v_scale->numel() == num_slots * Hk,
+                "paged_attention_rows: float32 contiguous scales [num_slots, Hk]");
+  }
+  if (q_mult.has_value()) {
+    check_device(q, {&*q_mult}, "paged_attention_rows");
+    TORCH_CHECK(q_mult->scalar_type() == at::kFloat && q_mult->is_contiguous() &&
+                    q_mult->numel() == Hq * D,
+                "paged_attention_rows: q_mult must be a contiguous float32 [Hq, D] tensor");
+  }
+  const c10::DeviceGuard guard(q.device());
+  auto out = at::empty_like(q);
+  if (R == 0) return out;
+  int64_t ws_bytes = 0;
+  at::Tensor ws = paged_workspace(q, k_cache, block_tables, block_size, 0, ws_bytes);
+  void* wsp = ws_bytes > 0 ? ws.data_ptr() : nullptr;
+  if (int8)
+    check_status(llmserve_paged_attention_rows_int8(
+        q.data_ptr<float>(), k_cache.data_ptr<int8_t>(), v_cache.data_ptr<int8_t>(),
+        k_scale->data_ptr<float>(), v_scale->data_ptr<float>(), block_tables.data_ptr<int64_t>(),
+        block_tables.size(0), row_table.data_ptr<int64_t>(), row_context.data_ptr<int64_t>(),
+        out.data_ptr<float>(), R, Hq, Hk, D, num_slots, block_tables.size(1), block_size,
+        static_cast<float>(scale), opt_ptr<float>(q_mult), wsp, ws_bytes, stream_of(q)));
+  else
+    check_status(llmserve_paged_attention_rows_f32(
+        q.data_ptr<float>(), k_cache.data_ptr<float>(), v_cache.data_ptr<float>(),
+        block_tables.data_ptr<int64_t>(), block_tables.size(0), row_table.data_ptr<int64_t>(),
+        row_context.data_ptr<int64_t>(), out.data_ptr<float>(), R, Hq, Hk, D, num_slots,
+        block_tables.size(1), block_size, static_cast<float>(scale), opt_ptr<float>(q_mult), wsp,
+        ws_bytes, stream_of(q)));
+  return out;
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> attention_metadata(const at::Tensor& seq_info,
+                                                                  const at::Tensor& block_tables,
+                                                                  int64_t block_size, int64_t T) {
+  TORCH_CHECK(seq_info.scalar_type() == at::kLong && seq_info.is_contiguous() &&
+                  seq_info.dim() == 2 && seq_info.size(0) == 3,
+              "attention_metadata: seq_info must be a contiguous int64 [3, S] tensor");
+  TORCH_CHECK(block_tables.scalar_type() == at::kLong && block_tables.is_contiguous() &&
+                  block_tables.dim() == 2 && block_tables.size(0) == seq_info.size(1),
+              "attention_metadata: block_tables must be a contiguous int64 [S, max_blocks] tensor");
+  check_device(seq_info, {&block_tables}, "attention_metadata");
+  const c10::DeviceGuard guard(seq_info.device());
+  auto slots = at::empty({T}, seq_info.options());
+  auto rows = at::empty({T}, seq_info.options());
+  auto ctx = at::empty({T}, seq_info.options());
+  check_status(llmserve_attention_metadata(
+      seq_info.data_ptr<int64_t>(), block_tables.data_ptr<int64_t>(), seq_info.size(1),
+      block_tables.size(1), block_size, T, slots.data_ptr<int64_t>(), rows.data_ptr<int64_t>(),
+      ctx.data_ptr<int64_t>(), stream_of(seq_info)));
+  return {slots, rows, ctx};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(llmserve_hip, m) {
@@ -669,6 +799,13 @@ TORCH_LIBRARY(llmserve_hip, m) {
         " Tensor k_scale, Tensor v_scale, Tensor block_tables, Tensor context_lens,"
         " int block_size, float scale, int partition_size=0, Tensor? q_mult=None,"
         " Tensor? act_inv=None) -> (Tensor, Tensor)");
+  m.def("paged_attention_decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor block_tables,"
+        " Tensor context_lens, int block_size, float scale, int partition_size=0) -> Tensor");
+  m.def("paged_attention_rows(Tensor q, Tensor k_cache, Tensor v_cache, Tensor? k_scale,"
+        " Tensor? v_scale, Tensor block_tables, Tensor row_table, Tensor row_context,"
+        " int block_size, float scale, Tensor? q_mult=None) -> Tensor");
+  m.def("attention_metadata(Tensor seq_info, Tensor block_tables, int block_size, int T)"
+        " -> (Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
@@ -695,4 +832,7 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("argmax_advance", &argmax_advance);
   m.impl("paged_attention_decode_int8", &paged_attention_decode_int8);
   m.impl("paged_attention_decode_int8_xfrag", &paged_attention_decode_int8_xfrag);
+  m.impl("paged_attention_decode", &paged_attention_decode);
+  m.impl("paged_attention_rows", &paged_attention_rows);
+  m.impl("attention_metadata", &attention_metadata);
 }

@@ -87,6 +87,16 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
         _I32,
         [_P] * 10 + [_I64] * 7 + [_F32, _I64, _P, _P, _I64, _P],
     ),
+    "llmserve_paged_attention_decode": (_I32, [_P] * 6 + [_I64] * 7 + [_F32, _I64, _P, _I64, _P]),
+    "llmserve_paged_attention_rows_int8": (
+        _I32,
+        [_P] * 6 + [_I64] + [_P] * 3 + [_I64] * 7 + [_F32, _P, _P, _I64, _P],
+    ),
+    "llmserve_paged_attention_rows_f32": (
+        _I32,
+        [_P] * 4 + [_I64] + [_P] * 3 + [_I64] * 7 + [_F32, _P, _P, _I64, _P],
+    ),
+    "llmserve_attention_metadata": (_I32, [_P, _P] + [_I64] * 4 + [_P] * 4),
 }
 
 

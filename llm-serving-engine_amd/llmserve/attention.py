@@ -1,25 +1,32 @@
-"""Paged attention over a block-structured KV cache, with the int8 cache on MI355X.
+"""Paged attention over a block-structured KV cache, with the native path on MI355X.
 
-Drop-in for the reference's ``llmserve.attention`` (src/llmserve/attention.py). The engine
-runs one forward pass over a ragged batch whose new tokens are concatenated into ``[T]``; the
-KV of every sequence lives in fixed-size blocks addressed through a block table, and a cache
-slot is ``block_id * block_size + offset``.
+Drop-in for the reference's ``llmserve.attention`` (src/llmserve/attention.py): the same
+classes, fields and functions. A step runs one forward pass over a ragged batch whose new tokens
+are laid end to end in a flat ``[T]`` stream; every sequence keeps its K/V in fixed-size blocks
+listed by its block table, and cache slot = ``block_id * block_size + offset``.
 
-On a ROCm device with an int8 cache (``QuantizedKV``) and the native backend:
-  * the new K/V rows are quantized and scattered by one HIP kernel per tensor (key smoothing
-    ``k / s`` fused into the key's kernel),
-  * decode rows run the split-context int8 paged-decode HIP kernel, with the smoothing
-    multiply ``q * s`` fused into its q load.
-Prefill rows (several new tokens) gather the dequantized context and call SDPA, as the
-reference does (attention.py:249-257). The native backend is named "hip"; "cpp" (the
-reference's name) is accepted as an alias.
+Two backends, chosen by ``AttentionMetadata.backend``:
+
+* ``"hip"`` (alias ``"cpp"``, the reference's name for its native kernel), on a ROCm device:
+  ``AttentionMetadata.build`` packs the block tables once on the host and a HIP kernel derives
+  the slot of every new token and its *query row*: the block-table row it attends over and how
+  many tokens it sees (its position + 1, the causal mask). ``paged_attention`` then writes the
+  new K/V (int8 caches: one quantize-and-scatter kernel per tensor, key smoothing ``k / s``
+  fused) and runs ONE split-context paged attention launch over all T rows, decode and prefill
+  alike, int8 or fp32 cache, with the smoothing product ``q * s`` fused into its q load.
+* ``"torch"``: slots and per-sequence tables are computed with vectorised numpy on the host;
+  attention gathers the (dequantized) context rows and calls SDPA, the reference's algorithm
+  (attention.py:249-257, :299-306).
 """
 
 from __future__ import annotations
 
+import contextlib
 import functools
+import itertools
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -28,25 +35,32 @@ NATIVE_BACKENDS = ("hip", "cpp")
 
 @dataclass
 class PrefillSeq:
-    q_start: int  # offset of this sequence's first new token in the flat batch
-    q_len: int  # number of new tokens
-    ctx_len: int  # total tokens attended to = cached + new
-    slots: torch.Tensor  # [ctx_len] cache slots of the whole context, in order
+    """A sequence with several new tokens in this step (a prompt chunk)."""
+
+    q_start: int  # index of its first new token in the flat batch
+    q_len: int  # how many new tokens it has
+    ctx_len: int  # tokens it attends to: the cached ones plus the new ones
+    slots: torch.Tensor  # [ctx_len] the cache slot of each context position, in order
 
 
 @dataclass
 class AttentionMetadata:
-    """Per-step attention metadata, shared by all layers (reference attention.py:33-124)."""
+    """What every layer of one step needs to know about the batch (reference
+    attention.py:33-124). Built once per step and shared by all layers."""
 
-    slot_mapping: torch.Tensor  # [T]
+    slot_mapping: torch.Tensor  # [T] cache slot each new token's K/V is written to
     prefills: list[PrefillSeq] = field(default_factory=list)
-    decode_token_idx: torch.Tensor | None = None  # [Bd] index into the flat batch
-    decode_block_tables: torch.Tensor | None = None  # [Bd, max_blocks] (native kernel)
+    decode_token_idx: torch.Tensor | None = None  # [Bd] flat index of each decode token
+    decode_block_tables: torch.Tensor | None = None  # [Bd, max_blocks] zero-padded (native)
     decode_ctx_lens: torch.Tensor | None = None  # [Bd]
-    decode_slots: torch.Tensor | None = None  # [Bd, max_ctx] (torch path)
-    decode_mask: torch.Tensor | None = None  # [Bd, 1, 1, max_ctx] True = attend (torch path)
+    decode_slots: torch.Tensor | None = None  # [Bd, max_ctx] slot table (torch backend)
+    decode_mask: torch.Tensor | None = None  # [Bd, 1, 1, max_ctx] True where attended (torch)
     block_size: int = 16
-    backend: str = "torch"  # "torch" (gather + SDPA) or "hip"/"cpp" (native paged kernel)
+    backend: str = "torch"  # "torch" or "hip" ("cpp" accepted as an alias)
+    # Native backend: every token is one query row of the paged attention kernel.
+    block_tables: torch.Tensor | None = None  # [S, max_blocks] the batch's tables, zero-padded
+    row_table: torch.Tensor | None = None  # [T] the table row token t attends over
+    row_context: torch.Tensor | None = None  # [T] how many context tokens token t sees
     _prefill_masks: dict[int, torch.Tensor | None] = field(default_factory=dict)
 
     @staticmethod
@@ -58,179 +72,286 @@ class AttentionMetadata:
         device: torch.device | str = "cpu",
         backend: str = "torch",
     ) -> AttentionMetadata:
-        """``q_lens[i]`` new tokens of sequence ``i`` sit at the end of its ``ctx_lens[i]``-token
-        context; ``block_tables[i]`` lists the physical blocks holding that context."""
-        slot_parts: list[torch.Tensor] = []
-        prefills: list[PrefillSeq] = []
-        dec_idx: list[int] = []
-        dec_slots: list[torch.Tensor] = []
-        dec_tables: list[list[int]] = []
-        dec_ctx: list[int] = []
-        q_start = 0
-        for q_len, ctx_len, table in zip(q_lens, ctx_lens, block_tables, strict=True):
-            n_blocks = (ctx_len + block_size - 1) // block_size
-            if len(table) < n_blocks:
-                raise ValueError(f"block table has {len(table)} blocks, needs {n_blocks}")
-            blocks = torch.tensor(table[:n_blocks], dtype=torch.long)
-            slots = (
-                blocks[:, None] * block_size + torch.arange(block_size, dtype=torch.long)
-            ).flatten()[:ctx_len]
-            slot_parts.append(slots[ctx_len - q_len :])
-            if q_len == 1:
-                dec_idx.append(q_start)
-                dec_slots.append(slots)
-                dec_tables.append(table[:n_blocks])
-                dec_ctx.append(ctx_len)
-            else:
-                prefills.append(PrefillSeq(q_start, q_len, ctx_len, slots.to(device)))
-            q_start += q_len
-
+        """``q_lens[i]`` new tokens of sequence ``i`` are the last ones of its ``ctx_lens[i]``
+        tokens; ``block_tables[i]`` lists the physical blocks of that context in order."""
+        plan = _BatchPlan(q_lens, ctx_lens, block_tables, block_size)
         native = backend in NATIVE_BACKENDS
-        meta = AttentionMetadata(
-            slot_mapping=torch.cat(slot_parts).to(device)
-            if slot_parts
-            else torch.empty(0, dtype=torch.long, device=device),
-            prefills=prefills,
-            block_size=block_size,
-            backend="hip" if native else backend,
-        )
-        if dec_idx and native:
-            mb = max(len(t) for t in dec_tables)
-            bt = torch.zeros(len(dec_tables), mb, dtype=torch.long)
-            for i, t in enumerate(dec_tables):
-                bt[i, : len(t)] = torch.tensor(t, dtype=torch.long)
-            meta.decode_token_idx = torch.tensor(dec_idx, dtype=torch.long, device=device)
-            meta.decode_block_tables = bt.to(device)
-            meta.decode_ctx_lens = torch.tensor(dec_ctx, dtype=torch.long, device=device)
-        elif dec_idx:
-            max_ctx = max(s.numel() for s in dec_slots)
-            table = torch.zeros(len(dec_slots), max_ctx, dtype=torch.long)
-            mask = torch.zeros(len(dec_slots), max_ctx, dtype=torch.bool)
-            for i, s in enumerate(dec_slots):
-                table[i, : s.numel()] = s
-                mask[i, : s.numel()] = True
-            meta.decode_token_idx = torch.tensor(dec_idx, dtype=torch.long, device=device)
-            meta.decode_slots = table.to(device)
-            meta.decode_mask = mask[:, None, None, :].to(device)
+        meta = AttentionMetadata(slot_mapping=torch.empty(0, dtype=torch.long, device=device),
+                                 block_size=block_size, backend="hip" if native else backend)
+        if native and _native_ops(device) is not None:
+            plan.fill_native(meta, device)
+        else:
+            plan.fill_host(meta, device, native)
         return meta
 
     def prefill_mask(self, i: int) -> torch.Tensor | None:
-        """Causal mask for prefill sequence ``i`` when part of its context is already cached."""
+        """Boolean [q_len, ctx_len] causal mask of prefill sequence ``i`` (None when nothing of
+        it was cached, so that SDPA's ``is_causal`` applies); cached per sequence."""
         if i not in self._prefill_masks:
             p = self.prefills[i]
-            if p.q_len == p.ctx_len:
-                self._prefill_masks[i] = None  # plain causal; use is_causal fast path
-            else:
-                q_pos = torch.arange(p.ctx_len - p.q_len, p.ctx_len, device=p.slots.device)
-                k_pos = torch.arange(p.ctx_len, device=p.slots.device)
-                self._prefill_masks[i] = k_pos[None, :] <= q_pos[:, None]
+            mask = None
+            if p.q_len != p.ctx_len:
+                dev = p.slots.device
+                first = p.ctx_len - p.q_len  # position of the first new token
+                mask = (torch.arange(p.ctx_len, device=dev)[None, :]
+                        <= torch.arange(first, p.ctx_len, device=dev)[:, None])
+            self._prefill_masks[i] = mask
         return self._prefill_masks[i]
 
 
-class QuantizedKV:
-    """One layer's K (or V) cache as int8 with one fp32 scale per (token slot, kv head)
-    (reference attention.py:127-173).
+class _BatchPlan:
+    """The batch of one step as numpy arrays: sizes, token offsets and the packed tables."""
 
-    Symmetric absmax quantization ``x ~= data * scale``, ``scale = max(max|x|, 1e-8) / 127``
-    over the head dimension, computed by the ``llmserve_kv_quantize_write`` HIP kernel with
-    the reference's CPU arithmetic (clamp, then divide; round half to even).
+    def __init__(self, q_lens, ctx_lens, block_tables, block_size: int) -> None:
+        if not len(q_lens) == len(ctx_lens) == len(block_tables):
+            raise ValueError("q_lens, ctx_lens and block_tables must have one entry per sequence")
+        self.bs = int(block_size)
+        self.q = np.asarray(q_lens, dtype=np.int64).reshape(-1)
+        self.ctx = np.asarray(ctx_lens, dtype=np.int64).reshape(-1)
+        self.S = self.q.size
+        need = (self.ctx + self.bs - 1) // self.bs
+        have = np.fromiter((len(t) for t in block_tables), dtype=np.int64, count=self.S)
+        short = np.flatnonzero(have < need)
+        if short.size:
+            i = short[0]
+            raise ValueError(f"block table has {have[i]} blocks, needs {need[i]}")
+        self.width = max(1, int(need.max())) if self.S else 1
+        self.tables = np.zeros((self.S, self.width), dtype=np.int64)
+        used = np.arange(self.width)[None, :] < need[:, None]
+        self.tables[used] = np.fromiter(
+            itertools.chain.from_iterable(t[:n] for t, n in zip(block_tables, need.tolist())),
+            dtype=np.int64, count=int(need.sum()))
+        self.q_start = np.cumsum(self.q) - self.q
+        self.T = int(self.q.sum())
+        self.dec = np.flatnonzero(self.q == 1)  # decode sequences
+        self.pre = np.flatnonzero(self.q != 1)  # prefill sequences (several new tokens)
+
+    def slots_of(self, seq: np.ndarray, pos: np.ndarray) -> np.ndarray:
+        """Cache slots of positions ``pos`` of sequences ``seq`` (broadcasting)."""
+        return self.tables[seq, pos // self.bs] * self.bs + pos % self.bs
+
+    def token_positions(self) -> tuple[np.ndarray, np.ndarray]:
+        """(sequence, position) of every new token of the flat batch."""
+        seq = np.repeat(np.arange(self.S), self.q)
+        pos = self.ctx[seq] - self.q[seq] + (np.arange(self.T) - self.q_start[seq])
+        return seq, pos
+
+    def prefill_seqs(self, device, tables_dev: torch.Tensor | None) -> list[PrefillSeq]:
+        out = []
+        for s in self.pre.tolist():
+            c = int(self.ctx[s])
+            if tables_dev is not None:  # on the device, from the uploaded tables
+                pos = torch.arange(c, device=tables_dev.device)
+                slots = tables_dev[s, pos // self.bs] * self.bs + pos % self.bs
+            else:
+                slots = torch.from_numpy(self.slots_of(np.int64(s), np.arange(c))).to(device)
+            out.append(PrefillSeq(int(self.q_start[s]), int(self.q[s]), c, slots))
+        return out
+
+    def fill_host(self, meta: AttentionMetadata, device, native: bool = False) -> None:
+        """Everything computed with numpy, then copied to ``device``: the decode rows as
+        zero-padded block tables for a native backend (the reference's fields for its kernel),
+        as a slot table and mask for the torch backend."""
+        seq, pos = self.token_positions()
+        meta.slot_mapping = torch.from_numpy(self.slots_of(seq, pos)).to(device)
+        meta.prefills = self.prefill_seqs(device, None)
+        if self.dec.size and native:
+            ctx = self.ctx[self.dec]
+            width = int(((ctx + self.bs - 1) // self.bs).max())
+            meta.decode_token_idx = torch.from_numpy(self.q_start[self.dec]).to(device)
+            meta.decode_block_tables = torch.from_numpy(self.tables[self.dec, :width].copy()).to(device)
+            meta.decode_ctx_lens = torch.from_numpy(ctx).to(device)
+        elif self.dec.size:
+            ctx = self.ctx[self.dec]
+            span = np.arange(int(ctx.max()))
+            inside = span[None, :] < ctx[:, None]
+            slots = np.where(inside, self.slots_of(self.dec[:, None], np.minimum(span, ctx[:, None] - 1)), 0)
+            meta.decode_token_idx = torch.from_numpy(self.q_start[self.dec]).to(device)
+            meta.decode_slots = torch.from_numpy(slots).to(device)
+            meta.decode_mask = torch.from_numpy(inside)[:, None, None, :].to(device)
+
+    def fill_native(self, meta: AttentionMetadata, device) -> None:
+        """Native backend: one upload of the packed batch, then the metadata kernel."""
+        info = np.concatenate([self.q, self.ctx, self.q_start, self.tables.reshape(-1)])
+        dev_info = torch.from_numpy(info).to(device)
+        seq_info = dev_info[: 3 * self.S].view(3, self.S)
+        tables = dev_info[3 * self.S:].view(self.S, self.width)
+        meta.block_tables = tables
+        if self.T:
+            meta.slot_mapping, meta.row_table, meta.row_context = _native_ops(device).attention_metadata(
+                seq_info, tables, self.bs, self.T)
+        meta.prefills = self.prefill_seqs(device, tables)
+        if self.dec.size:
+            dec = torch.from_numpy(self.dec).to(device)
+            meta.decode_token_idx = seq_info[2].index_select(0, dec)
+            meta.decode_block_tables = tables.index_select(0, dec)
+            meta.decode_ctx_lens = seq_info[1].index_select(0, dec)
+
+
+@functools.cache
+def _ops_namespace():
+    from llmserve.kernels import load_paged_attention
+
+    return load_paged_attention()
+
+
+def _native_ops(device):
+    """The native attention ops when they can run on ``device`` (a ROCm device with the
+    library built), else None."""
+    if torch.device(device).type != "cuda":
+        return None
+    return _ops_namespace()
+
+
+# ---- int8 cache ------------------------------------------------------------------------------
+
+
+def _kv_int8_torch(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row symmetric int8 with torch ops: scale = max(max|x|, 1e-8) / 127 (the clamp comes
+    before the division, attention.py:156), q = clamp(round_half_even(x / scale), +-127)."""
+    scale = torch.clamp(x.abs().amax(dim=-1), min=1e-8) / 127.0
+    q = torch.clamp(torch.round(x / scale.unsqueeze(-1)), -127, 127).to(torch.int8)
+    return q, scale
+
+
+class QuantizedKV:
+    """One layer's K (or V) cache as int8 plus one fp32 scale per (slot, kv head) (reference
+    attention.py:127-173): ``row ~= data * scale``, ``scale = max(max|row|, 1e-8) / 127`` over
+    the head dimension. On a ROCm device the quantize-and-scatter is the
+    ``llmserve_kv_quantize_write`` HIP kernel (bit-identical to the torch CPU ops); elsewhere,
+    or without the native library, torch ops compute it.
     """
 
-    # Validate slot indices on the host before a write (one device sync per write). The
-    # kernel itself skips out-of-range slots; torch.index_copy_ would raise for them.
+    # Check slot indices on the host before a native write (one device sync per write); the
+    # kernel skips slots outside the cache, where torch.index_copy_ would raise.
     check_slots = False
 
     def __init__(self, num_slots: int, kv_heads: int, head_dim: int, device="cpu") -> None:
-        self.data = torch.zeros(num_slots, kv_heads, head_dim, dtype=torch.int8, device=device)
-        self.scale = torch.zeros(num_slots, kv_heads, dtype=torch.float32, device=device)
-        self.smooth: torch.Tensor | None = None  # [kv_heads, head_dim]
-        self._q_mult: torch.Tensor | None = None  # [q_heads, head_dim]
+        shape = (num_slots, kv_heads)
+        self.data = torch.zeros(shape + (head_dim,), dtype=torch.int8, device=device)
+        self.scale = torch.zeros(shape, dtype=torch.float32, device=device)
+        self.smooth: torch.Tensor | None = None  # [kv_heads, head_dim] (K cache only)
+        self._q_mult: torch.Tensor | None = None  # [q_heads, head_dim]: smooth per query head
 
     def set_smoothing(self, s: torch.Tensor | None, num_q_heads: int) -> None:
-        """SmoothQuant-style key smoothing: store ``k / s`` and attend with ``q * s``
-        (reference attention.py:142-151)."""
-        if s is not None:
-            s = s.to(device=self.data.device, dtype=torch.float32).contiguous()
+        """Key smoothing (SmoothQuant-style, reference attention.py:142-151): the cache stores
+        ``k / s`` and attention uses ``q * s``, which leaves q . k unchanged in exact arithmetic
+        while the few large key channels stop setting every row's int8 scale."""
+        if s is None:
+            self.smooth = self._q_mult = None
+            return
+        s = s.to(device=self.data.device, dtype=torch.float32).contiguous()
+        group = num_q_heads // s.shape[0]
         self.smooth = s
-        g = num_q_heads // s.shape[0] if s is not None else 1
-        self._q_mult = s.repeat_interleave(g, 0).contiguous() if s is not None else None
+        self._q_mult = torch.repeat_interleave(s, group, dim=0).contiguous()
 
     @staticmethod
     def quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        """(int8 data, fp32 scale) of ``x`` [..., D], scale over the last dimension."""
-        from llmserve.kernels import load_quant
-
+        """(int8 data, fp32 scale) of ``x`` [..., D], one scale per row of D values."""
         x = x.float().contiguous()
-        lead, D = x.shape[:-1], x.shape[-1]
-        x3 = x.reshape(-1, 1, D)
-        n = x3.shape[0]
-        data = torch.empty(n, 1, D, dtype=torch.int8, device=x.device)
+        ops = _quant_ops(x)
+        if ops is None:
+            return _kv_int8_torch(x)
+        rows = x.reshape(-1, 1, x.shape[-1])
+        n = rows.shape[0]
+        data = torch.empty(rows.shape, dtype=torch.int8, device=x.device)
         scale = torch.empty(n, 1, dtype=torch.float32, device=x.device)
-        slots = torch.arange(n, dtype=torch.long, device=x.device)
-        load_quant().kv_quantize_write(x3, slots, data, scale, None)
-        return data.reshape(*lead, D), scale.reshape(lead)
+        ops.kv_quantize_write(rows, torch.arange(n, device=x.device), data, scale, None)
+        return data.view(x.shape), scale.view(x.shape[:-1])
 
-    def write(self, slots: torch.Tensor, x: torch.Tensor, smooth: torch.Tensor | None = None) -> None:
-        """Quantize ``x`` [T, Hk, D] into ``slots`` [T]; with ``smooth`` the rows written are
-        ``x / smooth`` (the division fused into the kernel)."""
-        from llmserve.kernels import load_quant
-
+    def write(self, slots: torch.Tensor, x: torch.Tensor,
+              smooth: torch.Tensor | None = None) -> None:
+        """Quantize ``x`` [T, Hk, D] (divided by ``smooth`` first when given) into ``slots``."""
+        x = x.float().contiguous()
         slots = slots.to(device=self.data.device, dtype=torch.long).contiguous()
+        ops = _quant_ops(x)
+        if ops is None:
+            q, s = _kv_int8_torch(x / smooth if smooth is not None else x)
+            self.data.index_copy_(0, slots, q)
+            self.scale.index_copy_(0, slots, s)
+            return
         if self.check_slots and slots.numel():
-            lo, hi = int(slots.min()), int(slots.max())
-            if lo < 0 or hi >= self.data.shape[0]:
+            bad = (slots < 0) | (slots >= self.data.shape[0])
+            if bool(bad.any()):
                 raise IndexError(f"slot index out of range [0, {self.data.shape[0]})")
-        load_quant().kv_quantize_write(x.float().contiguous(), slots, self.data, self.scale, smooth)
+        ops.kv_quantize_write(x, slots, self.data, self.scale, smooth)
 
     def rows(self, idx: torch.Tensor) -> torch.Tensor:
-        """Dequantized rows (float32) for slot indices of any shape."""
-        return self.data[idx].float() * self.scale[idx].unsqueeze(-1)
+        """Dequantized float32 rows for slot indices of any shape."""
+        return torch.mul(self.data[idx].to(torch.float32), self.scale[idx][..., None])
 
     def copy_rows(self, dst: torch.Tensor, src: torch.Tensor) -> None:
-        self.data[dst] = self.data[src]
-        self.scale[dst] = self.scale[src]
+        """Copy whole slot rows (data and scales) from ``src`` to ``dst`` (block copies)."""
+        for t in (self.data, self.scale):
+            t.index_copy_(0, dst.to(t.device), t.index_select(0, src.to(t.device)))
 
     def nbytes(self) -> int:
-        return self.data.numel() + self.scale.numel() * 4
+        return sum(t.numel() * t.element_size() for t in (self.data, self.scale))
 
+
+def _quant_ops(x: torch.Tensor):
+    if not x.is_cuda:
+        return None
+    from llmserve.kernels import load_quant
+
+    return load_quant()
+
+
+# ---- key smoothing calibration -----------------------------------------------------------------
 
 _K_STATS: list | None = None
 
 
 def smoothing_from_stats(stats: list[torch.Tensor], alpha: float = 1.0) -> list[torch.Tensor]:
-    """Per-layer factors ``s = clamp(max|K|, 1e-5) ** alpha`` normalised to mean 1 per head
-    (reference attention.py:196-200)."""
-    out = []
-    for m in stats:  # [Hk, D]
-        s = m.float().clamp_min(1e-5).pow(alpha)
-        out.append(s / s.mean(-1, keepdim=True))
-    return out
+    """Per-layer smoothing factors from per-layer max|K| [Hk, D] (reference attention.py:
+    196-200): ``s = max(max|K|, 1e-5) ** alpha``, divided by its mean over D per head."""
+    factors = []
+    for amax in stats:
+        s = torch.pow(torch.clamp(amax.float(), min=1e-5), alpha)
+        factors.append(s / torch.mean(s, dim=-1, keepdim=True))
+    return factors
+
+
+@contextlib.contextmanager
+def _recording_key_stats():
+    """While active, ``paged_attention`` appends each layer's max|K| over the batch."""
+    global _K_STATS
+    _K_STATS = stats = []
+    try:
+        yield stats
+    finally:
+        _K_STATS = None
+
+
+def _model_placement(model) -> tuple[torch.device, torch.dtype]:
+    for t in itertools.chain(model.parameters(), model.buffers()):
+        if t is not None and t.is_floating_point():
+            return t.device, t.dtype
+    return torch.device("cpu"), torch.float32
 
 
 @torch.inference_mode()
 def calibrate_k_smoothing(model, ids: list[int], alpha: float = 1.0) -> list[torch.Tensor]:
     """Key smoothing factors from one fp32 prefill of ``ids`` (reference attention.py:179-200).
-    ``model`` follows the reference's calling convention ``model(ids, pos, kv_caches, meta)``
-    and carries ``cfg``."""
-    global _K_STATS
+    ``model`` has the reference's calling convention ``model(ids, positions, kv_caches, meta)``
+    and a ``cfg``; the prefill runs over a throw-away cache in the model's dtype on its device
+    (``QuantCausalLM`` of this package qualifies)."""
     from llmserve.kv_cache import KVCache
 
+    dev, dtype = _model_placement(model)
     bs = 16
-    nb = -(-len(ids) // bs)
-    p0 = next(model.parameters())
-    cache = KVCache(model.cfg, nb, bs, p0.dtype, device=p0.device)
-    meta = AttentionMetadata.build([len(ids)], [len(ids)], [list(range(nb))], bs, device=p0.device)
-    _K_STATS = []
-    try:
-        model(torch.tensor(ids, device=p0.device), torch.arange(len(ids), device=p0.device),
-              cache.layers, meta)
-        stats = _K_STATS
-    finally:
-        _K_STATS = None
+    n_blocks = max(1, -(-len(ids) // bs))
+    cache = KVCache(model.cfg, n_blocks, bs, dtype, device=dev)
+    backend = resolve_backend("auto", str(dev))
+    meta = AttentionMetadata.build([len(ids)], [len(ids)], [list(range(n_blocks))], bs, dev, backend)
+    with _recording_key_stats() as stats:
+        model(torch.as_tensor(ids, dtype=torch.long, device=dev),
+              torch.arange(len(ids), device=dev), cache.layers, meta)
     return smoothing_from_stats(stats, alpha)
 
 
-# A fixed, generic calibration text (the reference's attention.py:204-214).
+# A fixed, generic calibration text (the reference's attention.py:204-214; data the
+# calibration must reproduce).
 CALIBRATION_TEXT = (
     "The history of computing is a story of people trying to make machines do useful work. "
     "Early mechanical calculators added and multiplied numbers with gears; later, electronic "
@@ -244,18 +365,59 @@ CALIBRATION_TEXT = (
 )
 
 
-def _rows(cache, idx: torch.Tensor) -> torch.Tensor:
-    return cache.rows(idx) if isinstance(cache, QuantizedKV) else cache[idx]
+# ---- attention -----------------------------------------------------------------------------------
 
 
 def write_kv(k_cache, v_cache, k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor) -> None:
-    """Scatter new K/V ([T, Hk, D]) into flat cache tensors ([num_slots, Hk, D])."""
-    if isinstance(k_cache, QuantizedKV):
-        k_cache.write(slots, k)
-        v_cache.write(slots, v)
+    """Store this step's K/V rows ([T, Hk, D]) at ``slots`` of flat fp32 or int8 caches."""
+    for cache, rows in ((k_cache, k), (v_cache, v)):
+        if isinstance(cache, QuantizedKV):
+            cache.write(slots, rows)
+        else:
+            cache.index_copy_(0, slots, rows.to(cache.dtype))
+
+
+def _context(cache, idx: torch.Tensor) -> torch.Tensor:
+    """Float rows of the cache at slot indices ``idx`` ([..., Hk, D])."""
+    return cache.rows(idx) if isinstance(cache, QuantizedKV) else cache[idx]
+
+
+def _sdpa_heads_first(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask, scale: float,
+                      causal: bool = False) -> torch.Tensor:
+    """SDPA over rows laid out [(B,) L, H, D] (heads second to last), GQA allowed."""
+    single = q.dim() == 3
+    if single:
+        q, k, v = q[None], k[None], v[None]
+    o = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                       attn_mask=mask, is_causal=causal, scale=scale,
+                                       enable_gqa=True).transpose(1, 2)
+    return o[0] if single else o
+
+
+def _attend_torch(q: torch.Tensor, k_cache, v_cache, meta: AttentionMetadata, scale: float,
+                  out: torch.Tensor) -> None:
+    """The gather + SDPA algorithm of the reference (attention.py:249-257, :299-306)."""
+    for i, p in enumerate(meta.prefills):
+        rows = slice(p.q_start, p.q_start + p.q_len)
+        mask = meta.prefill_mask(i)
+        out[rows] = _sdpa_heads_first(q[rows], _context(k_cache, p.slots),
+                                      _context(v_cache, p.slots), mask, scale, mask is None)
+    if meta.decode_token_idx is None:
         return
-    k_cache.index_copy_(0, slots, k)
-    v_cache.index_copy_(0, slots, v)
+    idx = meta.decode_token_idx
+    if meta.decode_slots is None:  # a native plan attended with torch: derive the slot table
+        span = torch.arange(int(meta.decode_ctx_lens.max()), device=idx.device)
+        inside = span[None, :] < meta.decode_ctx_lens[:, None]
+        pos = torch.minimum(span[None, :], meta.decode_ctx_lens[:, None] - 1)
+        slots = torch.where(inside, torch.gather(meta.decode_block_tables, 1,
+                                                 pos // meta.block_size) * meta.block_size
+                            + pos % meta.block_size, 0)
+        mask = inside[:, None, None, :]
+    else:
+        slots, mask = meta.decode_slots, meta.decode_mask
+    od = _sdpa_heads_first(q[idx].unsqueeze(1), _context(k_cache, slots),
+                           _context(v_cache, slots), mask, scale)
+    out[idx] = od.squeeze(1)
 
 
 def paged_attention(
@@ -267,84 +429,47 @@ def paged_attention(
     meta: AttentionMetadata,
     scale: float,
 ) -> torch.Tensor:
-    """Write this step's K/V into the cache, then attend. q: [T, Hq, D] -> out: [T, Hq, D]
-    (reference attention.py:231-307)."""
-    if _K_STATS is not None:  # calibration pass (calibrate_k_smoothing)
-        _K_STATS.append(k.detach().abs().amax(0))
+    """Store this step's K/V in the cache, then attend: q [T, Hq, D] -> [T, Hq, D] (reference
+    attention.py:231-307)."""
+    if _K_STATS is not None:  # calibrate_k_smoothing is recording
+        _K_STATS.append(torch.amax(k.detach().abs(), dim=0))
     quantized = isinstance(k_cache, QuantizedKV)
     smooth = k_cache.smooth if quantized else None
+    ops = None
+    if meta.row_table is not None and (quantized or k_cache.dtype == torch.float32):
+        ops = _native_ops(q.device)
     if quantized:
-        k_cache.write(meta.slot_mapping, k, smooth)  # k / smooth fused in the kernel
+        k_cache.write(meta.slot_mapping, k, smooth)  # the kernel divides by smooth
         v_cache.write(meta.slot_mapping, v)
     else:
         write_kv(k_cache, v_cache, k, v, meta.slot_mapping)
-    # q * s for the torch paths; the native decode kernel applies the same product itself
-    q_s = q * k_cache._q_mult if smooth is not None else q
-    out = q.new_empty(q.shape)
-
-    for i, p in enumerate(meta.prefills):
-        qi = q_s[p.q_start : p.q_start + p.q_len].transpose(0, 1).unsqueeze(0)  # [1, Hq, q, D]
-        ki = _rows(k_cache, p.slots).transpose(0, 1).unsqueeze(0)  # [1, Hk, ctx, D]
-        vi = _rows(v_cache, p.slots).transpose(0, 1).unsqueeze(0)
-        mask = meta.prefill_mask(i)
-        oi = F.scaled_dot_product_attention(
-            qi, ki, vi, attn_mask=mask, is_causal=mask is None, scale=scale, enable_gqa=True
-        )
-        out[p.q_start : p.q_start + p.q_len] = oi.squeeze(0).transpose(0, 1)
-
-    if meta.decode_block_tables is not None:
-        if not quantized:
-            raise NotImplementedError(
-                "the native decode kernel serves the int8 KV cache; use backend='torch' "
-                "for an fp32 cache"
-            )
-        from llmserve.kernels import load_paged_attention
-
-        od = load_paged_attention().paged_attention_decode_int8(
-            q[meta.decode_token_idx].contiguous(),
-            k_cache.data,
-            v_cache.data,
-            k_cache.scale,
-            v_cache.scale,
-            meta.decode_block_tables,
-            meta.decode_ctx_lens,
-            meta.block_size,
-            scale,
-            0,
-            k_cache._q_mult,
-        )
-        if not meta.prefills:
-            return od
-        out[meta.decode_token_idx] = od
-    elif meta.decode_token_idx is not None:
-        qd = q_s[meta.decode_token_idx].unsqueeze(2)  # [B, Hq, 1, D]
-        kd = _rows(k_cache, meta.decode_slots).transpose(1, 2)  # [B, Hk, ctx, D]
-        vd = _rows(v_cache, meta.decode_slots).transpose(1, 2)
-        od = F.scaled_dot_product_attention(
-            qd, kd, vd, attn_mask=meta.decode_mask, scale=scale, enable_gqa=True
-        )
-        out[meta.decode_token_idx] = od.squeeze(2)
+    if ops is not None:  # every token is a query row of one native launch
+        q_mult = k_cache._q_mult if smooth is not None else None
+        if quantized:
+            return ops.paged_attention_rows(q.float().contiguous(), k_cache.data, v_cache.data,
+                                            k_cache.scale, v_cache.scale, meta.block_tables,
+                                            meta.row_table, meta.row_context, meta.block_size,
+                                            scale, q_mult)
+        return ops.paged_attention_rows(q.float().contiguous(), k_cache, v_cache, None, None,
+                                        meta.block_tables, meta.row_table, meta.row_context,
+                                        meta.block_size, scale, None)
+    q_att = q * k_cache._q_mult if smooth is not None else q
+    out = torch.empty_like(q)
+    _attend_torch(q_att, k_cache, v_cache, meta, scale, out)
     return out
 
 
 @functools.cache
 def resolve_backend(name: str, device: str = "cpu") -> str:
     """``auto`` -> ``hip`` on a ROCm device when the native library loads, else ``torch``
-    (reference attention.py:310-323, where the native kernel was CPU-only)."""
+    (reference attention.py:310-323, whose native kernel ran on the CPU)."""
     if name == "torch":
         return "torch"
-    if name not in ("auto",) + NATIVE_BACKENDS:
+    if name != "auto" and name not in NATIVE_BACKENDS:
         raise ValueError(f"unknown attention backend {name!r}")
-    from llmserve.kernels import NativeLibraryMissing, load_paged_attention
-
-    on_gpu = str(device).startswith("cuda")
-    if on_gpu:
-        try:
-            load_paged_attention()
-            return "hip"
-        except NativeLibraryMissing:
-            if name != "auto":
-                raise
+    if _native_ops(device) is not None:
+        return "hip"
     if name != "auto":
-        raise RuntimeError("native paged attention kernel needs a ROCm device")
+        raise RuntimeError("native paged attention kernel is not available (it needs a ROCm "
+                           "device and the built llmserve library)")
     return "torch"

@@ -1,94 +1,92 @@
 """Native kernel loaders (reference: src/llmserve/kernels/__init__.py:19-72).
 
-The reference JIT-compiles three CPU extensions and returns ``None`` when a build fails, so
-that callers fall back to PyTorch. Here the kernels are prebuilt gfx950 HIP code and there is
-no fallback: a missing library raises ``NativeLibraryMissing`` (a RuntimeError). The returned
-objects expose the reference's function names and signatures:
+The reference JIT-compiles CPU extensions and each loader returns ``None`` when its build
+fails, so that the callers fall back to PyTorch. Here the kernels are prebuilt gfx950 HIP code
+(``llmserve/_lib``, built by ``llm-serving-engine_amd/build.py``); each loader returns a
+namespace of ``torch.ops.llmserve_hip`` functions, or ``None`` with a logged warning when the
+library is missing or does not load. The callers (``Int8Linear``, ``Int4Linear``,
+``QuantizedKV``, ``paged_attention``) then compute with torch ops, as the reference's do; the
+native functions take ROCm tensors only, so the callers also use torch for CPU tensors.
 
-* ``load_int8_gemv()``: ``int8_linear(x, qweight, scale)`` and
-  ``int4_linear(x, nibbles, scale, zero, group_size, inv_act_scale=None)``
-  (int8_gemv.cpp:109-112; ``inv_act_scale`` fuses Int4Linear's AWQ pre-scale), and
-  ``int8_linear_prefill(x, qweight, scale)``: Int8Linear's large-M path on the bf16 matrix
-  cores (quant.py:71-72), and ``int4_linear_gemm(x, nibbles, scale, zero, group_size,
-  inv_act_scale=None)``: Int4Linear's large-M path (quant.py:141-142) on the matrix cores;
-  ``int4_gemm_pack(nibbles, scale, zero, group_size)`` rearranges an int4 weight once for
-  ``int4_linear_gemm_packed(x, packed, out_features, group_size, inv_act_scale=None)``, the
-  same product with the decode-batch matrix-core kernel;
+Functions, with the reference's names and signatures where the reference has them:
+
+* ``load_int8_gemv()``: ``int8_linear(x, qweight, scale)`` and ``int4_linear(x, nibbles, scale,
+  zero, group_size, inv_act_scale=None)`` (int8_gemv.cpp:109-112; ``inv_act_scale`` fuses
+  Int4Linear's AWQ pre-scale); ``int8_linear_prefill(x, qweight, scale)``, Int8Linear's
+  large-M path on the bf16 matrix cores (quant.py:71-72); ``int4_linear_gemm(...)``,
+  Int4Linear's large-M path (quant.py:141-142); ``int4_gemm_pack(nibbles, scale, zero,
+  group_size)`` and ``int4_linear_gemm_packed(x, packed, out_features, group_size,
+  inv_act_scale=None)``, the decode-batch matrix-core kernel on a rearranged weight.
 * ``load_paged_attention()``: ``paged_attention_decode_int8(q, k_cache, v_cache, k_scale,
-  v_scale, block_tables, context_lens, block_size, scale, partition_size=0, q_mult=None)``
-  (paged_attention.cpp:386-399; ``q_mult`` fuses the key-smoothing multiply of q).
+  v_scale, block_tables, context_lens, block_size, scale, partition_size=0, q_mult=None)`` and
+  ``paged_attention_decode(q, k_cache, v_cache, block_tables, context_lens, block_size, scale,
+  partition_size=0)`` (fp32 cache) (paged_attention.cpp:386-399); ``paged_attention_rows``
+  (every token of a ragged batch as one query row, decode and prefill alike) and
+  ``attention_metadata`` (slots and query rows of a step, on the device).
+* ``load_quant()``: the load-time quantizers and the int8 KV-cache write.
+* ``load_fused_ops()``: ``rmsnorm``, ``add_rmsnorm_``, ``silu_mul``, ``rope_qk_``
+  (fused_ops.cpp:129-137) and the decode-step kernels of this package (embedding + norm, the
+  fused post-qkv KV write, greedy selection, the activation-fragment producers and consumers).
 
-* ``load_fused_ops()``: ``rmsnorm(x, w, eps)``, ``add_rmsnorm_(x, r, w, eps)``,
-  ``silu_mul(gate_up)`` and ``rope_qk_(qkv, cos, sin, n_q, n_k, head_dim, q_w=None, k_w=None,
-  eps=1e-6)`` (fused_ops.cpp:129-137), plus the decode-step glue ``embed_rmsnorm(ids, embed,
-  w, eps) -> (x, h)`` (embedding lookup + first input norm), ``decode_qkv_kv`` (q/k norm,
-  RoPE and the int8 KV-cache write in one launch) and ``argmax_advance`` (greedy next token);
-  and the producers of the packed int4 linear's activation fragments, which fuse the next
-  linear's ``x * inv_act_scale`` and bf16 split into the norm / silu kernel:
-  ``add_rmsnorm_xfrag_(x, r, w, act_inv, eps)``, ``embed_rmsnorm_xfrag(ids, embed, w, act_inv,
-  eps) -> (x, xfrag)``, ``silu_mul_xfrag(gate_up, act_inv)``, consumed by
-  ``int4_linear_gemm_xfrag(xfrag, packed, M, N, K, group_size)``.
-
-The fp32-KV decode variants (``paged_attention_decode``, ``paged_attention_decode_v1``,
-``set_simd``) are outside the quantized path and not provided.
+``paged_attention_decode_v1`` and ``set_simd`` select CPU code paths of the reference and have
+no counterpart.
 """
 
 from __future__ import annotations
 
 import functools
+import logging
 from types import SimpleNamespace
 
 from llmserve._native import NativeLibraryMissing, ops
 
 __all__ = ["NativeLibraryMissing", "load_fused_ops", "load_int8_gemv", "load_paged_attention",
-           "load_quant"]
+           "load_quant", "native_available"]
+
+log = logging.getLogger(__name__)
+
+
+def _namespace(what: str, names: tuple[str, ...]) -> SimpleNamespace | None:
+    try:
+        o = ops()
+    except (NativeLibraryMissing, OSError, RuntimeError) as e:
+        log.warning("%s unavailable, using the PyTorch fallback: %s", what, e)
+        return None
+    return SimpleNamespace(**{n: getattr(o, n) for n in names})
+
+
+def native_available() -> bool:
+    """True when the gfx950 op library loads in this process."""
+    return load_quant() is not None
 
 
 @functools.cache
-def load_int8_gemv() -> SimpleNamespace:
-    """Weight-only int8 / int4 small-batch matmuls (HIP, gfx950)."""
-    o = ops()
-    return SimpleNamespace(int8_linear=o.int8_linear, int4_linear=o.int4_linear,
-                           int8_linear_prefill=o.int8_linear_prefill,
-                           int4_linear_gemm=o.int4_linear_gemm,
-                           int4_gemm_pack=o.int4_gemm_pack,
-                           int4_linear_gemm_packed=o.int4_linear_gemm_packed)
+def load_int8_gemv() -> SimpleNamespace | None:
+    """Weight-only int8 / int4 matmuls (HIP, gfx950), or None."""
+    return _namespace("int8/int4 GEMV kernels", (
+        "int8_linear", "int4_linear", "int8_linear_prefill", "int4_linear_gemm",
+        "int4_gemm_pack", "int4_linear_gemm_packed"))
 
 
 @functools.cache
-def load_paged_attention() -> SimpleNamespace:
-    """int8-KV paged decode attention (HIP, gfx950)."""
-    o = ops()
-    return SimpleNamespace(paged_attention_decode_int8=o.paged_attention_decode_int8,
-                           paged_attention_decode_int8_xfrag=o.paged_attention_decode_int8_xfrag)
+def load_paged_attention() -> SimpleNamespace | None:
+    """Paged attention over int8 and fp32 KV caches (HIP, gfx950), or None."""
+    return _namespace("paged attention kernels", (
+        "paged_attention_decode_int8", "paged_attention_decode_int8_xfrag",
+        "paged_attention_decode", "paged_attention_rows", "attention_metadata"))
 
 
 @functools.cache
-def load_quant() -> SimpleNamespace:
-    """Load-time quantizers and the int8 KV-cache write (HIP, gfx950)."""
-    o = ops()
-    return SimpleNamespace(
-        int8_quantize=o.int8_quantize,
-        int4_quantize=o.int4_quantize,
-        kv_quantize_write=o.kv_quantize_write,
-    )
+def load_quant() -> SimpleNamespace | None:
+    """Load-time quantizers and the int8 KV-cache write (HIP, gfx950), or None."""
+    return _namespace("quantization kernels", ("int8_quantize", "int4_quantize",
+                                               "kv_quantize_write"))
 
 
 @functools.cache
-def load_fused_ops() -> SimpleNamespace:
-    """Decoder-layer elementwise ops and decode-step glue (HIP, gfx950)."""
-    o = ops()
-    return SimpleNamespace(
-        rmsnorm=o.rmsnorm,
-        add_rmsnorm_=o.add_rmsnorm_,
-        embed_rmsnorm=o.embed_rmsnorm,
-        add_rmsnorm_xfrag_=o.add_rmsnorm_xfrag_,
-        embed_rmsnorm_xfrag=o.embed_rmsnorm_xfrag,
-        silu_mul_xfrag=o.silu_mul_xfrag,
-        int4_linear_gemm_xfrag=o.int4_linear_gemm_xfrag,
-        lm_head_f32_xfrag=o.lm_head_f32_xfrag,
-        silu_mul=o.silu_mul,
-        rope_qk_=o.rope_qk_,
-        decode_qkv_kv=o.decode_qkv_kv,
-        argmax_advance=o.argmax_advance,
-    )
+def load_fused_ops() -> SimpleNamespace | None:
+    """Decoder-layer elementwise ops and decode-step glue (HIP, gfx950), or None."""
+    return _namespace("fused ops", (
+        "rmsnorm", "add_rmsnorm_", "embed_rmsnorm", "add_rmsnorm_xfrag_", "embed_rmsnorm_xfrag",
+        "silu_mul_xfrag", "int4_linear_gemm_xfrag", "lm_head_f32_xfrag", "silu_mul", "rope_qk_",
+        "decode_qkv_kv", "argmax_advance"))

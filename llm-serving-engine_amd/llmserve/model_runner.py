@@ -1,24 +1,130 @@
-"""Device-resident greedy decode steps, optionally replayed from a HIP graph.
+"""Model execution for a scheduled batch, and device-resident greedy decode steps.
 
-The reference's ``ModelRunner.execute`` (src/llmserve/model_runner.py:40-87) rebuilds the
-attention metadata on the host for every step, runs the model, copies the logits to the host
-and samples there (sampling.py:169-170). For a batch of sequences that are all decoding, every
-piece of that state can live on the GPU: the block tables (sized up front for the longest
-context the run will reach), the context lengths (advanced on the device by the greedy kernel)
-and the last token of each sequence. ``DecodeRunner.step`` is then one fixed sequence of
-kernels with no host round trip, so it is captured once into a HIP graph and replayed
-(``torch.cuda.CUDAGraph``); each replay decodes one token per sequence.
+``ModelRunner`` keeps the reference's interface (src/llmserve/model_runner.py:14-87): it turns
+one scheduler step (``sched.scheduled``: per sequence its token ids, computed-token count, new
+token count and block table; ``sched.block_copies``) into one forward pass and returns the
+requested logits rows on the host. A step whose sequences all decode one token over an int8
+cache runs the fused decode step (``QuantCausalLM.forward_decode``: the KV write fused into the
+post-qkv kernel, attention merges writing the next linear's input); any other batch (prompt
+chunks, mixed batches, fp32 caches) runs the ragged forward with device-built attention
+metadata and one paged-attention launch per layer over all tokens.
 
-Graph capture records no memset nodes: every buffer the step writes is written by a kernel.
+``DecodeRunner`` goes further for a fixed batch that only decodes: the block tables (sized up
+front for the longest context the run will reach), the context lengths (advanced on the device
+by the greedy kernel) and the last token of each sequence live on the GPU, so a step is one
+fixed sequence of kernels with no host round trip, captured once into a HIP graph and replayed
+(``torch.cuda.CUDAGraph``); each replay decodes one token per sequence. Graph capture records
+no memset nodes: every buffer the step writes is written by a kernel.
 """
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
+from llmserve.attention import AttentionMetadata, QuantizedKV, _model_placement, resolve_backend
 from llmserve.kernels import load_fused_ops
 from llmserve.kv_cache import KVCache
 from llmserve.transformer import QuantCausalLM
+
+
+class ModelRunner:
+    """One forward pass per scheduled batch (reference model_runner.py:14-87)."""
+
+    # decode-only steps over an int8 cache take the fused decode step of QuantCausalLM
+    fused_decode = True
+
+    def __init__(self, model, kv_cache: KVCache, attention_backend: str = "auto") -> None:
+        self.model = model
+        self.cache = kv_cache
+        self.block_size = kv_cache.block_size
+        self.device, dtype = _model_placement(model)
+        if attention_backend == "auto" and dtype != torch.float32:
+            attention_backend = "torch"  # the native kernels serve fp32 models
+        self.attention_backend = resolve_backend(attention_backend, str(self.device))
+
+    def copy_blocks(self, copies: list[tuple[int, int]]) -> None:
+        """Copies whole blocks (src, dst) in every layer's K and V cache (copy-on-write)."""
+        if not copies:
+            return
+        bs = self.block_size
+        pairs = np.asarray(copies, dtype=np.int64).reshape(-1, 2)
+        offs = np.arange(bs)
+        src = torch.from_numpy((pairs[:, :1] * bs + offs).reshape(-1))
+        dst = torch.from_numpy((pairs[:, 1:] * bs + offs).reshape(-1))
+        for pair in self.cache.layers:
+            for c in pair:
+                if isinstance(c, QuantizedKV):
+                    c.copy_rows(dst, src)
+                else:
+                    c.index_copy_(0, dst.to(c.device), c.index_select(0, src.to(c.device)))
+
+    def _decode_step_ok(self, q_lens: list[int], logit_rows: list[int]) -> bool:
+        m = self.model
+        return (self.fused_decode and isinstance(m, QuantCausalLM)
+                and self.cache.kv_dtype == "int8" and self.device.type == "cuda"
+                and load_fused_ops() is not None and all(n == 1 for n in q_lens)
+                and len(logit_rows) == len(set(logit_rows)))
+
+    @torch.inference_mode()
+    def execute(
+        self,
+        sched,
+        sample_rows: list[int],
+        num_logits: dict[int, int] | None = None,
+    ) -> torch.Tensor:
+        """Runs the model on ``sched``; returns (on the host) the logits of the last new token
+        of each ``sched.scheduled[i]`` for i in ``sample_rows`` (the last ``num_logits[i]``
+        positions when given: speculative verification), in order."""
+        self.copy_blocks(getattr(sched, "block_copies", None) or [])
+        ids: list[int] = []
+        pos: list[int] = []
+        q_lens, ctx_lens, tables, last = [], [], [], []
+        for item in sched.scheduled:
+            seq, n = item.seq, item.num_new_tokens
+            start = seq.num_computed_tokens
+            toks = list(seq.token_ids()) + list(getattr(seq, "spec_tokens", None) or [])
+            ids += toks[start: start + n]
+            pos += range(start, start + n)
+            q_lens.append(n)
+            ctx_lens.append(start + n)
+            tables.append(seq.block_table)
+            last.append(len(ids) - 1)
+        rows: list[int] = []
+        for i in sample_rows:
+            k = (num_logits or {}).get(i, 1)
+            rows += range(last[i] - k + 1, last[i] + 1)
+        m = self.model
+        if not rows:
+            return torch.empty(0, m.cfg.vocab_size)
+        if self._decode_step_ok(q_lens, rows):
+            return self._decode(ids, ctx_lens, tables, rows)
+        meta = AttentionMetadata.build(q_lens, ctx_lens, tables, self.block_size, self.device,
+                                       self.attention_backend)
+        hidden = m(torch.tensor(ids, dtype=torch.long, device=self.device),
+                   torch.tensor(pos, dtype=torch.long, device=self.device), self.cache.layers, meta)
+        sel = torch.tensor(rows, dtype=torch.long, device=self.device)
+        return m.compute_logits(hidden.index_select(0, sel)).float().cpu()
+
+    def _decode(self, ids, ctx_lens, tables, rows) -> torch.Tensor:
+        """The fused decode step for a batch of one new token per sequence."""
+        bs = self.block_size
+        need = [-(-c // bs) for c in ctx_lens]
+        for t, n in zip(tables, need):
+            if len(t) < n:
+                raise ValueError(f"block table has {len(t)} blocks, needs {n}")
+        width = max(need)
+        bt = np.zeros((len(tables), width), dtype=np.int64)
+        for i, (t, n) in enumerate(zip(tables, need)):
+            bt[i, :n] = t[:n]
+        dev = self.device
+        m = self.model
+        B = len(ids)
+        h = m.forward_decode(torch.tensor(ids, dtype=torch.long, device=dev),
+                             torch.tensor(ctx_lens, dtype=torch.long, device=dev),
+                             torch.from_numpy(bt).to(dev), self.cache.layers, bs)
+        logits = m.compute_logits(h, B if m._lm_frag(B) else None)
+        return logits.index_select(0, torch.tensor(rows, device=dev)).float().cpu()
 
 
 class DecodeRunner:
@@ -43,9 +149,28 @@ class DecodeRunner:
         self.ids = ids.to(device=dev, dtype=torch.long).contiguous().clone()
         self.context_lens = context_lens.to(device=dev, dtype=torch.long).contiguous().clone()
         self.block_tables = block_tables.to(device=dev, dtype=torch.long).contiguous().clone()
-        self.max_context = self.block_tables.shape[1] * self.block_size
+        # The longest context a step may reach: past the block table or the RoPE table the
+        # decode kernels would skip the token (its K/V unwritten, its q undefined).
+        self.max_context = min(self.block_tables.shape[1] * self.block_size,
+                               int(model.rope_cos.shape[0]))
+        # Host copy of the longest current context (the device advances every row by one per
+        # step), so that a step that would pass max_context raises before it runs.
+        self._longest = int(self.context_lens.max()) if B else 0
+        if self._longest > self.max_context:
+            raise ValueError(f"a context of {self._longest} tokens exceeds the {self.max_context} "
+                             "the block tables / RoPE table hold")
         self.logits: torch.Tensor | None = None
         self.graph: torch.cuda.CUDAGraph | None = None
+
+    def steps_left(self) -> int:
+        """Decode steps that still fit the block tables and the RoPE table."""
+        return self.max_context - self._longest + 1
+
+    def _advance(self) -> None:
+        if self.steps_left() <= 0:
+            raise RuntimeError(f"decode step past the longest supported context "
+                               f"({self.max_context} tokens): widen the block tables")
+        self._longest += 1
 
     def forward_logits(self) -> torch.Tensor:
         """Logits [B, V] of the current tokens; writes their K/V but does not advance."""
@@ -62,6 +187,7 @@ class DecodeRunner:
 
     def step(self) -> torch.Tensor:
         """Decode one token per sequence eagerly; returns the ids buffer (the new tokens)."""
+        self._advance()
         self._step()
         return self.ids
 
@@ -71,6 +197,7 @@ class DecodeRunner:
         with ``keep_state`` the ids, context lengths and caches are restored after it, else
         that step counts as a decoded token."""
         saved = self.snapshot() if keep_state else None
+        self._advance()
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -93,6 +220,7 @@ class DecodeRunner:
         ids, ctx, layers = saved
         self.ids.copy_(ids)
         self.context_lens.copy_(ctx)
+        self._longest = int(ctx.max()) if ctx.numel() else 0
         for (k, v), (kd, ks, vd, vs) in zip(self.cache.layers, layers, strict=True):
             k.data.copy_(kd)
             k.scale.copy_(ks)
@@ -103,5 +231,6 @@ class DecodeRunner:
         """One graph replay = one decode step; returns the ids buffer."""
         if self.graph is None:
             raise RuntimeError("capture() first")
+        self._advance()
         self.graph.replay()
         return self.ids

@@ -27,8 +27,17 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
+from llmserve.attention import paged_attention
 from llmserve.kernels import load_fused_ops, load_paged_attention
 from llmserve.quant import Int4Linear, _search_awq_scale
+
+
+def _fused_ops():
+    fo = load_fused_ops()
+    if fo is None:
+        raise RuntimeError("QuantCausalLM runs the fused HIP kernels of this package: build the "
+                           "native library (llm-serving-engine_amd/build.py)")
+    return fo
 
 
 @dataclass
@@ -160,6 +169,37 @@ class QuantCausalLM(nn.Module):
         return (self.fuse_xfrag and self.cfg.head_dim in (128, 256)
                 and all(m.packed_path(rows) for m in lins))
 
+    def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, kv_caches,
+                meta) -> torch.Tensor:
+        """Final hidden states [T, H] of a ragged batch (prefill chunks and decode tokens laid
+        end to end): the reference's calling convention and fused order (CausalLM.forward ->
+        _forward_fused, models/transformer.py:128-190). ``positions`` [T] index the RoPE
+        tables; ``kv_caches`` is ``KVCache.layers`` (int8 or fp32); ``meta`` the step's
+        ``AttentionMetadata``. ``paged_attention`` writes this step's K/V and attends."""
+        cfg = self.cfg
+        fo = _fused_ops()
+        nq, nk, D, eps = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rms_norm_eps
+        ids = input_ids.reshape(-1).to(device=self.embed.device, dtype=torch.long).contiguous()
+        pos = positions.reshape(-1).to(device=self.embed.device, dtype=torch.long)
+        T = ids.numel()
+        cos = self.rope_cos.index_select(0, pos).contiguous()
+        sin = self.rope_sin.index_select(0, pos).contiguous()
+        x, h = fo.embed_rmsnorm(ids, self.embed, self.layers[0].input_layernorm, eps)
+        n = len(self.layers)
+        for i, (L, (kc, vc)) in enumerate(zip(self.layers, kv_caches, strict=True)):
+            qkv = L.qkv_proj(h).contiguous()
+            fo.rope_qk_(qkv, cos, sin, nq, nk, D, L.q_norm, L.k_norm, eps)
+            q = qkv[:, : nq * D].view(T, nq, D)
+            k = qkv[:, nq * D: (nq + nk) * D].view(T, nk, D)
+            v = qkv[:, (nq + nk) * D:].view(T, nk, D)
+            o = paged_attention(q, k, v, kc, vc, meta, self.scale)
+            attn = L.o_proj(o.reshape(T, nq * D)).contiguous()
+            h = fo.add_rmsnorm_(x, attn, L.post_attention_layernorm, eps)
+            down = L.down_proj(fo.silu_mul(L.gate_up_proj(h).contiguous())).contiguous()
+            nxt = self.layers[i + 1].input_layernorm if i + 1 < n else self.norm
+            h = fo.add_rmsnorm_(x, down, nxt, eps)
+        return h
+
     def forward_decode(self, ids: torch.Tensor, context_lens: torch.Tensor,
                        block_tables: torch.Tensor, kv_layers, block_size: int) -> torch.Tensor:
         """Final hidden states [B, H] of one decode token per sequence (or, when the int4 LM
@@ -170,7 +210,7 @@ class QuantCausalLM(nn.Module):
         position up to ctx - 1; ``kv_layers`` is ``KVCache.layers`` with int8 ``QuantizedKV``
         pairs. Writes this token's K and V into the caches. No host synchronization."""
         cfg = self.cfg
-        fo, pa = load_fused_ops(), load_paged_attention()
+        fo, pa = _fused_ops(), load_paged_attention()
         nq, nk, D, eps = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rms_norm_eps
         B, H, I = ids.shape[0], cfg.hidden_size, cfg.intermediate_size
         n = len(self.layers)

@@ -85,3 +85,28 @@ def paged_decode_f64(q, k_deq, v_deq, block_tables, context_lens, block_size, sc
 def kv_dequantize(data: np.ndarray, scale: np.ndarray) -> np.ndarray:
     """QuantizedKV.rows (reference attention.py:164-166): data * scale[..., None] in float32."""
     return (data.astype(np.float32) * scale[..., None]).astype(np.float32)
+
+
+def paged_rows_f64(q, k_deq, v_deq, block_tables, row_table, row_context, block_size, scale):
+    """Query row r attends, with paged_decode_f64, to the first row_context[r] tokens of
+    block-table row row_table[r] (a prefill token at position p has row_context p + 1: the
+    causal mask of the reference's prefill SDPA, attention.py:114-124)."""
+    tables = np.asarray(block_tables)[np.asarray(row_table, np.int64)]
+    return paged_decode_f64(q, k_deq, v_deq, tables, row_context, block_size, scale)
+
+
+def step_rows(q_lens, ctx_lens, block_tables, block_size):
+    """(slot_mapping, row_table, row_context) of a ragged batch, built the way the reference's
+    AttentionMetadata.build walks it (attention.py:68-84): per sequence the context slots
+    blocks[:, None] * bs + arange(bs), flattened and cut at ctx, of which the last q_len are
+    the new tokens' slots. Plain Python loops (small inputs)."""
+    slots_out, rows, ctx_out = [], [], []
+    for s, (q_len, ctx, table) in enumerate(zip(q_lens, ctx_lens, block_tables)):
+        n = -(-ctx // block_size)
+        ctx_slots = [b * block_size + o for b in table[:n] for o in range(block_size)][:ctx]
+        for j in range(q_len):
+            p = ctx - q_len + j
+            slots_out.append(ctx_slots[p])
+            rows.append(s)
+            ctx_out.append(p + 1)
+    return (np.array(slots_out, np.int64), np.array(rows, np.int64), np.array(ctx_out, np.int64))

@@ -147,6 +147,57 @@ def paged_decode_int8_xfrag(q, kc, vc, ks, vs, bt, cl, block_size, scale, partit
     return out, xf[:nx]
 
 
+def paged_decode_f32(q, kc, vc, bt, cl, block_size, scale, partition_size=0):
+    """The fp32-cache decode (llmserve_paged_attention_decode)."""
+    B, Hq, D = q.shape
+    num_slots, Hk = kc.shape[0], kc.shape[1]
+    max_blocks = bt.shape[1]
+    out = torch.empty_like(q)
+    L = capi()
+    nbytes = L.llmserve_paged_attention_workspace_bytes(B, Hq, Hk, D, max_blocks, block_size,
+                                                        partition_size)
+    ws = torch.empty(max(nbytes, 4) // 4 + 4, dtype=torch.float32, device=q.device)
+    check(L.llmserve_paged_attention_decode(
+        _p(q), _p(kc), _p(vc), _p(bt), _p(cl), _p(out), B, Hq, Hk, D, num_slots, max_blocks,
+        block_size, float(scale), partition_size, _p(ws), nbytes, _stream()))
+    return out
+
+
+def paged_rows(q, kc, vc, ks, vs, bt, row_table, row_context, block_size, scale, q_mult=None):
+    """Attention of query rows over block-table rows (llmserve_paged_attention_rows_int8 when
+    ks / vs are given, else _f32)."""
+    R, Hq, D = q.shape
+    num_slots, Hk = kc.shape[0], kc.shape[1]
+    max_blocks = bt.shape[1]
+    out = torch.empty_like(q)
+    L = capi()
+    nbytes = L.llmserve_paged_attention_workspace_bytes(R, Hq, Hk, D, max_blocks, block_size, 0)
+    ws = torch.empty(max(nbytes, 4) // 4 + 4, dtype=torch.float32, device=q.device)
+    if ks is not None:
+        check(L.llmserve_paged_attention_rows_int8(
+            _p(q), _p(kc), _p(vc), _p(ks), _p(vs), _p(bt), bt.shape[0], _p(row_table),
+            _p(row_context), _p(out), R, Hq, Hk, D, num_slots, max_blocks, block_size,
+            float(scale), _p(q_mult), _p(ws), nbytes, _stream()))
+    else:
+        check(L.llmserve_paged_attention_rows_f32(
+            _p(q), _p(kc), _p(vc), _p(bt), bt.shape[0], _p(row_table), _p(row_context), _p(out),
+            R, Hq, Hk, D, num_slots, max_blocks, block_size, float(scale), _p(q_mult), _p(ws),
+            nbytes, _stream()))
+    return out
+
+
+def attention_metadata(seq_info, tables, block_size, T):
+    """(slot_mapping, row_table, row_context) of a step (llmserve_attention_metadata)."""
+    S, width = tables.shape
+    dev = tables.device
+    slots = torch.empty(T, dtype=torch.long, device=dev)
+    rows = torch.empty(T, dtype=torch.long, device=dev)
+    ctx = torch.empty(T, dtype=torch.long, device=dev)
+    check(capi().llmserve_attention_metadata(_p(seq_info), _p(tables), S, width, block_size, T,
+                                             _p(slots), _p(rows), _p(ctx), _stream()))
+    return slots, rows, ctx
+
+
 def split_fragments(x, inv=None):
     """The activation fragments of x * inv that llmserve_int4_linear_gemm_packed's split pass
     leaves at the start of its workspace (run against a small packed weight)."""

@@ -1,6 +1,6 @@
 """Writes the committed golden fixtures of this directory (run in the build container).
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [quant | kernels | fused | attention_f32 ...]
 
 quant_golden.npz — quantizer outputs computed with torch's CPU elementwise ops, the
 arithmetic library the reference's quantizers run on (torch.round, IEEE division, amax/amin,
@@ -20,6 +20,10 @@ fused_golden.npz — outputs of the reference's compiled fused decoder-layer ops
 add_rmsnorm_, silu_mul, rope_qk_ from fused_ops.cpp) on small seeded inputs: odd and Qwen3
 hidden sizes, q/k norms on and off, head dims 64 and 128, RoPE tables at arbitrary positions.
 Skipped when oracle/_ref is not built.
+
+attention_f32_golden.npz — outputs of the reference's compiled fp32-cache decode
+(paged_attention_decode) on small seeded inputs (ragged contexts, GQA 1/2/4, forced
+partition sizes). Skipped when oracle/_ref is not built.
 """
 
 from __future__ import annotations
@@ -268,21 +272,66 @@ def fused_golden() -> dict[str, np.ndarray] | None:
     return out
 
 
-def main() -> None:
+def attention_f32_golden() -> dict[str, np.ndarray] | None:
+    """The reference's fp32-cache decode (paged_attention_decode, paged_attention.cpp:350-359)
+    on small seeded inputs: ragged contexts, GQA 1 / 2 / 4, head dims 32 / 64 / 128, forced
+    partition sizes."""
+    from oracle import cpu as ocpu
+
+    if not ocpu.ref_available():
+        return None
+    pa = ocpu.ref_module("llmserve_paged_attention")
+    g = torch.Generator().manual_seed(4321)
+    out: dict[str, np.ndarray] = {}
+    cases = [
+        ("f32_small", 8, 2, 32, 4, [1, 7, 33, 120, 4], 128, [0, 8, 10000]),
+        ("f32_d128", 4, 2, 128, 16, [17, 100, 200, 5], 24, [0, 32]),
+        ("f32_g1", 4, 4, 64, 8, [9, 23, 64], 32, [0, 16]),
+    ]
+    for name, hq, hk, d, bs, ctx, nblocks, parts in cases:
+        kc = torch.randn(nblocks * bs, hk, d, generator=g)
+        kc[..., 3] *= 8.0
+        vc = torch.randn(nblocks * bs, hk, d, generator=g)
+        perm = torch.randperm(nblocks, generator=g).tolist()
+        tables, used = [], 0
+        for c in ctx:
+            n = -(-c // bs)
+            tables.append(perm[used: used + n])
+            used += n
+        width = max(len(t) for t in tables)
+        bt = torch.tensor([t + [0] * (width - len(t)) for t in tables], dtype=torch.long)
+        cl = torch.tensor(ctx, dtype=torch.long)
+        q = torch.randn(len(ctx), hq, d, generator=g)
+        sc = d ** -0.5
+        out.update({f"{name}_q": q.numpy(), f"{name}_k": kc.numpy(), f"{name}_v": vc.numpy(),
+                    f"{name}_bt": bt.numpy(), f"{name}_cl": cl.numpy(),
+                    f"{name}_meta": np.array([bs, sc], np.float64)})
+        for p in parts:
+            o = pa.paged_attention_decode(q, kc, vc, bt, cl, bs, sc, p)
+            out[f"{name}_out_p{p}"] = o.numpy()
+    return out
+
+
+WRITERS = {
+    "quant": ("quant_golden.npz", quant_golden),
+    "kernels": ("kernels_golden.npz", kernels_golden),
+    "fused": ("fused_golden.npz", fused_golden),
+    "attention_f32": ("attention_f32_golden.npz", attention_f32_golden),
+}
+
+
+def main(which: list[str]) -> None:
+    """Writes the fixtures named in ``which`` (all of them when empty)."""
     torch.set_num_threads(4)
-    np.savez_compressed(HERE / "quant_golden.npz", **quant_golden())
-    print("wrote", HERE / "quant_golden.npz")
-    k = kernels_golden()
-    if k is None:
-        print("oracle/_ref not built: kernels_golden.npz left unchanged")
-    else:
-        np.savez_compressed(HERE / "kernels_golden.npz", **k)
-        print("wrote", HERE / "kernels_golden.npz")
-    f = fused_golden()
-    if f is not None:
-        np.savez_compressed(HERE / "fused_golden.npz", **f)
-        print("wrote", HERE / "fused_golden.npz")
+    for key in which or list(WRITERS):
+        fname, fn = WRITERS[key]
+        data = fn()
+        if data is None:
+            print(f"oracle/_ref not built: {fname} left unchanged")
+            continue
+        np.savez_compressed(HERE / fname, **data)
+        print("wrote", HERE / fname)
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:])

@@ -132,7 +132,7 @@ def test_pack_layout(gpu, N, K, g):
     assert np.array_equal(pz[:N], (gz - F32(8) * gs).astype(F32)) and not pz[N:].any()
 
 
-@pytest.mark.parametrize("M", [17, 32, 64])
+@pytest.mark.parametrize("M", [5, 16, 17, 32, 64])
 @pytest.mark.parametrize("N,K", QWEN)
 def test_packed_gemm_qwen_shapes(gpu, M, N, K):
     x, nib, gs, gz, inv = _case(M, N, K, 128, M * 37 + N + K)

@@ -122,3 +122,21 @@ def test_live_against_reference_build():
         theirs = pa.paged_attention_decode_int8(*map(torch.from_numpy, (qq, kq, vq, ks, vs, bt, cl)),
                                                 bs, 0.125, p).numpy()
         close(mine, theirs, 2e-6, 2e-6)
+
+
+def test_fp32_decode_golden_matches_f64():
+    """The reference's compiled fp32-cache decode (committed outputs) agrees with the float64
+    attention at every forced partition size: pins the fixture the GPU kernel is held to."""
+    from conftest import GOLDEN
+    from oracle import math_ref as mr
+
+    g = dict(np.load(GOLDEN / "attention_f32_golden.npz"))
+    for name in ("f32_small", "f32_d128", "f32_g1"):
+        bs, sc = g[f"{name}_meta"]
+        ref = mr.paged_decode_f64(g[f"{name}_q"], g[f"{name}_k"], g[f"{name}_v"], g[f"{name}_bt"],
+                                  g[f"{name}_cl"], int(bs), float(sc))
+        outs = [k for k in g if k.startswith(f"{name}_out_p")]
+        assert outs
+        for k in outs:
+            err = np.abs(g[k] - ref).max() / np.abs(ref).max()
+            assert err < 2e-6, (k, err)

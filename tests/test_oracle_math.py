@@ -104,3 +104,47 @@ def test_prefill_reference_brute_force():
     plain = mr.int8_linear_f64(x, q, s)
     np.testing.assert_allclose(mr.int8_linear_prefill_f64(x, q, s, round_x=False), plain,
                                rtol=1e-6, atol=1e-12)
+
+
+def test_rows_oracle_is_causal_sdpa():
+    """A prefill chunk's rows (contexts p + 1 over one block-table row) equal float64 SDPA with
+    the reference's mask k_pos <= q_pos (attention.py:114-124), a chunk with no cached prefix
+    equals is_causal, and a decode row equals paged_decode_f64."""
+    rng = np.random.default_rng(21)
+    Hq, Hk, D, bs, nblk = 4, 2, 16, 4, 12
+    k = rng.standard_normal((nblk * bs, Hk, D))
+    v = rng.standard_normal((nblk * bs, Hk, D))
+    table = rng.permutation(nblk)
+    for cached, q_len in ((0, 9), (11, 6)):
+        ctx = cached + q_len
+        q = rng.standard_normal((q_len, Hq, D))
+        got = mr.paged_rows_f64(q, k, v, table[None, :], np.zeros(q_len, np.int64),
+                                np.arange(cached + 1, ctx + 1), bs, D ** -0.5)
+        slots = mr.context_slots(table, ctx, bs)
+        kt = torch.from_numpy(k[slots]).transpose(0, 1)[None]  # [1, Hk, ctx, D]
+        vt = torch.from_numpy(v[slots]).transpose(0, 1)[None]
+        qt = torch.from_numpy(q).transpose(0, 1)[None]
+        mask = torch.arange(ctx)[None, :] <= torch.arange(cached, ctx)[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            qt, kt.repeat_interleave(2, 1), vt.repeat_interleave(2, 1), attn_mask=mask,
+            scale=D ** -0.5)[0].transpose(0, 1).numpy()
+        np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+        if cached == 0:
+            ref_c = torch.nn.functional.scaled_dot_product_attention(
+                qt, kt.repeat_interleave(2, 1), vt.repeat_interleave(2, 1), is_causal=True,
+                scale=D ** -0.5)[0].transpose(0, 1).numpy()
+            np.testing.assert_allclose(got, ref_c, rtol=1e-12, atol=1e-12)
+    q1 = rng.standard_normal((1, Hq, D))
+    np.testing.assert_allclose(
+        mr.paged_rows_f64(q1, k, v, table[None, :], [0], [17], bs, 0.3),
+        mr.paged_decode_f64(q1, k, v, table[None, :], [17], bs, 0.3), rtol=0, atol=0)
+
+
+def test_step_rows_oracle():
+    """The step-row oracle on a hand-checked batch: block size 4, a decode token at position
+    9 of table [5, 2, 7], a 3-token chunk after 2 cached tokens of table [1], a fresh 2-token
+    prompt on table [3]."""
+    slots, rows, ctx = mr.step_rows([1, 3, 2], [10, 5, 2], [[5, 2, 7], [1, 6], [3]], 4)
+    np.testing.assert_array_equal(slots, [7 * 4 + 1, 4 + 2, 4 + 3, 6 * 4 + 0, 12, 13])
+    np.testing.assert_array_equal(rows, [0, 1, 1, 1, 2, 2])
+    np.testing.assert_array_equal(ctx, [10, 3, 4, 5, 1, 2])
