@@ -401,6 +401,25 @@ int llmserve_attention_metadata(const int64_t* seq_info, const int64_t* block_ta
                                 int64_t* slot_mapping, int64_t* row_table, int64_t* row_context,
                                 void* stream);
 
+/*
+ * llmserve_paged_attention_decode_int8 without a workspace argument, for callers that cannot
+ * allocate device memory (HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The split-context partials go to a scratch
+ * array of llmserve_paged_attention_noalloc_scratch_bytes() bytes (16 MiB) that the library
+ * holds on each device it runs on until the process ends; a call whose partials
+ * (llmserve_paged_attention_workspace_bytes(...)) exceed it fails with LLMSERVE_ERR_INVALID
+ * before anything runs. Calls on one device share the array: calls that overlap on a device
+ * race. Arguments and results otherwise as llmserve_paged_attention_decode_int8 (same kernels,
+ * same bits). Allocates nothing.
+ */
+int64_t llmserve_paged_attention_noalloc_scratch_bytes(void);
+int llmserve_paged_attention_decode_int8_noalloc(
+    const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
+    const float* v_scale, const int64_t* block_tables, const int64_t* context_lens, float* out,
+    int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots, int64_t max_blocks,
+    int64_t block_size, float scale, int64_t partition_size, const float* q_mult /* nullable */,
+    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

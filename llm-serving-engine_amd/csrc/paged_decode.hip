@@ -36,6 +36,7 @@
 // The scores are the reference's s = (scale * k_scale) * (q . k_int8) and the values
 // acc += (p * v_scale) * v_int8 (paged_attention.cpp:301-355), up to the order of the
 // float operations (scale folded into q; exp2 of log2-unit scores).
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1048,4 +1049,64 @@ extern "C" int llmserve_paged_attention_rows_f32(
                       RowMap{row_table, table_rows}, row_context, out, R, Hq, Hk, D, num_slots,
                       max_blocks, block_size, scale, 0, q_mult, FragOut{nullptr, nullptr},
                       workspace, workspace_bytes, stream);
+}
+
+// ---- allocation-free variant --------------------------------------------------------------
+// Callers that cannot allocate device memory (code under HIP graph capture, tight serving
+// loops) get the split-context partials from this file-scope array instead of a workspace:
+// each GPU the library runs on holds its own copy until the process ends. Calls that overlap
+// on one GPU share it and race; nothing in it needs clearing (the merge reads only partials
+// the same call's decode kernel wrote).
+constexpr int64_t kNoAllocScratchBytes = 16LL << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// The device address of `scratch` on the current device, looked up once per device (the
+// array's name in host code is only a stand-in for the symbol).
+void* noalloc_scratch() {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    lsh::set_error("paged_attention_decode_int8_noalloc: no current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      lsh::set_error("paged_attention_decode_int8_noalloc: hipGetSymbolAddress failed (%s)",
+                     hipGetErrorString(e));
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
+}  // namespace
+
+extern "C" int64_t llmserve_paged_attention_noalloc_scratch_bytes(void) {
+  return kNoAllocScratchBytes;
+}
+
+extern "C" int llmserve_paged_attention_decode_int8_noalloc(
+    const float* q, const int8_t* k_cache, const int8_t* v_cache, const float* k_scale,
+    const float* v_scale, const int64_t* block_tables, const int64_t* context_lens, float* out,
+    int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t num_slots, int64_t max_blocks,
+    int64_t block_size, float scale, int64_t partition_size, const float* q_mult, void* stream) {
+  const int64_t need = llmserve_paged_attention_workspace_bytes(B, Hq, Hk, D, max_blocks,
+                                                                block_size, partition_size);
+  LSH_CHECK(need <= kNoAllocScratchBytes,
+            "paged_attention_decode_int8_noalloc: the call needs %lld bytes of partials, more "
+            "than the library's %lld-byte scratch array (use the workspace entry point)",
+            (long long)need, (long long)kNoAllocScratchBytes);
+  if (B == 0) return LLMSERVE_OK;
+  void* ws = noalloc_scratch();
+  if (ws == nullptr) return LLMSERVE_ERR_HIP;
+  return decode_int8(q, k_cache, v_cache, k_scale, v_scale, block_tables, context_lens, out, B, Hq,
+                     Hk, D, num_slots, max_blocks, block_size, scale, partition_size, q_mult,
+                     FragOut{nullptr, nullptr}, ws, kNoAllocScratchBytes, stream);
 }

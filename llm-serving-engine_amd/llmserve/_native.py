@@ -97,6 +97,11 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
         [_P] * 4 + [_I64] + [_P] * 3 + [_I64] * 7 + [_F32, _P, _P, _I64, _P],
     ),
     "llmserve_attention_metadata": (_I32, [_P, _P] + [_I64] * 4 + [_P] * 4),
+    "llmserve_paged_attention_noalloc_scratch_bytes": (_I64, []),
+    "llmserve_paged_attention_decode_int8_noalloc": (
+        _I32,
+        [_P] * 8 + [_I64] * 7 + [_F32, _I64, _P, _P],
+    ),
 }
 
 
