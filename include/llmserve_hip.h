@@ -402,6 +402,51 @@ int llmserve_attention_metadata(const int64_t* seq_info, const int64_t* block_ta
                                 void* stream);
 
 /*
+ * The linear chain of one decoder layer for a decode batch of M <= 4 sequences, as one
+ * persistent launch (replaces, for small batches, the reference's per-op sequence of
+ * _forward_fused, models/transformer.py:157-189, with Int4Linear.forward, quant.py:134-151,
+ * and the cache write of paged_attention, attention.py:241-246):
+ *   x1 = x_in + o_proj(attn);  h = rmsnorm(x1) * post_w;  a = silu(gate(h)) * up(h)
+ *   x_out = x1 + down(a);      h2 = rmsnorm(x_out) * next_w
+ *   then, when qkv_nib is given (not the last layer): the next layer's qkv = qkv_proj(h2),
+ *   per-head RMSNorm (q_w / k_w, nullable) and rotate-half RoPE of q and k at position
+ *   p = context_lens[m] - 1 (rows p of cos_t / sin_t [max_pos, 128]), q -> q_out [M, n_q, 128],
+ *   k / k_smooth (nullable) and v int8-quantized into the caches at slot
+ *   block_tables[m, p / block_size] * block_size + p % block_size (the quantizer of
+ *   llmserve_kv_quantize_write; a position outside the tables leaves the cache and gives a NaN
+ *   q row); otherwise h_out (nullable) = h2, the final norm's output.
+ * Embedding mode (attn == NULL): x_out = embed[ids] (an id outside [0, vocab) gives a NaN
+ * row), then the qkv part for layer 0 with next_w = its input norm.
+ * int4 weights are the Int4Linear buffers (nibbles [N, K/2], g_scale / g_zero [N, K/128],
+ * inv_act_scale [K] nullable); o_proj [H, n_q*128], gate_up [2I, H], down [H, I], qkv
+ * [(n_q + 2 n_k) * 128, H]. Requires head_dim = group_size = 128, H a multiple of 128 in
+ * [256, 1024] and of 4 * (n_q + 2 n_k), n_q * 128 <= 2048, I a multiple of 256 and of H / 4
+ * with I / (H / 4) a multiple of 4 and at most 16, 16-byte aligned weights, activations and
+ * norm weights; x_out must not alias x_in. The (H / 4 [+ n_q + 2 n_k]) workgroups hand
+ * activations to each other through `workspace` (llmserve_decode_chain_workspace_bytes(H, I)
+ * bytes, 16-byte aligned, zero before its first use and then owned by the chain: launches
+ * that overlap on one workspace race) and must all be resident at once (checked). Each
+ * hand-off wait gives up after `spin_limit` polls, sets the workspace's error word
+ * (llmserve_decode_chain_error) and lets the grid finish. No counterpart in the reference.
+ */
+int64_t llmserve_decode_chain_workspace_bytes(int64_t H, int64_t I);
+int llmserve_decode_chain(
+    const float* attn, const float* x_in, const int64_t* ids, const float* embed, int64_t vocab,
+    float* x_out, float* h_out, const uint8_t* o_nib, const float* o_s, const float* o_z,
+    const float* o_inv, const float* post_w, const uint8_t* gu_nib, const float* gu_s,
+    const float* gu_z, const float* gu_inv, const uint8_t* dn_nib, const float* dn_s,
+    const float* dn_z, const float* dn_inv, const float* next_w, const uint8_t* qkv_nib,
+    const float* qkv_s, const float* qkv_z, const float* qkv_inv, const float* q_w,
+    const float* k_w, const float* cos_t, const float* sin_t, int64_t max_pos,
+    const int64_t* context_lens, const int64_t* block_tables, int64_t max_blocks,
+    int64_t block_size, const float* k_smooth, float* q_out, int8_t* k_cache, int8_t* v_cache,
+    float* k_scale, float* v_scale, int64_t num_slots, int64_t M, int64_t H, int64_t I,
+    int64_t n_q, int64_t n_k, int64_t head_dim, int64_t group_size, float eps, void* workspace,
+    int64_t workspace_bytes, int64_t spin_limit, void* stream);
+/* The chain workspace's error word (nonzero: a hand-off wait ran out of polls). Synchronizes. */
+int llmserve_decode_chain_error(const void* workspace, int* error);
+
+/*
  * llmserve_paged_attention_decode_int8 without a workspace argument, for callers that cannot
  * allocate device memory (HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). No counterpart in the reference. The split-context partials go to a scratch

@@ -1,6 +1,6 @@
 """Builds the gfx950 libraries in-tree (no JIT cache, no hipify, no torch build system).
 
-    python llm-serving-engine_amd/build.py
+    python llm-serving-engine_amd/build.py [--incremental] [-v]
 
 Outputs, next to the Python package so that they travel with the source tree:
   llmserve/_lib/libllmserve_hip.so    HIP kernels + the C ABI of include/llmserve_hip.h
@@ -57,6 +57,7 @@ HIP_SOURCES = [
     "fused_ops.hip",
     "paged_decode.hip",
     "attn_meta.hip",
+    "decode_chain.hip",
     "lm_head.hip",
 ]
 
@@ -83,16 +84,28 @@ def _torch_paths() -> tuple[list[str], list[str]]:
     return inc, [lib]
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> tuple[Path, Path]:
-    """Compile every HIP source and link both libraries. Always rebuilds."""
+def _stale(src: Path, obj: Path) -> bool:
+    """True when obj is missing or older than its source or any header it may include."""
+    if not obj.is_file():
+        return True
+    deps = [src, *CSRC.glob("*.h"), *INCLUDE.glob("*.h"), Path(__file__)]
+    return max(d.stat().st_mtime for d in deps) > obj.stat().st_mtime
+
+
+def build(verbose: bool = False, jobs: int | None = None,
+          incremental: bool = False) -> tuple[Path, Path]:
+    """Compile the HIP sources and link both libraries. Rebuilds everything unless
+    ``incremental`` (then only objects older than their sources or the headers)."""
     OBJ_DIR.mkdir(exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     jobs = jobs or min(8, os.cpu_count() or 1)
     objs = [OBJ_DIR / (Path(s).stem + ".o") for s in HIP_SOURCES]
+    todo = [(s, o) for s, o in zip(HIP_SOURCES, objs)
+            if not incremental or _stale(CSRC / s, o)]
     with cf.ThreadPoolExecutor(jobs) as ex:
         futs = [
             ex.submit(_run, [HIPCC, *HIP_FLAGS, "-c", str(CSRC / s), "-o", str(o)], verbose)
-            for s, o in zip(HIP_SOURCES, objs)
+            for s, o in todo
         ]
         for f in futs:
             f.result()
@@ -132,5 +145,5 @@ def build(verbose: bool = False, jobs: int | None = None) -> tuple[Path, Path]:
 
 
 if __name__ == "__main__":
-    for p in build(verbose="-v" in sys.argv):
+    for p in build(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv):
         print(p)

@@ -1,0 +1,765 @@
+// The linear chain of one decoder layer for a decode batch of at most 4 sequences, as ONE
+// persistent launch: the layer's o_proj, residual add + post-attention RMSNorm, gate_up and
+// silu * up, down_proj, residual add + the next layer's input RMSNorm, then the next layer's
+// qkv projection with its q/k RMSNorm, RoPE at each sequence's position and the int8 K/V
+// write (the reference's _forward_fused order, models/transformer.py:157-189, with the int4
+// linears of quant.py:134-151 and the cache write of attention.py:241-246). At one to four
+// rows each of these matrices is 1-3 MB: a kernel per op spends its time in launch and
+// dependent-latency gaps (~3 us each, eight per layer), not in HBM. Here the weights of every
+// stage are requested when the kernel starts, and the stages hand their small activation
+// vectors to each other inside the launch.
+//
+// Workgroups (512 threads = 8 wavefronts, one per CU, all resident at once):
+//   MLP groups w < H / 8:   o_proj rows 8w..8w+7 (a wavefront per row), gate rows and up rows
+//                           of channels [C w, C (w + 1)) (C = I / (H / 8)), down rows
+//                           8w..8w+7; for the last layer also those residual channels and
+//                           their final norm.
+//   head groups (after):    one q, k or v head of the next layer's qkv projection each (128
+//                           rows, 16 per wavefront), a 1 / (n_q + 2 n_k) share of the new
+//                           residual channels, the head's norm / RoPE / cache write.
+// Hand-offs: a producer stores each output value as one 8-byte word (float bits | launch tag
+// << 32) with a device-scope store; a consumer polls the words it needs with device-scope
+// loads until every one carries this launch's tag, so data and readiness travel together and
+// no counter or fence is needed. Three hand-offs per layer: o_proj out (ex1, H words per row),
+// silu * up (ex2, I words), down_proj out (ex3, H words). Every wait is bounded by
+// `spin_limit` polls; a wait that runs out sets the error word and the workgroup returns, so
+// the grid always drains. The launch tag is ctl[0] + 1 (never 0, the value of cleared words);
+// the last workgroup to finish (ctl[1] counts them) resets the count and advances ctl[0], so
+// the next launch on the stream uses a new tag. The caller's workspace holds ctl and the three
+// exchange buffers; launches that overlap on one workspace race.
+//
+// Layouts: int4 weights are the reference buffers (nibbles [N, K/2], even channel low;
+// group scale / zero [N, K/128]); x' = x * inv_act_scale is staged in LDS with each
+// 32-channel slice's eight 16-byte chunks rotated by the slice index (conflict-free
+// ds_read_b128); a lane holds 16-byte weight chunks (32 channels of one group) and computes
+// s * sum x'q + (z - 8 s) * sum x' (int8_gemv.cpp:48-52), partial sums reduced with DPP.
+#include "common.h"
+#include "kv_quant.h"
+#include "rope.h"
+
+namespace {
+
+using lsh::kWave;
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;  // 8
+constexpr int kMaxRows = 4;   // sequences per launch
+constexpr int kHeadDim = 128;
+constexpr int kGroup = 128;   // quantization group (channels)
+constexpr int kMaxH = 1024;   // hidden size: two channels per thread; gate_up / qkv rows are one
+                              // 32-chunk half wavefront
+constexpr int kMaxKq = 2048;  // o_proj input: one 64-chunk wavefront
+constexpr int kMaxI = 4096;   // down_proj input: at most two chunks per lane
+constexpr int kMaxGuPass = 4; // gate_up rows per workgroup <= 16 * kMaxGuPass
+constexpr int kHeadPasses = kHeadDim / (2 * kWaves);  // 8: two qkv rows per wavefront per pass
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct ChainArgs {
+  // residual stream, attention output, outputs
+  const float* attn;   // [M, Kq] this layer's attention output (MLP part)
+  const float* x_in;   // [M, H] residual stream before this layer's o_proj (MLP part)
+  const int64_t* ids;  // [M] token ids: embedding mode (no MLP part)
+  const float* embed;  // [V, H]
+  int64_t vocab;
+  float* x_out;        // [M, H] residual after the down_proj add (or the embedding rows)
+  float* h_out;        // [M, H] the final norm's output (last layer) or null
+  // this layer: o_proj, post-attention norm, gate_up, down_proj; then the next norm
+  const uint8_t* o_nib;
+  const float *o_s, *o_z, *o_inv;
+  const float* post_w;
+  const uint8_t* gu_nib;
+  const float *gu_s, *gu_z, *gu_inv;
+  const uint8_t* dn_nib;
+  const float *dn_s, *dn_z, *dn_inv;
+  const float* next_w;
+  // the next layer's qkv projection, q/k norm, RoPE and cache write
+  const uint8_t* qkv_nib;
+  const float *qkv_s, *qkv_z, *qkv_inv;
+  const float *q_w, *k_w;
+  const float *cos_t, *sin_t;
+  int64_t max_pos;
+  const int64_t* ctx;  // [M] context length including the token (position ctx - 1)
+  const int64_t* bt;   // [M, max_blocks]
+  int64_t max_blocks, bs, num_slots;
+  const float* smooth;  // [nk, D] or null
+  float* q_out;         // [M, nq, D]
+  int8_t *kc, *vc;
+  float *ks, *vs;
+  // hand-offs and control words
+  uint64_t *ex1, *ex2, *ex3;  // [kMaxRows][H], [kMaxRows][I], [kMaxRows][H]
+  uint32_t* ctl;              // tag base, finished workgroups, error
+  uint32_t spin_limit;
+  int M, H, Kq, I, nq, nk;
+  int mlp_groups;   // H / 8, or 0 (embedding mode)
+  int head_groups;  // nq + 2 nk, or 0 (last layer)
+  float eps;
+};
+
+// ---- hand-off words --------------------------------------------------------------------------
+
+__device__ __forceinline__ void put(uint64_t* p, float v, uint32_t tag) {
+  const uint64_t w = (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, v);
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t peek(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls the words addr(i) for the i set in `need` (N <= 32) until each carries `tag`, handing
+// each value to sink(i, value) as it arrives. Every round issues the loads of all missing
+// words together. Returns false when the poll budget runs out (the error word is then set).
+template <int N, typename Addr, typename Sink>
+__device__ bool take(uint32_t need, uint32_t tag, const ChainArgs& a, Addr addr, Sink sink) {
+  static_assert(N <= 32, "take: at most 32 words per thread");
+  uint32_t ready = 0;
+  for (uint32_t spin = 0;; ++spin) {
+    uint64_t w[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if ((need & ~ready) >> i & 1u) w[i] = peek(addr(i));
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (((need & ~ready) >> i & 1u) && static_cast<uint32_t>(w[i] >> 32) == tag) {
+        sink(i, __builtin_bit_cast(float, static_cast<uint32_t>(w[i])));
+        ready |= 1u << i;
+      }
+    if (ready == need) return true;
+    if (spin >= a.spin_limit) {
+      __hip_atomic_fetch_or(a.ctl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// ---- staging and dot products ------------------------------------------------------------------
+
+// LDS offset of channel k of a staged row: 32-channel slice sl = k / 32 keeps its eight
+// 16-byte chunks rotated by sl, so the 16 lanes of a ds_read_b128 phase, reading chunk j of
+// consecutive slices, hit 16 distinct bank groups.
+__device__ __forceinline__ int xoff(int k) {
+  const int sl = k >> 5, j = (k >> 2) & 7;
+  return (sl << 5) + (((j + sl) & 7) << 2) + (k & 3);
+}
+
+__device__ __forceinline__ float4 lds4(const float* p) {
+  return *static_cast<const float4*>(__builtin_assume_aligned(p, 16));
+}
+
+__device__ __forceinline__ float4 mul4(float4 v, float4 t) {
+  return make_float4(__fmul_rn(v.x, t.x), __fmul_rn(v.y, t.y), __fmul_rn(v.z, t.z),
+                     __fmul_rn(v.w, t.w));
+}
+
+// A lane's 16-byte weight chunk (32 channels of one group) with the group scale s and z - 8 s;
+// `on` false: no chunk (the loads are clamped in bounds, the terms zeroed).
+struct Chunk {
+  u32x4 w;
+  float s, zc;
+  bool on;
+};
+
+__device__ __forceinline__ Chunk fetch(const uint8_t* nib, const float* gs, const float* gz,
+                                       int K, int64_t row, int c, bool on) {
+  const int G = K / kGroup;
+  const int cc = on ? c : 0;
+  Chunk f;
+  f.w = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>(nib + row * (K / 2) + static_cast<int64_t>(cc) * 16));
+  const float s = gs[row * G + cc / 4], z = gz[row * G + cc / 4];
+  f.s = s;
+  f.zc = z - 8.f * s;
+  f.on = on;
+  return f;
+}
+
+// The lane's terms s * sum x'q + (z - 8 s) * sum x' of chunk c (channels 32c..32c+31) of
+// the staged rows m < MT of K channels.
+template <int MT>
+__device__ __forceinline__ void chunk_terms(const Chunk& f, int c, const float* xs, int K,
+                                            float (&v)[MT]) {
+  float q[32];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u = f.w[i];
+    const uint32_t lo = u & 0x0f0f0f0fu, hi = (u >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      q[8 * i + 2 * b] = static_cast<float>((lo >> (8 * b)) & 0xffu);
+      q[8 * i + 2 * b + 1] = static_cast<float>((hi >> (8 * b)) & 0xffu);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const float* row = xs + m * K + (c << 5);
+    float d = 0.f, sx = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 x = lds4(row + (((j + c) & 7) << 2));
+      d += x.x * q[4 * j] + x.y * q[4 * j + 1] + x.z * q[4 * j + 2] + x.w * q[4 * j + 3];
+      sx += (x.x + x.y) + (x.z + x.w);
+    }
+    v[m] = f.on ? f.s * d + f.zc * sx : 0.f;
+  }
+}
+
+// Rows [0, MT) of a [M, K] source (K <= kMaxKq; rows >= M repeat row M - 1 and are never
+// summed) times inv (nullable; the reference's separate float32 multiply), as float4 chunks in
+// registers: loaded before any later stage's weights, so that the LDS stores wait for these
+// loads only.
+template <int MT>
+struct Staged {
+  static constexpr int kN = MT * kMaxKq / 4 / kThreads;
+  float4 v[kN];
+};
+
+template <int MT>
+__device__ __forceinline__ void stage_load(Staged<MT>& st, const float* src, const float* inv,
+                                           int K, int M) {
+  const int n4 = MT * K / 4;
+#pragma unroll
+  for (int u = 0; u < Staged<MT>::kN; ++u) {
+    const int q = min(static_cast<int>(threadIdx.x) + u * kThreads, n4 - 1);
+    const int m = (q * 4) / K, k = (q * 4) % K;
+    st.v[u] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(min(m, M - 1)) * K + k);
+    if (inv) st.v[u] = mul4(st.v[u], *reinterpret_cast<const float4*>(inv + k));
+  }
+}
+
+template <int MT>
+__device__ __forceinline__ void stage_store(const Staged<MT>& st, float* xs, int K) {
+  const int n4 = MT * K / 4;
+#pragma unroll
+  for (int u = 0; u < Staged<MT>::kN; ++u) {
+    const int q = static_cast<int>(threadIdx.x) + u * kThreads;
+    if (q < n4) {
+      const int m = (q * 4) / K, k = (q * 4) % K;
+      *reinterpret_cast<float4*>(xs + m * K + xoff(k)) = st.v[u];
+    }
+  }
+}
+
+// Block sum of one value per thread in a fixed order; every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = lsh::wave_sum_from<1>(v);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+}
+
+// Residual rows: thread t holds channels 2t and 2t + 1 of rows m < MT.
+template <int MT>
+struct Resid {
+  float v[MT][2];
+};
+
+template <int MT>
+__device__ __forceinline__ void row_inv_rms(const Resid<MT>& r, int H, int M, float eps,
+                                            float* red, float (&inv)[MT]) {
+  const bool own = 2 * static_cast<int>(threadIdx.x) < H;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const float ss = own && m < M ? r.v[m][0] * r.v[m][0] + r.v[m][1] * r.v[m][1] : 0.f;
+    const float tot = block_sum(ss, red);
+    inv[m] = 1.f / sqrtf(tot / static_cast<float>(H) + eps);
+  }
+}
+
+// The RMSNorm w * (r * inv) of the residual rows times act_inv (nullable) -> LDS (xoff).
+template <int MT>
+__device__ __forceinline__ void norm_to_lds(const Resid<MT>& r, const float* w,
+                                            const float* act_inv, float eps, int H, int M,
+                                            float* xs, float* red) {
+  float inv[MT];
+  row_inv_rms(r, H, M, eps, red, inv);
+  const int k0 = 2 * threadIdx.x;
+  if (k0 >= H) return;
+  const float2 wv = *reinterpret_cast<const float2*>(w + k0);
+  const float2 iv = act_inv ? *reinterpret_cast<const float2*>(act_inv + k0) : make_float2(1.f, 1.f);
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    float h0 = wv.x * (r.v[m][0] * inv[m]), h1 = wv.y * (r.v[m][1] * inv[m]);
+    if (act_inv) {
+      h0 = __fmul_rn(h0, iv.x);
+      h1 = __fmul_rn(h1, iv.y);
+    }
+    *reinterpret_cast<float2*>(xs + m * H + xoff(k0)) = make_float2(h0, h1);
+  }
+}
+
+template <int MT>
+__device__ __forceinline__ void load_rows(const float* src, int H, int M, Resid<MT>& x) {
+  const int k0 = 2 * threadIdx.x;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const float2 v = (m < M && k0 < H)
+                         ? *reinterpret_cast<const float2*>(src + static_cast<int64_t>(m) * H + k0)
+                         : make_float2(0.f, 0.f);
+    x.v[m][0] = v.x;
+    x.v[m][1] = v.y;
+  }
+}
+
+// Writes the residual channels [lo, hi) of rows m < M (thread t owns 2t, 2t + 1).
+template <int MT>
+__device__ __forceinline__ void store_rows(const Resid<MT>& x, float* out, int H, int M, int lo,
+                                           int hi) {
+  const int k0 = 2 * threadIdx.x;
+  if (k0 < lo || k0 >= hi || k0 >= H) return;
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+    if (m < M)
+      *reinterpret_cast<float2*>(out + static_cast<int64_t>(m) * H + k0) =
+          make_float2(x.v[m][0], x.v[m][1]);
+}
+
+// Marks this workgroup finished; the last one advances the tag base (skipping the value whose
+// tag would wrap to 0) for the next launch. Every workgroup read the base when it started.
+__device__ __forceinline__ void finish(const ChainArgs& a) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t n = __hip_atomic_fetch_add(a.ctl + 1, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    if (n + 1 == gridDim.x) {
+      const uint32_t cur = __hip_atomic_load(a.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.ctl, cur >= 0xfffffffeu ? 0u : cur + 1u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Bits 0 .. n-1.
+__device__ __forceinline__ uint32_t low_bits(int n) { return n >= 32 ? ~0u : (1u << n) - 1u; }
+
+// ---- the two kinds of workgroup ----------------------------------------------------------------
+
+template <int MT>
+__device__ void mlp_group(const ChainArgs& a, uint32_t tag, float* lds, float* red) {
+  const int w = blockIdx.x;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int H = a.H, Kq = a.Kq, I = a.I, M = a.M;
+  const int C = I / a.mlp_groups;  // gate (and up) channels of this workgroup
+  const int passes = 2 * C / (2 * kWaves);
+  const int half = lane / 32, hl = lane % 32;
+  const int k0 = 2 * threadIdx.x;
+  float* xs = lds;                        // staged activations [MT][K] (xoff)
+  float* rows = lds + kMaxRows * kMaxI;   // per-stage row results
+
+  // 1. o_proj's weights and the attention rows first (the first stage waits only for them),
+  //    then gate_up's and down's weights, then the residual rows
+  const int orow = 8 * w + wave;
+  const Chunk fo = fetch(a.o_nib, a.o_s, a.o_z, Kq, orow, lane, lane < Kq / 32);
+  Staged<MT> st;
+  stage_load(st, a.attn, a.o_inv, Kq, M);
+  Chunk fg[kMaxGuPass];
+#pragma unroll
+  for (int p = 0; p < kMaxGuPass; ++p) {
+    const int r = 16 * p + 2 * wave + half;  // gate rows 0..C-1, then up rows
+    const bool on = p < passes && hl < H / 32;
+    const int row = p < passes ? (r < C ? C * w + r : I + C * w + (r - C)) : C * w;
+    fg[p] = fetch(a.gu_nib, a.gu_s, a.gu_z, H, row, hl, on);
+  }
+  const Chunk fd0 = fetch(a.dn_nib, a.dn_s, a.dn_z, I, orow, lane, lane < I / 32);
+  const Chunk fd1 = fetch(a.dn_nib, a.dn_s, a.dn_z, I, orow, lane + kWave, lane + kWave < I / 32);
+  Resid<MT> x;
+  load_rows(a.x_in, H, M, x);
+  stage_store(st, xs, Kq);
+  __syncthreads();
+
+  // 2. o_proj row 8w + wave -> ex1
+  {
+    float v[MT];
+    chunk_terms<MT>(fo, lane, xs, Kq, v);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float t = lsh::group_total<kWave>(v[m]);
+      if (m < M && lane == kWave - 1) put(a.ex1 + m * H + orow, t, tag);
+    }
+  }
+
+  // 3. x += o (all channels, all rows), post-attention norm times gate_up's inv -> LDS
+  {
+    float o[2 * MT];
+    const uint32_t need = k0 < H ? low_bits(2 * M) : 0u;
+    const bool ok = take<2 * MT>(
+        need, tag, a, [&](int i) { return a.ex1 + (i / 2) * H + k0 + (i % 2); },
+        [&](int i, float val) { o[i] = val; });
+    if (__syncthreads_or(!ok)) return finish(a);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      x.v[m][0] = x.v[m][0] + o[2 * m];
+      x.v[m][1] = x.v[m][1] + o[2 * m + 1];
+    }
+    norm_to_lds(x, a.post_w, a.gu_inv, a.eps, H, M, xs, red);  // after its barriers
+    __syncthreads();
+  }
+
+  // 4. gate_up rows (16 per pass), silu(gate) * up of the workgroup's C channels -> ex2
+  {
+#pragma unroll
+    for (int p = 0; p < kMaxGuPass; ++p) {
+      if (p >= passes) break;
+      float v[MT];
+      chunk_terms<MT>(fg[p], hl, xs, H, v);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float t = lsh::group_total<32>(v[m]);
+        if (hl == 31) rows[(16 * p + 2 * wave + half) * kMaxRows + m] = t;
+      }
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < C * M) {
+      const int j = t % C, m = t / C;
+      const float g = rows[j * kMaxRows + m], u = rows[(C + j) * kMaxRows + m];
+      put(a.ex2 + m * I + C * w + j, g / (1.f + expf(-g)) * u, tag);
+    }
+  }
+
+  // 5. down_proj row 8w + wave over the I channels of silu * up -> ex3
+  {
+    constexpr int kPer = kMaxI / kThreads;  // words per thread per row
+    const int per = I / kThreads;           // I % 512 == 0 (checked by the host)
+    uint32_t need = 0;
+#pragma unroll
+    for (int i = 0; i < MT * kPer; ++i)
+      if (i / kPer < M && i % kPer < per) need |= 1u << i;
+    __syncthreads();  // every wavefront is done with the gate_up stage's LDS rows
+    const bool ok = take<MT * kPer>(
+        need, tag, a,
+        [&](int i) { return a.ex2 + (i / kPer) * I + threadIdx.x + (i % kPer) * kThreads; },
+        [&](int i, float val) {
+          const int k = threadIdx.x + (i % kPer) * kThreads;
+          xs[(i / kPer) * I + xoff(k)] = a.dn_inv ? __fmul_rn(val, a.dn_inv[k]) : val;
+        });
+    // rows M..MT-1 of the staged input are never read into a stored sum; keep them finite
+    if (__syncthreads_or(!ok)) return finish(a);
+    float v0[MT], v1[MT];
+    chunk_terms<MT>(fd0, lane, xs, I, v0);
+    chunk_terms<MT>(fd1, lane + kWave, xs, I, v1);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float t = lsh::group_total<kWave>(v0[m] + v1[m]);
+      if (m < M && lane == kWave - 1) put(a.ex3 + m * H + orow, t, tag);
+    }
+  }
+
+  // 6. the last layer: x += down, the residual channels 8w..8w+7 and their final norm
+  if (a.head_groups == 0) {
+    float dv[2 * MT];
+    const uint32_t need = k0 < H ? low_bits(2 * M) : 0u;
+    const bool ok = take<2 * MT>(
+        need, tag, a, [&](int i) { return a.ex3 + (i / 2) * H + k0 + (i % 2); },
+        [&](int i, float val) { dv[i] = val; });
+    if (__syncthreads_or(!ok)) return finish(a);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      x.v[m][0] = x.v[m][0] + dv[2 * m];
+      x.v[m][1] = x.v[m][1] + dv[2 * m + 1];
+    }
+    store_rows(x, a.x_out, H, M, 8 * w, 8 * w + 8);
+    if (a.h_out) {
+      float inv[MT];
+      row_inv_rms(x, H, M, a.eps, red, inv);
+      if (k0 >= 8 * w && k0 < 8 * w + 8) {
+        const float2 wv = *reinterpret_cast<const float2*>(a.next_w + k0);
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          if (m < M)
+            *reinterpret_cast<float2*>(a.h_out + static_cast<int64_t>(m) * H + k0) =
+                make_float2(wv.x * (x.v[m][0] * inv[m]), wv.y * (x.v[m][1] * inv[m]));
+      }
+    }
+  }
+  finish(a);
+}
+
+template <int MT>
+__device__ void head_group(const ChainArgs& a, uint32_t tag, float* lds, float* red) {
+  const int hh = blockIdx.x - a.mlp_groups;  // q heads, then k heads, then v heads
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int H = a.H, M = a.M;
+  const int half = lane / 32, hl = lane % 32;
+  const int k0 = 2 * threadIdx.x;
+  constexpr int D = kHeadDim;
+  float* xs = lds;
+  float* out = lds + kMaxRows * kMaxI;  // [D][kMaxRows]
+
+  // 1. the head's 128 qkv rows (a lane: chunk hl of rows 16 wave + 2 p + half)
+  Chunk fq[kHeadPasses];
+#pragma unroll
+  for (int p = 0; p < kHeadPasses; ++p)
+    fq[p] = fetch(a.qkv_nib, a.qkv_s, a.qkv_z, H, static_cast<int64_t>(hh) * D + 16 * wave + 2 * p + half,
+                  hl, hl < H / 32);
+  // 2. the residual rows: (x + o) + down, or the embedding rows
+  Resid<MT> x;
+  if (a.mlp_groups == 0) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int64_t id = m < M ? a.ids[m] : 0;
+      float2 v = make_float2(0.f, 0.f);
+      if (m < M && k0 < H)
+        v = (id >= 0 && id < a.vocab) ? *reinterpret_cast<const float2*>(a.embed + id * H + k0)
+                                      : make_float2(__builtin_nanf(""), __builtin_nanf(""));
+      x.v[m][0] = v.x;
+      x.v[m][1] = v.y;
+    }
+  } else {
+    load_rows(a.x_in, H, M, x);
+    // words [0, 2 MT): down (m, c) -- the last hand-off, polled first; [2 MT, 4 MT): o (m, c)
+    float od[4 * MT];
+    const uint32_t rows_mask = low_bits(2 * M);
+    const uint32_t need = k0 < H ? (rows_mask | (rows_mask << (2 * MT))) : 0u;
+    const bool ok = take<4 * MT>(
+        need, tag, a,
+        [&](int i) {
+          const int j = i % (2 * MT);
+          return (i < 2 * MT ? a.ex3 : a.ex1) + (j / 2) * H + k0 + (j % 2);
+        },
+        [&](int i, float val) { od[i] = val; });
+    if (__syncthreads_or(!ok)) return finish(a);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      x.v[m][0] = (x.v[m][0] + od[2 * MT + 2 * m]) + od[2 * m];
+      x.v[m][1] = (x.v[m][1] + od[2 * MT + 2 * m + 1]) + od[2 * m + 1];
+    }
+  }
+  {  // this group's share of the new residual channels
+    const int share = H / a.head_groups;
+    store_rows(x, a.x_out, H, M, hh * share, (hh + 1) * share);
+  }
+
+  // 3. the next layer's input norm times qkv's inv -> LDS, then the head's 128 rows
+  norm_to_lds(x, a.next_w, a.qkv_inv, a.eps, H, M, xs, red);
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < kHeadPasses; ++p) {
+    float v[MT];
+    chunk_terms<MT>(fq[p], hl, xs, H, v);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float t = lsh::group_total<32>(v[m]);
+      if (hl == 31) out[(16 * wave + 2 * p + half) * kMaxRows + m] = t;
+    }
+  }
+  __syncthreads();
+
+  // 4. one wavefront per sequence: q/k norm + RoPE at position ctx - 1, then q out or the
+  //    int8 cache write (the quantizer of llmserve_kv_quantize_write)
+  const int m = wave;
+  if (m < M) {
+    float v[2];
+    v[0] = out[lane * kMaxRows + m];
+    v[1] = out[(lane + kWave) * kMaxRows + m];
+    const int64_t pos = a.ctx[m] - 1;
+    const bool ok = pos >= 0 && pos < a.max_pos && pos / a.bs < a.max_blocks;
+    const bool is_q = hh < a.nq, is_k = !is_q && hh < a.nq + a.nk;
+    if (ok) {
+      if (is_q || is_k)
+        lsh::norm_rope(v, is_q ? a.q_w : a.k_w, a.cos_t + pos * D, a.sin_t + pos * D, D, a.eps);
+      if (is_q) {
+        float* o = a.q_out + (static_cast<int64_t>(m) * a.nq + hh) * D;
+        o[lane] = v[0];
+        o[lane + kWave] = v[1];
+      } else {
+        const int64_t blk = a.bt[m * a.max_blocks + pos / a.bs];
+        const int64_t slot = blk * a.bs + pos % a.bs;
+        if (blk >= 0 && slot < a.num_slots) {
+          const int h = is_k ? hh - a.nq : hh - a.nq - a.nk;
+          const int64_t at = slot * a.nk + h;
+          if (is_k)
+            lsh::kv_quant_row(v, a.smooth ? a.smooth + static_cast<int64_t>(h) * D : nullptr, D,
+                              a.kc + at * D, a.ks + at);
+          else
+            lsh::kv_quant_row(v, nullptr, D, a.vc + at * D, a.vs + at);
+        }
+      }
+    } else if (is_q) {  // a position outside the tables: a NaN q, visible in the logits
+      float* o = a.q_out + (static_cast<int64_t>(m) * a.nq + hh) * D;
+      o[lane] = __builtin_nanf("");
+      o[lane + kWave] = __builtin_nanf("");
+    }
+  }
+  finish(a);
+}
+
+template <int MT>
+__global__ __launch_bounds__(kThreads) void decode_chain_kernel(ChainArgs a) {
+  // staged rows ([MT][K] floats, K up to kMaxI) and after them a stage's row results
+  __shared__ __align__(16) float lds[kMaxRows * kMaxI + kHeadDim * kMaxRows];
+  __shared__ float red[kWaves];
+  const uint32_t tag = __hip_atomic_load(a.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  if (static_cast<int>(blockIdx.x) < a.mlp_groups)
+    mlp_group<MT>(a, tag, lds, red);
+  else
+    head_group<MT>(a, tag, lds, red);
+}
+
+template <int MT>
+int launch_chain(const ChainArgs& a, int grid, hipStream_t st) {
+  int dev = 0, cus = 0, per = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, decode_chain_kernel<MT>, kThreads, 0) !=
+          hipSuccess) {
+    lsh::set_error("decode_chain: device query failed");
+    return LLMSERVE_ERR_HIP;
+  }
+  // every workgroup must be resident at once (they wait for each other)
+  LSH_CHECK(static_cast<int64_t>(cus) * per >= grid,
+            "decode_chain: %d workgroups do not fit at once (%d CUs x %d)", grid, cus, per);
+  lsh::launch(decode_chain_kernel<MT>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, st,
+              true, a);
+  return lsh::launch_status("decode_chain");
+}
+
+}  // namespace
+
+extern "C" int64_t llmserve_decode_chain_workspace_bytes(int64_t H, int64_t I) {
+  if (H <= 0 || I <= 0) return 0;
+  return 256 + static_cast<int64_t>(kMaxRows) * (2 * H + I) * 8;
+}
+
+extern "C" int llmserve_decode_chain(
+    const float* attn, const float* x_in, const int64_t* ids, const float* embed, int64_t vocab,
+    float* x_out, float* h_out, const uint8_t* o_nib, const float* o_s, const float* o_z,
+    const float* o_inv, const float* post_w, const uint8_t* gu_nib, const float* gu_s,
+    const float* gu_z, const float* gu_inv, const uint8_t* dn_nib, const float* dn_s,
+    const float* dn_z, const float* dn_inv, const float* next_w, const uint8_t* qkv_nib,
+    const float* qkv_s, const float* qkv_z, const float* qkv_inv, const float* q_w,
+    const float* k_w, const float* cos_t, const float* sin_t, int64_t max_pos,
+    const int64_t* context_lens, const int64_t* block_tables, int64_t max_blocks,
+    int64_t block_size, const float* k_smooth, float* q_out, int8_t* k_cache, int8_t* v_cache,
+    float* k_scale, float* v_scale, int64_t num_slots, int64_t M, int64_t H, int64_t I,
+    int64_t n_q, int64_t n_k, int64_t head_dim, int64_t group_size, float eps, void* workspace,
+    int64_t workspace_bytes, int64_t spin_limit, void* stream) {
+  const bool mlp = attn != nullptr, next = qkv_nib != nullptr;
+  LSH_CHECK(M >= 1 && M <= kMaxRows, "decode_chain: 1 to %d rows (got %lld)", kMaxRows, (long long)M);
+  LSH_CHECK(head_dim == kHeadDim && group_size == kGroup,
+            "decode_chain: head_dim and group_size must be 128 (got %lld, %lld)",
+            (long long)head_dim, (long long)group_size);
+  LSH_CHECK(H >= 256 && H <= kMaxH && H % 128 == 0, "decode_chain: hidden size %lld not in "
+            "{256, 384, ..., 1024}", (long long)H);
+  LSH_CHECK(n_q >= 1 && n_k >= 1 && n_q % n_k == 0, "decode_chain: bad head counts");
+  LSH_CHECK(H % (2 * (n_q + 2 * n_k)) == 0,
+            "decode_chain: H must split evenly over the n_q + 2 n_k head groups");
+  const int64_t Kq = n_q * head_dim;
+  const int64_t mlp_groups = mlp ? H / 8 : 0;
+  LSH_CHECK(mlp || next, "decode_chain: nothing to do (no attention input and no qkv)");
+  if (mlp) {
+    LSH_CHECK(Kq <= kMaxKq && Kq % 128 == 0, "decode_chain: n_q * head_dim = %lld above %d",
+              (long long)Kq, kMaxKq);
+    LSH_CHECK(I % kThreads == 0 && I <= kMaxI && I % mlp_groups == 0,
+              "decode_chain: intermediate size %lld must be a multiple of %d and of H / 8, "
+              "at most %d", (long long)I, kThreads, kMaxI);
+    const int64_t C = I / mlp_groups;
+    LSH_CHECK(C % kWaves == 0 && 2 * C <= 2 * kWaves * kMaxGuPass,
+              "decode_chain: %lld gate channels per workgroup (need a multiple of %d, <= %d)",
+              (long long)C, kWaves, kWaves * kMaxGuPass);
+    LSH_CHECK(x_in && o_nib && o_s && o_z && post_w && gu_nib && gu_s && gu_z && dn_nib && dn_s &&
+                  dn_z && next_w,
+              "decode_chain: null MLP pointer");
+  } else {
+    LSH_CHECK(ids && embed && vocab > 0, "decode_chain: the embedding mode needs ids and embed");
+  }
+  if (next) {
+    LSH_CHECK(qkv_s && qkv_z && next_w && cos_t && sin_t && context_lens && block_tables &&
+                  q_out && k_cache && v_cache && k_scale && v_scale,
+              "decode_chain: null qkv pointer");
+    LSH_CHECK(max_blocks >= 1 && block_size >= 1 && max_pos >= 1, "decode_chain: empty tables");
+  } else {
+    LSH_CHECK(mlp, "decode_chain: the last layer needs the MLP part");
+  }
+  LSH_CHECK(x_out != nullptr, "decode_chain: null x_out");
+  LSH_CHECK(workspace && lsh::aligned16(workspace) &&
+                workspace_bytes >= llmserve_decode_chain_workspace_bytes(H, I),
+            "decode_chain: workspace of %lld bytes needed",
+            (long long)llmserve_decode_chain_workspace_bytes(H, I));
+  auto al = [](const void* p) { return p == nullptr || lsh::aligned16(p); };
+  LSH_CHECK(al(attn) && al(x_in) && al(embed) && al(o_nib) && al(gu_nib) && al(dn_nib) &&
+                al(qkv_nib) && al(o_inv) && al(gu_inv) && al(dn_inv) && al(qkv_inv) &&
+                al(post_w) && al(next_w),
+            "decode_chain: weights, activations and norm weights must be 16-byte aligned");
+
+  ChainArgs a{};
+  a.attn = attn;
+  a.x_in = x_in;
+  a.ids = ids;
+  a.embed = embed;
+  a.vocab = vocab;
+  a.x_out = x_out;
+  a.h_out = h_out;
+  a.o_nib = o_nib;
+  a.o_s = o_s;
+  a.o_z = o_z;
+  a.o_inv = o_inv;
+  a.post_w = post_w;
+  a.gu_nib = gu_nib;
+  a.gu_s = gu_s;
+  a.gu_z = gu_z;
+  a.gu_inv = gu_inv;
+  a.dn_nib = dn_nib;
+  a.dn_s = dn_s;
+  a.dn_z = dn_z;
+  a.dn_inv = dn_inv;
+  a.next_w = next_w;
+  a.qkv_nib = qkv_nib;
+  a.qkv_s = qkv_s;
+  a.qkv_z = qkv_z;
+  a.qkv_inv = qkv_inv;
+  a.q_w = q_w;
+  a.k_w = k_w;
+  a.cos_t = cos_t;
+  a.sin_t = sin_t;
+  a.max_pos = max_pos;
+  a.ctx = context_lens;
+  a.bt = block_tables;
+  a.max_blocks = max_blocks;
+  a.bs = block_size;
+  a.num_slots = num_slots;
+  a.smooth = k_smooth;
+  a.q_out = q_out;
+  a.kc = k_cache;
+  a.vc = v_cache;
+  a.ks = k_scale;
+  a.vs = v_scale;
+  char* ws = static_cast<char*>(workspace);
+  a.ctl = reinterpret_cast<uint32_t*>(ws);
+  a.ex1 = reinterpret_cast<uint64_t*>(ws + 256);
+  a.ex2 = a.ex1 + kMaxRows * H;
+  a.ex3 = a.ex2 + kMaxRows * I;
+  a.spin_limit = static_cast<uint32_t>(spin_limit < 0 ? 0 : (spin_limit > 0x7fffffff ? 0x7fffffff : spin_limit));
+  a.M = static_cast<int>(M);
+  a.H = static_cast<int>(H);
+  a.Kq = static_cast<int>(Kq);
+  a.I = static_cast<int>(I);
+  a.nq = static_cast<int>(n_q);
+  a.nk = static_cast<int>(n_k);
+  a.mlp_groups = static_cast<int>(mlp_groups);
+  a.head_groups = next ? static_cast<int>(n_q + 2 * n_k) : 0;
+  a.eps = eps;
+  const int grid = a.mlp_groups + a.head_groups;
+  hipStream_t st = lsh::as_stream(stream);
+  switch (M) {
+    case 1: return launch_chain<1>(a, grid, st);
+    case 2: return launch_chain<2>(a, grid, st);
+    default: return launch_chain<4>(a, grid, st);
+  }
+}
+
+// The error word of a chain workspace (1 when a hand-off wait ran out of polls since the
+// workspace was cleared). Synchronizes with the device.
+extern "C" int llmserve_decode_chain_error(const void* workspace, int* error) {
+  LSH_CHECK(workspace && error, "decode_chain_error: null pointer");
+  uint32_t ctl[3] = {0, 0, 0};
+  if (hipMemcpy(ctl, workspace, sizeof(ctl), hipMemcpyDeviceToHost) != hipSuccess) {
+    lsh::set_error("decode_chain_error: hipMemcpy failed");
+    return LLMSERVE_ERR_HIP;
+  }
+  *error = static_cast<int>(ctl[2]);
+  return LLMSERVE_OK;
+}

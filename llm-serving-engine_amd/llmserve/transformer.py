@@ -27,6 +27,8 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
+import ctypes
+
 from llmserve.attention import paged_attention
 from llmserve.kernels import load_fused_ops, load_paged_attention
 from llmserve.quant import Int4Linear, _search_awq_scale
@@ -163,6 +165,119 @@ class QuantCausalLM(nn.Module):
     # (lm_head_f32_xfrag, within a few 1e-6 of fp32) instead of torch.mm (hipBLASLt).
     fp32_head_kernel = True
 
+    # Up to 4 rows the step runs one persistent launch per layer for the whole linear chain
+    # (o_proj .. next qkv, with the norms, silu * up, RoPE and the cache write:
+    # llmserve_decode_chain) instead of a launch per op.
+    use_chain = True
+    chain_spin_limit = 1 << 22  # polls per hand-off wait before the chain gives up
+
+    def _chain_ok(self, rows: int) -> bool:
+        cfg = self.cfg
+        if not (self.use_chain and 1 <= rows <= 4 and self.embed.is_cuda):
+            return False
+        H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+        heads = cfg.num_attention_heads + 2 * cfg.num_key_value_heads
+        if D != 128 or self.group_size != 128 or cfg.num_attention_heads * D > 2048:
+            return False
+        if not (256 <= H <= 1024 and H % 128 == 0 and H % (2 * heads) == 0):
+            return False
+        if not (I % 512 == 0 and I <= 4096 and I % (H // 8) == 0):
+            return False
+        C = I // (H // 8)
+        return C % 8 == 0 and C <= 32
+
+    def chain_workspace(self) -> torch.Tensor:
+        """The chain's hand-off workspace (zeroed once, then owned by the chain launches of
+        this model: steps on one model must not overlap)."""
+        ws = getattr(self, "_chain_ws", None)
+        if ws is None:
+            from llmserve._native import capi
+
+            n = capi().llmserve_decode_chain_workspace_bytes(self.cfg.hidden_size,
+                                                             self.cfg.intermediate_size)
+            ws = torch.zeros(n, dtype=torch.uint8, device=self.embed.device)
+            self._chain_ws = ws
+        return ws
+
+    def chain_error(self) -> int:
+        """Nonzero when a chain hand-off wait ran out of polls (synchronizes)."""
+        from llmserve._native import capi, check
+
+        err = ctypes.c_int(0)
+        check(capi().llmserve_decode_chain_error(ctypes.c_void_p(self.chain_workspace().data_ptr()),
+                                                 ctypes.byref(err)))
+        return err.value
+
+    def _chain(self, *, rows, x_out, attn=None, x_in=None, ids=None, layer=None, nxt=None,
+               h_out=None, q_out=None, caches=None, context_lens=None, block_tables=None,
+               block_size=16, spin_limit=None) -> None:
+        """One llmserve_decode_chain launch: layer ``layer``'s MLP half (None: embedding mode)
+        and ``nxt``'s qkv part (None: the last layer, writing ``h_out``)."""
+        from llmserve._native import capi, check
+
+        cfg = self.cfg
+
+        def p(t):
+            return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+        def lin(m):
+            return [p(m.nibbles), p(m.g_scale), p(m.g_zero), p(m.inv_act_scale)] if m else [None] * 4
+
+        ws = self.chain_workspace()
+        kc = vc = None
+        if nxt is not None:
+            kc, vc = caches
+        args = [p(attn), p(x_in), p(ids), p(self.embed), cfg.vocab_size, p(x_out), p(h_out)]
+        args += lin(layer.o_proj if layer else None)
+        args += [p(layer.post_attention_layernorm) if layer else None]
+        args += lin(layer.gate_up_proj if layer else None)
+        args += lin(layer.down_proj if layer else None)
+        args += [p(nxt.input_layernorm if nxt is not None else self.norm)]
+        args += lin(nxt.qkv_proj if nxt is not None else None)
+        args += [p(nxt.q_norm) if nxt is not None else None, p(nxt.k_norm) if nxt is not None else None,
+                 p(self.rope_cos), p(self.rope_sin), self.rope_cos.shape[0], p(context_lens),
+                 p(block_tables), block_tables.shape[1] if block_tables is not None else 0,
+                 block_size, p(kc.smooth) if kc is not None else None, p(q_out),
+                 p(kc.data) if kc is not None else None, p(vc.data) if vc is not None else None,
+                 p(kc.scale) if kc is not None else None, p(vc.scale) if vc is not None else None,
+                 kc.data.shape[0] if kc is not None else 0, rows, cfg.hidden_size,
+                 cfg.intermediate_size, cfg.num_attention_heads, cfg.num_key_value_heads,
+                 cfg.head_dim, self.group_size, ctypes.c_float(cfg.rms_norm_eps), p(ws), ws.numel(),
+                 self.chain_spin_limit if spin_limit is None else spin_limit,
+                 ctypes.c_void_p(torch.cuda.current_stream(ws.device).cuda_stream)]
+        check(capi().llmserve_decode_chain(*args))
+
+    def _forward_decode_chain(self, ids, context_lens, block_tables, kv_layers, block_size):
+        """forward_decode for 1..4 rows: an embedding + layer-0 qkv launch, then per layer the
+        paged decode and one chain launch (the last one writes the final norm's output)."""
+        cfg = self.cfg
+        pa = load_paged_attention()
+        B, H = ids.numel(), cfg.hidden_size
+        nq, D = cfg.num_attention_heads, cfg.head_dim
+        dev = self.embed.device
+        n = len(self.layers)
+        x = torch.empty(B, H, device=dev)
+        q = torch.empty(B, nq, D, device=dev)
+        self._chain(rows=B, x_out=x, ids=ids, nxt=self.layers[0], q_out=q, caches=kv_layers[0],
+                    context_lens=context_lens, block_tables=block_tables, block_size=block_size)
+        h = None
+        for i, L in enumerate(self.layers):
+            kc, vc = kv_layers[i]
+            attn = pa.paged_attention_decode_int8(q, kc.data, vc.data, kc.scale, vc.scale,
+                                                  block_tables, context_lens, block_size,
+                                                  self.scale, 0, kc._q_mult)
+            nxt = self.layers[i + 1] if i + 1 < n else None
+            x_new = torch.empty(B, H, device=dev)
+            q = torch.empty(B, nq, D, device=dev) if nxt is not None else None
+            if nxt is None:
+                h = torch.empty(B, H, device=dev)
+            self._chain(rows=B, x_out=x_new, attn=attn.view(B, nq * D), x_in=x, layer=L, nxt=nxt,
+                        h_out=h, q_out=q, caches=kv_layers[i + 1] if nxt is not None else None,
+                        context_lens=context_lens, block_tables=block_tables,
+                        block_size=block_size)
+            x = x_new
+        return h
+
     def _xfrag_ok(self, rows: int) -> bool:
         lins = [m for L in self.layers for m in (L.qkv_proj, L.o_proj, L.gate_up_proj, L.down_proj)]
         # the attention merge writes fragments of whole 128-channel blocks: head_dim 128 or 256
@@ -209,6 +324,9 @@ class QuantCausalLM(nn.Module):
         position is ctx - 1); ``block_tables`` [B, max_blocks] int64 holds the blocks of every
         position up to ctx - 1; ``kv_layers`` is ``KVCache.layers`` with int8 ``QuantizedKV``
         pairs. Writes this token's K and V into the caches. No host synchronization."""
+        if self._chain_ok(ids.numel()):
+            return self._forward_decode_chain(ids, context_lens, block_tables, kv_layers,
+                                              block_size)
         cfg = self.cfg
         fo, pa = _fused_ops(), load_paged_attention()
         nq, nk, D, eps = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rms_norm_eps

@@ -1,0 +1,162 @@
+"""The decode chain (llmserve_decode_chain: one persistent launch per layer for 1-4 rows)
+against the per-op decode step, and its bounded waits.
+
+The per-op step (QuantCausalLM.use_chain = False: the GEMV linears and the fused norm / silu /
+rope-and-write kernels, each pinned against the oracle elsewhere) is the reference here: the
+chain computes the same float32 operations in other summation orders, so logits agree within
+2e-5 of max|logits| (the tolerance of the GEMV step against the oracle; 2e-3 for two-layer
+models, see the test) and the int8 K/V rows
+it writes are within one quantization step (under 1% of values) at the same slots, every other
+slot unchanged. The step oracle comparison of tests/test_gpu_step.py runs the chain as well
+(its 2- and 4-row cases). Graph replays of chain steps are bit-identical to eager ones. A
+chain whose hand-off waits are given no poll budget gives up, sets its error word and the
+grid finishes; the next launch on the workspace is correct.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_step import BS, setup, tiny_cfg
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny1_cfg():
+    import dataclasses
+
+    return dataclasses.replace(tiny_cfg(), num_hidden_layers=1)
+
+
+def qwen_like_cfg(layers=2):
+    from llmserve.transformer import ModelConfig
+
+    return ModelConfig(vocab_size=4096, hidden_size=1024, intermediate_size=3072,
+                       num_hidden_layers=layers, num_attention_heads=16, num_key_value_heads=8,
+                       head_dim=128, max_position_embeddings=8192)
+
+
+def _step_both(cfg, ctx, seed):
+    """(chain run, per-op run) of one step from the same state: logits, ids, caches."""
+    model, cache, runner, host, ids, ctx, bt = setup(cfg, ctx, seed)
+    assert model._chain_ok(len(ids))
+    start = runner.snapshot()
+    out = []
+    for chain in (True, False):
+        runner.restore(start)
+        model.use_chain = chain
+        runner.step()
+        torch.cuda.synchronize()
+        out.append((runner.logits.clone(), runner.ids.clone(), runner.context_lens.clone(),
+                    runner.snapshot()[2]))
+    model.use_chain = True
+    assert model.chain_error() == 0
+    return out, start
+
+
+def qwen1_cfg():
+    return qwen_like_cfg(1)
+
+
+# With one layer both runs attend over the same cache rows: 2e-5. With two, layer 1's new K/V
+# rows are quantized from activations that differ by ~1e-6, so a value at a rounding boundary
+# can land one int8 step apart, and over a 3-token context one such step moves the logits by
+# up to a few 1e-4: 2e-3 (the K/V check below still bounds those steps).
+@pytest.mark.parametrize("cfg_fn,ctx,tol", [
+    (tiny1_cfg, [37], 2e-5), (tiny1_cfg, [1, 300], 2e-5), (tiny1_cfg, [5, 16, 17], 2e-5),
+    (tiny1_cfg, [9, 64, 200, 511], 2e-5), (qwen1_cfg, [700], 2e-5),
+    (qwen1_cfg, [3, 1024, 77, 2049], 2e-5),
+    (tiny_cfg, [9, 64, 200, 511], 2e-3), (qwen_like_cfg, [3, 1024, 77, 2049], 2e-3),
+])
+def test_chain_step_matches_per_op_step(gpu, cfg_fn, ctx, tol):
+    cfg = cfg_fn()
+    (a, b), start = _step_both(cfg, ctx, 41 + len(ctx))
+    la, lb = a[0].double(), b[0].double()
+    err = float((la - lb).abs().max() / lb.abs().max())
+    assert err < tol, err
+    assert torch.equal(a[2], b[2])
+    top2 = torch.topk(lb, 2, dim=-1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 1e-4 * lb.abs().max()
+    assert torch.equal(a[1][clear], b[1][clear])
+    for (ka, ksa, va, vsa), (kb, ksb, vb, vsb), (k0, ks0, v0, vs0) in zip(a[3], b[3], start[2]):
+        for x, y in ((ka, kb), (va, vb)):
+            d = (x.to(torch.int32) - y.to(torch.int32)).abs()
+            assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 0.01
+        torch.testing.assert_close(ksa, ksb, rtol=2e-5, atol=0)
+        torch.testing.assert_close(vsa, vsb, rtol=2e-5, atol=0)
+        # only the new tokens' slots changed
+        changed = (ka != k0).any(-1).any(-1) | (ksa != ks0).any(-1)
+        assert int(changed.sum()) <= len(ctx)
+
+
+def test_chain_graph_replays_equal_eager(gpu):
+    cfg = tiny_cfg()
+    _, cache, runner, _, _, _, _ = setup(cfg, [30, 150, 77], 23, extra=8)
+    assert runner.model._chain_ok(3)
+    start = runner.snapshot()
+    eager = []
+    for _ in range(3):
+        runner.step()
+        eager.append((runner.ids.clone(), runner.logits.clone(), runner.context_lens.clone()))
+    eager_cache = runner.snapshot()[2]
+    runner.restore(start)
+    runner.capture(keep_state=True)
+    for i in range(3):
+        runner.replay()
+        torch.cuda.synchronize()
+        _ = torch.randn(1000, device="cuda").sum().item()  # unrelated eager work between replays
+        ids, logits, ctx = eager[i]
+        assert torch.equal(runner.ids, ids)
+        assert torch.equal(runner.logits, logits)
+        assert torch.equal(runner.context_lens, ctx)
+    for (k, v), (kd, ks, vd, vs) in zip(cache.layers, eager_cache):
+        assert torch.equal(k.data, kd) and torch.equal(k.scale, ks)
+        assert torch.equal(v.data, vd) and torch.equal(v.scale, vs)
+    assert runner.model.chain_error() == 0
+
+
+def test_chain_gives_up_without_poll_budget(gpu):
+    """spin_limit 0: every hand-off gets one poll; waits that find their words missing give
+    up, set the error word, and the grid drains (the launch returns). The workspace then
+    serves a normal launch."""
+    cfg = tiny_cfg()
+    model, cache, runner, host, ids, ctx, bt = setup(cfg, [40, 90], 61)
+    B, H = 2, cfg.hidden_size
+    nq, D = cfg.num_attention_heads, cfg.head_dim
+    dev = torch.device("cuda")
+    x = torch.randn(B, H, device=dev)
+    attn = torch.randn(B, nq * D, device=dev)
+    x_out = torch.empty(B, H, device=dev)
+    q = torch.empty(B, nq, D, device=dev)
+    kw = dict(rows=B, attn=attn, x_in=x, layer=model.layers[0], nxt=model.layers[1], q_out=q,
+              caches=cache.layers[1], context_lens=runner.context_lens,
+              block_tables=runner.block_tables, block_size=BS)
+    failed = 0
+    for _ in range(20):  # one poll is rarely enough for all groups
+        model._chain(x_out=x_out, spin_limit=0, **kw)
+        torch.cuda.synchronize()
+        failed += model.chain_error() != 0
+        model.chain_workspace()[8:12].zero_()  # clear the error word (ctl[2])
+    assert failed > 0
+    model._chain(x_out=x_out, **kw)
+    ref = x_out.clone()
+    model._chain(x_out=x_out, **kw)
+    torch.cuda.synchronize()
+    assert model.chain_error() == 0 and torch.equal(x_out, ref)
+    assert torch.isfinite(ref).all()
+
+
+def test_chain_rejects_bad_geometry(gpu):
+    from llmserve.transformer import ModelConfig, QuantCausalLM
+
+    cfg = ModelConfig(vocab_size=512, hidden_size=384, intermediate_size=1024,
+                      num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2,
+                      head_dim=128, max_position_embeddings=256)
+    m = QuantCausalLM(cfg, 128, seed=1)
+    assert not m._chain_ok(1)  # I = 1024 is not a multiple of H / 8 = 48
+    with pytest.raises(RuntimeError, match="intermediate size"):
+        m._chain(rows=1, x_out=torch.empty(1, 384, device="cuda"),
+                 attn=torch.zeros(1, 512, device="cuda"), x_in=torch.zeros(1, 384, device="cuda"),
+                 layer=m.layers[0], h_out=torch.empty(1, 384, device="cuda"))
