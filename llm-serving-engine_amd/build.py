@@ -84,11 +84,24 @@ def _torch_paths() -> tuple[list[str], list[str]]:
     return inc, [lib]
 
 
+def _includes(path: Path, seen: set[Path]) -> set[Path]:
+    """The in-tree headers `path` includes, transitively."""
+    import re
+
+    for name in re.findall(r'^#include "([^"]+)"', path.read_text(), re.M):
+        for d in (CSRC, INCLUDE):
+            h = d / name
+            if h.is_file() and h not in seen:
+                seen.add(h)
+                _includes(h, seen)
+    return seen
+
+
 def _stale(src: Path, obj: Path) -> bool:
-    """True when obj is missing or older than its source or any header it may include."""
+    """True when obj is missing or older than its source or a header it includes."""
     if not obj.is_file():
         return True
-    deps = [src, *CSRC.glob("*.h"), *INCLUDE.glob("*.h"), Path(__file__)]
+    deps = [src, *_includes(src, set()), Path(__file__)]
     return max(d.stat().st_mtime for d in deps) > obj.stat().st_mtime
 
 

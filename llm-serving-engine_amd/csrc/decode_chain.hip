@@ -86,44 +86,60 @@ struct ChainArgs {
   int8_t *kc, *vc;
   float *ks, *vs;
   // hand-offs and control words
-  uint64_t *ex1, *ex2, *ex3;  // [kMaxRows][H], [kMaxRows][I], [kMaxRows][H]
+  uint64_t *ex1, *ex2, *ex3;  // [kCopies][kMaxRows][H], [..][I], [..][H] words
   uint32_t* ctl;              // tag base, finished workgroups, error
   uint32_t spin_limit;
   int M, H, Kq, I, nq, nk;
   int mlp_groups;   // H / 8, or 0 (embedding mode)
   int head_groups;  // nq + 2 nk, or 0 (last layer)
+  int grid;         // mlp_groups + head_groups
   float eps;
 };
 
 // ---- hand-off words --------------------------------------------------------------------------
+// Each hand-off vector is written in kCopies replicas and a consumer reads the replica of its
+// workgroup index modulo kCopies (the XCD it most likely runs on): every replica's lines are
+// polled by an eighth of the consumers. A consumer polls two words per 16-byte device-scope
+// load (each 8-byte word is stored whole, so each half of a load is one word as stored).
 
-__device__ __forceinline__ void put(uint64_t* p, float v, uint32_t tag) {
+constexpr int kCopies = 8;
+constexpr int kPolicyDevice = 16;  // buffer-load cache policy: device scope (sc1)
+
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void put(uint64_t* base, int64_t stride, int64_t idx, float v,
+                                    uint32_t tag) {
   const uint64_t w = (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, v);
-  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int c = 0; c < kCopies; ++c)
+    __hip_atomic_store(base + c * stride + idx, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ uint64_t peek(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Polls the words addr(i) for the i set in `need` (N <= 32) until each carries `tag`, handing
-// each value to sink(i, value) as it arrives. Every round issues the loads of all missing
-// words together. Returns false when the poll budget runs out (the error word is then set).
-template <int N, typename Addr, typename Sink>
-__device__ bool take(uint32_t need, uint32_t tag, const ChainArgs& a, Addr addr, Sink sink) {
-  static_assert(N <= 32, "take: at most 32 words per thread");
+// Polls the word pairs at byte offsets off(i) of `src` (a 16-byte aligned buffer resource)
+// for the i set in `need` (N <= 32) until both words carry `tag`, handing each pair's values to
+// sink(i, lo, hi) as it arrives. Every round issues the loads of all missing pairs together.
+// Returns false when the poll budget runs out (the error word is then set).
+template <int N, typename Off, typename Sink>
+__device__ bool take(__amdgpu_buffer_rsrc_t src, uint32_t need, uint32_t tag, const ChainArgs& a,
+                     Off off, Sink sink) {
+  static_assert(N <= 32, "take: at most 32 pairs per thread");
   uint32_t ready = 0;
   for (uint32_t spin = 0;; ++spin) {
-    uint64_t w[N];
+    u32x4v w[N];
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      if ((need & ~ready) >> i & 1u) w[i] = peek(addr(i));
+      if ((need & ~ready) >> i & 1u)
+        w[i] = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                              src, static_cast<uint32_t>(off(i)), 0, kPolicyDevice));
 #pragma unroll
-    for (int i = 0; i < N; ++i)
-      if (((need & ~ready) >> i & 1u) && static_cast<uint32_t>(w[i] >> 32) == tag) {
-        sink(i, __builtin_bit_cast(float, static_cast<uint32_t>(w[i])));
+    for (int i = 0; i < N; ++i) {
+      if (!((need & ~ready) >> i & 1u)) continue;
+      const uint32_t t0 = w[i][1], t1 = w[i][3], v0 = w[i][0], v1 = w[i][2];
+      if (t0 == tag && t1 == tag) {
+        sink(i, __builtin_bit_cast(float, v0), __builtin_bit_cast(float, v1));
         ready |= 1u << i;
       }
+    }
     if (ready == need) return true;
     if (spin >= a.spin_limit) {
       __hip_atomic_fetch_or(a.ctl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -133,11 +149,17 @@ __device__ bool take(uint32_t need, uint32_t tag, const ChainArgs& a, Addr addr,
   }
 }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t replica(const uint64_t* base, int64_t words) {
+  const int c = blockIdx.x % kCopies;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(base + c * words), 0,
+                                           static_cast<int>(words * 8), 0x00020000);
+}
+
 // ---- staging and dot products ------------------------------------------------------------------
 
 // LDS offset of channel k of a staged row: 32-channel slice sl = k / 32 keeps its eight
 // 16-byte chunks rotated by sl, so the 16 lanes of a ds_read_b128 phase, reading chunk j of
-// consecutive slices, hit 16 distinct bank groups.
+// consecutive slices, hit 16 distinct bank groups. Channels 2p and 2p + 1 stay adjacent.
 __device__ __forceinline__ int xoff(int k) {
   const int sl = k >> 5, j = (k >> 2) & 7;
   return (sl << 5) + (((j + sl) & 7) << 2) + (k & 3);
@@ -175,10 +197,11 @@ __device__ __forceinline__ Chunk fetch(const uint8_t* nib, const float* gs, cons
 }
 
 // The lane's terms s * sum x'q + (z - 8 s) * sum x' of chunk c (channels 32c..32c+31) of
-// the staged rows m < MT of K channels.
+// the staged rows m < MT of K channels; sum x' is the chunk's sum cs[m * K / 32 + c], staged
+// with the row (it is the same for every weight row).
 template <int MT>
-__device__ __forceinline__ void chunk_terms(const Chunk& f, int c, const float* xs, int K,
-                                            float (&v)[MT]) {
+__device__ __forceinline__ void chunk_terms(const Chunk& f, int c, const float* xs, const float* cs,
+                                            int K, float (&v)[MT]) {
   float q[32];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -193,14 +216,13 @@ __device__ __forceinline__ void chunk_terms(const Chunk& f, int c, const float* 
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
     const float* row = xs + m * K + (c << 5);
-    float d = 0.f, sx = 0.f;
+    float d = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float4 x = lds4(row + (((j + c) & 7) << 2));
       d += x.x * q[4 * j] + x.y * q[4 * j + 1] + x.z * q[4 * j + 2] + x.w * q[4 * j + 3];
-      sx += (x.x + x.y) + (x.z + x.w);
     }
-    v[m] = f.on ? f.s * d + f.zc * sx : 0.f;
+    v[m] = f.on ? f.s * d + f.zc * cs[m * (K >> 5) + c] : 0.f;
   }
 }
 
@@ -227,15 +249,20 @@ __device__ __forceinline__ void stage_load(Staged<MT>& st, const float* src, con
   }
 }
 
+// The staged rows -> LDS (xoff layout) and their chunk sums -> cs (a chunk is the float4s of
+// 8 consecutive threads; K is a multiple of 128, so those 8 are all in or all out).
 template <int MT>
-__device__ __forceinline__ void stage_store(const Staged<MT>& st, float* xs, int K) {
+__device__ __forceinline__ void stage_store(const Staged<MT>& st, float* xs, float* cs, int K) {
   const int n4 = MT * K / 4;
 #pragma unroll
   for (int u = 0; u < Staged<MT>::kN; ++u) {
     const int q = static_cast<int>(threadIdx.x) + u * kThreads;
+    const float4 x = st.v[u];
+    const float sum = lsh::group_sum<8>((x.x + x.y) + (x.z + x.w));
     if (q < n4) {
       const int m = (q * 4) / K, k = (q * 4) % K;
-      *reinterpret_cast<float4*>(xs + m * K + xoff(k)) = st.v[u];
+      *reinterpret_cast<float4*>(xs + m * K + xoff(k)) = x;
+      if (q % 8 == 0) cs[m * (K >> 5) + (k >> 5)] = sum;
     }
   }
 }
@@ -248,6 +275,21 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   if (lane == 0) red[wave] = v;
   __syncthreads();
   return ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+}
+
+// True in every thread when `v` is true in any thread of the block. `slots` holds kWaves ints
+// of LDS that no other code uses. (The runtime's __syncthreads_or reads the workgroup size
+// from the dispatch packet with a global load on every call: a memory round trip on the
+// critical path after each hand-off.)
+__device__ __forceinline__ bool block_any(bool v, int* slots) {
+  const bool w = __builtin_amdgcn_ballot_w64(v) != 0;
+  __syncthreads();  // the previous call's reads are done
+  if (threadIdx.x % kWave == 0) slots[threadIdx.x / kWave] = w;
+  __syncthreads();
+  int r = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) r |= slots[i];
+  return r != 0;
 }
 
 // Residual rows: thread t holds channels 2t and 2t + 1 of rows m < MT.
@@ -268,25 +310,34 @@ __device__ __forceinline__ void row_inv_rms(const Resid<MT>& r, int H, int M, fl
   }
 }
 
-// The RMSNorm w * (r * inv) of the residual rows times act_inv (nullable) -> LDS (xoff).
+// A thread's two channels of a [H] vector (zero past H; null gives `dflt`).
+__device__ __forceinline__ float2 chan2(const float* p, int H, float dflt) {
+  const int k0 = 2 * threadIdx.x;
+  if (p == nullptr) return make_float2(dflt, dflt);
+  return k0 < H ? *reinterpret_cast<const float2*>(p + k0) : make_float2(0.f, 0.f);
+}
+
+// The RMSNorm w * (r * inv) of the residual rows times act_inv (when given) -> LDS (xoff),
+// and each 32-channel chunk's sum (16 consecutive threads; H is a multiple of 128) -> cs.
 template <int MT>
-__device__ __forceinline__ void norm_to_lds(const Resid<MT>& r, const float* w,
-                                            const float* act_inv, float eps, int H, int M,
-                                            float* xs, float* red) {
+__device__ __forceinline__ void norm_to_lds(const Resid<MT>& r, float2 wv, float2 iv, bool inv_on,
+                                            float eps, int H, int M, float* xs, float* cs,
+                                            float* red) {
   float inv[MT];
   row_inv_rms(r, H, M, eps, red, inv);
-  const int k0 = 2 * threadIdx.x;
-  if (k0 >= H) return;
-  const float2 wv = *reinterpret_cast<const float2*>(w + k0);
-  const float2 iv = act_inv ? *reinterpret_cast<const float2*>(act_inv + k0) : make_float2(1.f, 1.f);
+  const int t = threadIdx.x, k0 = 2 * t;
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
     float h0 = wv.x * (r.v[m][0] * inv[m]), h1 = wv.y * (r.v[m][1] * inv[m]);
-    if (act_inv) {
+    if (inv_on) {
       h0 = __fmul_rn(h0, iv.x);
       h1 = __fmul_rn(h1, iv.y);
     }
-    *reinterpret_cast<float2*>(xs + m * H + xoff(k0)) = make_float2(h0, h1);
+    const float sum = lsh::group_sum<16>(h0 + h1);
+    if (k0 < H) {
+      *reinterpret_cast<float2*>(xs + m * H + xoff(k0)) = make_float2(h0, h1);
+      if (t % 16 == 0) cs[m * (H >> 5) + (t >> 4)] = sum;
+    }
   }
 }
 
@@ -317,13 +368,13 @@ __device__ __forceinline__ void store_rows(const Resid<MT>& x, float* out, int H
 }
 
 // Marks this workgroup finished; the last one advances the tag base (skipping the value whose
-// tag would wrap to 0) for the next launch. Every workgroup read the base when it started.
+// tag would wrap to 0) for the next launch. Every workgroup read the base before it counted itself.
 __device__ __forceinline__ void finish(const ChainArgs& a) {
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t n = __hip_atomic_fetch_add(a.ctl + 1, 1u, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
-    if (n + 1 == gridDim.x) {
+    if (n + 1 == static_cast<uint32_t>(a.grid)) {
       const uint32_t cur = __hip_atomic_load(a.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(a.ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(a.ctl, cur >= 0xfffffffeu ? 0u : cur + 1u, __ATOMIC_RELAXED,
@@ -332,13 +383,20 @@ __device__ __forceinline__ void finish(const ChainArgs& a) {
   }
 }
 
+// This launch's tag: the base the previous launch left, plus one. Read after a workgroup has
+// requested its weights, so that those loads do not queue behind this device-scope read.
+__device__ __forceinline__ uint32_t launch_tag(const ChainArgs& a) {
+  return __hip_atomic_load(a.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+}
+
 // Bits 0 .. n-1.
 __device__ __forceinline__ uint32_t low_bits(int n) { return n >= 32 ? ~0u : (1u << n) - 1u; }
 
 // ---- the two kinds of workgroup ----------------------------------------------------------------
 
 template <int MT>
-__device__ void mlp_group(const ChainArgs& a, uint32_t tag, float* lds, float* red) {
+__device__ void mlp_group(const ChainArgs& a, float* xs, float* cs, float* rows, float* red,
+                          int* flags) {
   const int w = blockIdx.x;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int H = a.H, Kq = a.Kq, I = a.I, M = a.M;
@@ -346,11 +404,12 @@ __device__ void mlp_group(const ChainArgs& a, uint32_t tag, float* lds, float* r
   const int passes = 2 * C / (2 * kWaves);
   const int half = lane / 32, hl = lane % 32;
   const int k0 = 2 * threadIdx.x;
-  float* xs = lds;                        // staged activations [MT][K] (xoff)
-  float* rows = lds + kMaxRows * kMaxI;   // per-stage row results
+  const int64_t s1 = static_cast<int64_t>(kMaxRows) * H, s2 = static_cast<int64_t>(kMaxRows) * I;
+  constexpr int kPairs = kMaxI / 2 / kThreads;  // down-input word pairs per thread per row
 
   // 1. o_proj's weights and the attention rows first (the first stage waits only for them),
-  //    then gate_up's and down's weights, then the residual rows
+  //    then gate_up's and down's weights, the residual rows and every small vector a later
+  //    stage needs, so that no stage after a hand-off waits for memory
   const int orow = 8 * w + wave;
   const Chunk fo = fetch(a.o_nib, a.o_s, a.o_z, Kq, orow, lane, lane < Kq / 32);
   Staged<MT> st;
@@ -367,34 +426,47 @@ __device__ void mlp_group(const ChainArgs& a, uint32_t tag, float* lds, float* r
   const Chunk fd1 = fetch(a.dn_nib, a.dn_s, a.dn_z, I, orow, lane + kWave, lane + kWave < I / 32);
   Resid<MT> x;
   load_rows(a.x_in, H, M, x);
-  stage_store(st, xs, Kq);
+  const float2 post_w = chan2(a.post_w, H, 1.f), gu_inv = chan2(a.gu_inv, H, 1.f);
+  const float2 next_w = chan2(a.next_w, H, 1.f);
+  float2 dn_inv[kPairs];
+#pragma unroll
+  for (int i = 0; i < kPairs; ++i) {
+    const int pr = static_cast<int>(threadIdx.x) + i * kThreads;  // channels 2pr, 2pr + 1
+    dn_inv[i] = (a.dn_inv && 2 * pr < I) ? *reinterpret_cast<const float2*>(a.dn_inv + 2 * pr)
+                                         : make_float2(1.f, 1.f);
+  }
+  const uint32_t tag = launch_tag(a);
+  stage_store(st, xs, cs, Kq);
   __syncthreads();
 
   // 2. o_proj row 8w + wave -> ex1
   {
     float v[MT];
-    chunk_terms<MT>(fo, lane, xs, Kq, v);
+    chunk_terms<MT>(fo, lane, xs, cs, Kq, v);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       const float t = lsh::group_total<kWave>(v[m]);
-      if (m < M && lane == kWave - 1) put(a.ex1 + m * H + orow, t, tag);
+      if (m < M && lane == kWave - 1) put(a.ex1, s1, m * H + orow, t, tag);
     }
   }
 
   // 3. x += o (all channels, all rows), post-attention norm times gate_up's inv -> LDS
   {
-    float o[2 * MT];
-    const uint32_t need = k0 < H ? low_bits(2 * M) : 0u;
-    const bool ok = take<2 * MT>(
-        need, tag, a, [&](int i) { return a.ex1 + (i / 2) * H + k0 + (i % 2); },
-        [&](int i, float val) { o[i] = val; });
-    if (__syncthreads_or(!ok)) return finish(a);
+    float o[MT][2];
+    const bool ok = take<MT>(
+        replica(a.ex1, s1), k0 < H ? low_bits(M) : 0u, tag, a,
+        [&](int m) { return (m * H + k0) * 8; },
+        [&](int m, float v0, float v1) {
+          o[m][0] = v0;
+          o[m][1] = v1;
+        });
+    if (block_any(!ok, flags)) return finish(a);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      x.v[m][0] = x.v[m][0] + o[2 * m];
-      x.v[m][1] = x.v[m][1] + o[2 * m + 1];
+      x.v[m][0] = x.v[m][0] + o[m][0];
+      x.v[m][1] = x.v[m][1] + o[m][1];
     }
-    norm_to_lds(x, a.post_w, a.gu_inv, a.eps, H, M, xs, red);  // after its barriers
+    norm_to_lds(x, post_w, gu_inv, a.gu_inv != nullptr, a.eps, H, M, xs, cs, red);
     __syncthreads();
   }
 
@@ -404,74 +476,90 @@ __device__ void mlp_group(const ChainArgs& a, uint32_t tag, float* lds, float* r
     for (int p = 0; p < kMaxGuPass; ++p) {
       if (p >= passes) break;
       float v[MT];
-      chunk_terms<MT>(fg[p], hl, xs, H, v);
+      chunk_terms<MT>(fg[p], hl, xs, cs, H, v);
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         const float t = lsh::group_total<32>(v[m]);
-        if (hl == 31) rows[(16 * p + 2 * wave + half) * kMaxRows + m] = t;
+        if (hl == 31) rows[(16 * p + 2 * wave + half) * MT + m] = t;
       }
     }
     __syncthreads();
     const int t = threadIdx.x;
     if (t < C * M) {
       const int j = t % C, m = t / C;
-      const float g = rows[j * kMaxRows + m], u = rows[(C + j) * kMaxRows + m];
-      put(a.ex2 + m * I + C * w + j, g / (1.f + expf(-g)) * u, tag);
+      const float g = rows[j * MT + m], u = rows[(C + j) * MT + m];
+      put(a.ex2, s2, m * I + C * w + j, g / (1.f + expf(-g)) * u, tag);
     }
   }
 
   // 5. down_proj row 8w + wave over the I channels of silu * up -> ex3
   {
-    constexpr int kPer = kMaxI / kThreads;  // words per thread per row
-    const int per = I / kThreads;           // I % 512 == 0 (checked by the host)
     uint32_t need = 0;
 #pragma unroll
-    for (int i = 0; i < MT * kPer; ++i)
-      if (i / kPer < M && i % kPer < per) need |= 1u << i;
+    for (int i = 0; i < MT * kPairs; ++i)
+      if (i / kPairs < M && 2 * (static_cast<int>(threadIdx.x) + (i % kPairs) * kThreads) < I)
+        need |= 1u << i;
     __syncthreads();  // every wavefront is done with the gate_up stage's LDS rows
-    const bool ok = take<MT * kPer>(
-        need, tag, a,
-        [&](int i) { return a.ex2 + (i / kPer) * I + threadIdx.x + (i % kPer) * kThreads; },
-        [&](int i, float val) {
-          const int k = threadIdx.x + (i % kPer) * kThreads;
-          xs[(i / kPer) * I + xoff(k)] = a.dn_inv ? __fmul_rn(val, a.dn_inv[k]) : val;
+    const bool ok = take<MT * kPairs>(
+        replica(a.ex2, s2), need, tag, a,
+        [&](int i) {
+          return ((i / kPairs) * I + 2 * (static_cast<int>(threadIdx.x) + (i % kPairs) * kThreads)) * 8;
+        },
+        [&](int i, float v0, float v1) {
+          const int k = 2 * (static_cast<int>(threadIdx.x) + (i % kPairs) * kThreads);
+          const float2 iv = dn_inv[i % kPairs];
+          *reinterpret_cast<float2*>(xs + (i / kPairs) * I + xoff(k)) =
+              a.dn_inv ? make_float2(__fmul_rn(v0, iv.x), __fmul_rn(v1, iv.y)) : make_float2(v0, v1);
         });
-    // rows M..MT-1 of the staged input are never read into a stored sum; keep them finite
-    if (__syncthreads_or(!ok)) return finish(a);
+    if (block_any(!ok, flags)) return finish(a);
     float v0[MT], v1[MT];
-    chunk_terms<MT>(fd0, lane, xs, I, v0);
-    chunk_terms<MT>(fd1, lane + kWave, xs, I, v1);
+    // each 32-channel chunk's sum: the pairs of 16 consecutive threads (I is a multiple of 512,
+    // so those 16 are all in or all out)
+#pragma unroll
+    for (int i = 0; i < MT * kPairs; ++i) {
+      const int pr = static_cast<int>(threadIdx.x) + (i % kPairs) * kThreads;
+      const bool in = (need >> i) & 1u;
+      float2 v = make_float2(0.f, 0.f);
+      if (in) v = *reinterpret_cast<const float2*>(xs + (i / kPairs) * I + xoff(2 * pr));
+      const float sum = lsh::group_sum<16>(v.x + v.y);
+      if (in && pr % 16 == 0) cs[(i / kPairs) * (I >> 5) + (pr >> 4)] = sum;
+    }
+    __syncthreads();
+    chunk_terms<MT>(fd0, lane, xs, cs, I, v0);
+    chunk_terms<MT>(fd1, lane + kWave, xs, cs, I, v1);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       const float t = lsh::group_total<kWave>(v0[m] + v1[m]);
-      if (m < M && lane == kWave - 1) put(a.ex3 + m * H + orow, t, tag);
+      if (m < M && lane == kWave - 1) put(a.ex3, s1, m * H + orow, t, tag);
     }
   }
 
   // 6. the last layer: x += down, the residual channels 8w..8w+7 and their final norm
   if (a.head_groups == 0) {
-    float dv[2 * MT];
-    const uint32_t need = k0 < H ? low_bits(2 * M) : 0u;
-    const bool ok = take<2 * MT>(
-        need, tag, a, [&](int i) { return a.ex3 + (i / 2) * H + k0 + (i % 2); },
-        [&](int i, float val) { dv[i] = val; });
-    if (__syncthreads_or(!ok)) return finish(a);
+    float dv[MT][2];
+    const bool ok = take<MT>(
+        replica(a.ex3, s1), k0 < H ? low_bits(M) : 0u, tag, a,
+        [&](int m) { return (m * H + k0) * 8; },
+        [&](int m, float v0, float v1) {
+          dv[m][0] = v0;
+          dv[m][1] = v1;
+        });
+    if (block_any(!ok, flags)) return finish(a);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      x.v[m][0] = x.v[m][0] + dv[2 * m];
-      x.v[m][1] = x.v[m][1] + dv[2 * m + 1];
+      x.v[m][0] = x.v[m][0] + dv[m][0];
+      x.v[m][1] = x.v[m][1] + dv[m][1];
     }
     store_rows(x, a.x_out, H, M, 8 * w, 8 * w + 8);
     if (a.h_out) {
       float inv[MT];
       row_inv_rms(x, H, M, a.eps, red, inv);
       if (k0 >= 8 * w && k0 < 8 * w + 8) {
-        const float2 wv = *reinterpret_cast<const float2*>(a.next_w + k0);
 #pragma unroll
         for (int m = 0; m < MT; ++m)
           if (m < M)
             *reinterpret_cast<float2*>(a.h_out + static_cast<int64_t>(m) * H + k0) =
-                make_float2(wv.x * (x.v[m][0] * inv[m]), wv.y * (x.v[m][1] * inv[m]));
+                make_float2(next_w.x * (x.v[m][0] * inv[m]), next_w.y * (x.v[m][1] * inv[m]));
       }
     }
   }
@@ -479,103 +567,138 @@ __device__ void mlp_group(const ChainArgs& a, uint32_t tag, float* lds, float* r
 }
 
 template <int MT>
-__device__ void head_group(const ChainArgs& a, uint32_t tag, float* lds, float* red) {
+__device__ void head_group(const ChainArgs& a, float* xs, float* cs, float* out, float* red,
+                           int* flags) {
   const int hh = blockIdx.x - a.mlp_groups;  // q heads, then k heads, then v heads
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int H = a.H, M = a.M;
   const int half = lane / 32, hl = lane % 32;
   const int k0 = 2 * threadIdx.x;
   constexpr int D = kHeadDim;
-  float* xs = lds;
-  float* out = lds + kMaxRows * kMaxI;  // [D][kMaxRows]
+  const int64_t s1 = static_cast<int64_t>(kMaxRows) * H;
+  const bool is_q = hh < a.nq, is_k = !is_q && hh < a.nq + a.nk;
 
-  // 1. the head's 128 qkv rows (a lane: chunk hl of rows 16 wave + 2 p + half)
+  // 1. the head's 128 qkv rows (a lane: chunk hl of rows 16 wave + 2 p + half), then every
+  //    small vector the later stages need: the norm weight and qkv's inv, and for wavefront
+  //    m < M the position, slot, RoPE row, q/k norm weight and smoothing of sequence m
   Chunk fq[kHeadPasses];
 #pragma unroll
   for (int p = 0; p < kHeadPasses; ++p)
     fq[p] = fetch(a.qkv_nib, a.qkv_s, a.qkv_z, H, static_cast<int64_t>(hh) * D + 16 * wave + 2 * p + half,
                   hl, hl < H / 32);
+  const float2 next_w = chan2(a.next_w, H, 1.f), qkv_inv = chan2(a.qkv_inv, H, 1.f);
+  const int m = wave;  // stage 4: one wavefront per sequence
+  int64_t pos = -1, slot = -1;
+  float cosv[2] = {0.f, 0.f}, sn[2] = {0.f, 0.f}, nw[2] = {1.f, 1.f}, sm[2] = {1.f, 1.f};
+  const float* nwp = is_q ? a.q_w : (is_k ? a.k_w : nullptr);
+  const int kvh = is_k ? hh - a.nq : hh - a.nq - a.nk;
+  if (m < M) {
+    pos = a.ctx[m] - 1;
+    if (pos >= 0 && pos < a.max_pos && pos / a.bs < a.max_blocks) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        cosv[i] = a.cos_t[pos * D + lane + i * kWave];
+        sn[i] = a.sin_t[pos * D + lane + i * kWave];
+        if (nwp) nw[i] = nwp[lane + i * kWave];
+        if (is_k && a.smooth) sm[i] = a.smooth[static_cast<int64_t>(kvh) * D + lane + i * kWave];
+      }
+      if (!is_q) {
+        const int64_t blk = a.bt[m * a.max_blocks + pos / a.bs];
+        slot = blk * a.bs + pos % a.bs;
+        if (blk < 0 || slot >= a.num_slots) slot = -1;
+      }
+    } else {
+      pos = -1;
+    }
+  }
+  const uint32_t tag = launch_tag(a);
   // 2. the residual rows: (x + o) + down, or the embedding rows
   Resid<MT> x;
   if (a.mlp_groups == 0) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const int64_t id = m < M ? a.ids[m] : 0;
+    for (int r = 0; r < MT; ++r) {
+      const int64_t id = r < M ? a.ids[r] : 0;
       float2 v = make_float2(0.f, 0.f);
-      if (m < M && k0 < H)
+      if (r < M && k0 < H)
         v = (id >= 0 && id < a.vocab) ? *reinterpret_cast<const float2*>(a.embed + id * H + k0)
                                       : make_float2(__builtin_nanf(""), __builtin_nanf(""));
-      x.v[m][0] = v.x;
-      x.v[m][1] = v.y;
+      x.v[r][0] = v.x;
+      x.v[r][1] = v.y;
     }
   } else {
     load_rows(a.x_in, H, M, x);
-    // words [0, 2 MT): down (m, c) -- the last hand-off, polled first; [2 MT, 4 MT): o (m, c)
-    float od[4 * MT];
-    const uint32_t rows_mask = low_bits(2 * M);
-    const uint32_t need = k0 < H ? (rows_mask | (rows_mask << (2 * MT))) : 0u;
-    const bool ok = take<4 * MT>(
-        need, tag, a,
-        [&](int i) {
-          const int j = i % (2 * MT);
-          return (i < 2 * MT ? a.ex3 : a.ex1) + (j / 2) * H + k0 + (j % 2);
-        },
-        [&](int i, float val) { od[i] = val; });
-    if (__syncthreads_or(!ok)) return finish(a);
+    float dv[MT][2], ov[MT][2];
+    // o_proj's hand-off completes long before down_proj's: it is taken first, while down_proj
+    // still runs (taken second, it would add a poll round trip after the last hand-off)
+    bool ok = take<MT>(
+        replica(a.ex1, s1), k0 < H ? low_bits(M) : 0u, tag, a,
+        [&](int r) { return (r * H + k0) * 8; },
+        [&](int r, float v0, float v1) {
+          ov[r][0] = v0;
+          ov[r][1] = v1;
+        });
+    ok = ok && take<MT>(
+        replica(a.ex3, s1), k0 < H ? low_bits(M) : 0u, tag, a,
+        [&](int r) { return (r * H + k0) * 8; },
+        [&](int r, float v0, float v1) {
+          dv[r][0] = v0;
+          dv[r][1] = v1;
+        });
+    if (block_any(!ok, flags)) return finish(a);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      x.v[m][0] = (x.v[m][0] + od[2 * MT + 2 * m]) + od[2 * m];
-      x.v[m][1] = (x.v[m][1] + od[2 * MT + 2 * m + 1]) + od[2 * m + 1];
+    for (int r = 0; r < MT; ++r) {
+      x.v[r][0] = (x.v[r][0] + ov[r][0]) + dv[r][0];
+      x.v[r][1] = (x.v[r][1] + ov[r][1]) + dv[r][1];
     }
   }
-  {  // this group's share of the new residual channels
-    const int share = H / a.head_groups;
-    store_rows(x, a.x_out, H, M, hh * share, (hh + 1) * share);
-  }
-
   // 3. the next layer's input norm times qkv's inv -> LDS, then the head's 128 rows
-  norm_to_lds(x, a.next_w, a.qkv_inv, a.eps, H, M, xs, red);
+  norm_to_lds(x, next_w, qkv_inv, a.qkv_inv != nullptr, a.eps, H, M, xs, cs, red);
   __syncthreads();
 #pragma unroll
   for (int p = 0; p < kHeadPasses; ++p) {
     float v[MT];
-    chunk_terms<MT>(fq[p], hl, xs, H, v);
+    chunk_terms<MT>(fq[p], hl, xs, cs, H, v);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float t = lsh::group_total<32>(v[m]);
-      if (hl == 31) out[(16 * wave + 2 * p + half) * kMaxRows + m] = t;
+    for (int r = 0; r < MT; ++r) {
+      const float t = lsh::group_total<32>(v[r]);
+      if (hl == 31) out[(16 * wave + 2 * p + half) * MT + r] = t;
     }
   }
   __syncthreads();
 
-  // 4. one wavefront per sequence: q/k norm + RoPE at position ctx - 1, then q out or the
-  //    int8 cache write (the quantizer of llmserve_kv_quantize_write)
-  const int m = wave;
+  // 4. one wavefront per sequence: q/k norm + RoPE at position ctx - 1 (norm_rope's
+  //    arithmetic on the prefetched rows), then q out or the int8 cache write (the quantizer
+  //    of llmserve_kv_quantize_write)
   if (m < M) {
     float v[2];
-    v[0] = out[lane * kMaxRows + m];
-    v[1] = out[(lane + kWave) * kMaxRows + m];
-    const int64_t pos = a.ctx[m] - 1;
-    const bool ok = pos >= 0 && pos < a.max_pos && pos / a.bs < a.max_blocks;
-    const bool is_q = hh < a.nq, is_k = !is_q && hh < a.nq + a.nk;
-    if (ok) {
-      if (is_q || is_k)
-        lsh::norm_rope(v, is_q ? a.q_w : a.k_w, a.cos_t + pos * D, a.sin_t + pos * D, D, a.eps);
+    v[0] = out[lane * MT + m];
+    v[1] = out[(lane + kWave) * MT + m];
+    if (pos >= 0) {
+      if (is_q || is_k) {
+        if (nwp) {
+          const float ss = lsh::wave_sum_from<1>(v[0] * v[0] + v[1] * v[1]);
+          const float inv = 1.f / sqrtf(ss / static_cast<float>(D) + a.eps);
+          v[0] = nw[0] * (v[0] * inv);
+          v[1] = nw[1] * (v[1] * inv);
+        }
+        // rotate_half: element d < D/2 pairs with d + D/2, the other register of the lane
+        const float r0 = v[0] * cosv[0] - v[1] * sn[0];
+        const float r1 = v[1] * cosv[1] + v[0] * sn[1];
+        v[0] = r0;
+        v[1] = r1;
+      }
       if (is_q) {
         float* o = a.q_out + (static_cast<int64_t>(m) * a.nq + hh) * D;
         o[lane] = v[0];
         o[lane + kWave] = v[1];
-      } else {
-        const int64_t blk = a.bt[m * a.max_blocks + pos / a.bs];
-        const int64_t slot = blk * a.bs + pos % a.bs;
-        if (blk >= 0 && slot < a.num_slots) {
-          const int h = is_k ? hh - a.nq : hh - a.nq - a.nk;
-          const int64_t at = slot * a.nk + h;
-          if (is_k)
-            lsh::kv_quant_row(v, a.smooth ? a.smooth + static_cast<int64_t>(h) * D : nullptr, D,
-                              a.kc + at * D, a.ks + at);
-          else
-            lsh::kv_quant_row(v, nullptr, D, a.vc + at * D, a.vs + at);
+      } else if (slot >= 0) {
+        const int64_t at = slot * a.nk + kvh;
+        if (is_k) {
+          float u[2] = {v[0], v[1]};
+          lsh::kv_quant_row_smoothed(u, sm, a.smooth != nullptr, a.kc + at * D, a.ks + at);
+        } else {
+          float u[2] = {v[0], v[1]};
+          lsh::kv_quant_row_smoothed(u, sm, false, a.vc + at * D, a.vs + at);
         }
       }
     } else if (is_q) {  // a position outside the tables: a NaN q, visible in the logits
@@ -584,19 +707,26 @@ __device__ void head_group(const ChainArgs& a, uint32_t tag, float* lds, float* 
       o[lane + kWave] = __builtin_nanf("");
     }
   }
+  {  // this group's share of the new residual channels, stored last: a later wait on loads
+     // (vmcnt counts stores too) would otherwise also wait for this store
+    const int share = H / a.head_groups;
+    store_rows(x, a.x_out, H, M, hh * share, (hh + 1) * share);
+  }
   finish(a);
 }
 
 template <int MT>
 __global__ __launch_bounds__(kThreads) void decode_chain_kernel(ChainArgs a) {
-  // staged rows ([MT][K] floats, K up to kMaxI) and after them a stage's row results
-  __shared__ __align__(16) float lds[kMaxRows * kMaxI + kHeadDim * kMaxRows];
+  // staged rows ([MT][K] floats, K up to kMaxI) and a stage's row results
+  __shared__ __align__(16) float xs[MT * kMaxI];
+  __shared__ float cs[MT * kMaxI / 32];  // the staged rows' 32-channel chunk sums
+  __shared__ __align__(16) float rows[kHeadDim * MT];
   __shared__ float red[kWaves];
-  const uint32_t tag = __hip_atomic_load(a.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  __shared__ int flags[kWaves];
   if (static_cast<int>(blockIdx.x) < a.mlp_groups)
-    mlp_group<MT>(a, tag, lds, red);
+    mlp_group<MT>(a, xs, cs, rows, red, flags);
   else
-    head_group<MT>(a, tag, lds, red);
+    head_group<MT>(a, xs, cs, rows, red, flags);
 }
 
 template <int MT>
@@ -621,7 +751,7 @@ int launch_chain(const ChainArgs& a, int grid, hipStream_t st) {
 
 extern "C" int64_t llmserve_decode_chain_workspace_bytes(int64_t H, int64_t I) {
   if (H <= 0 || I <= 0) return 0;
-  return 256 + static_cast<int64_t>(kMaxRows) * (2 * H + I) * 8;
+  return 256 + static_cast<int64_t>(kCopies) * kMaxRows * (2 * H + I) * 8;
 }
 
 extern "C" int llmserve_decode_chain(
@@ -729,9 +859,9 @@ extern "C" int llmserve_decode_chain(
   a.vs = v_scale;
   char* ws = static_cast<char*>(workspace);
   a.ctl = reinterpret_cast<uint32_t*>(ws);
-  a.ex1 = reinterpret_cast<uint64_t*>(ws + 256);
-  a.ex2 = a.ex1 + kMaxRows * H;
-  a.ex3 = a.ex2 + kMaxRows * I;
+  a.ex1 = reinterpret_cast<uint64_t*>(ws + 256);  // kCopies replicas of each
+  a.ex2 = a.ex1 + static_cast<int64_t>(kCopies) * kMaxRows * H;
+  a.ex3 = a.ex2 + static_cast<int64_t>(kCopies) * kMaxRows * I;
   a.spin_limit = static_cast<uint32_t>(spin_limit < 0 ? 0 : (spin_limit > 0x7fffffff ? 0x7fffffff : spin_limit));
   a.M = static_cast<int>(M);
   a.H = static_cast<int>(H);
@@ -742,7 +872,8 @@ extern "C" int llmserve_decode_chain(
   a.mlp_groups = static_cast<int>(mlp_groups);
   a.head_groups = next ? static_cast<int>(n_q + 2 * n_k) : 0;
   a.eps = eps;
-  const int grid = a.mlp_groups + a.head_groups;
+  a.grid = a.mlp_groups + a.head_groups;
+  const int grid = a.grid;
   hipStream_t st = lsh::as_stream(stream);
   switch (M) {
     case 1: return launch_chain<1>(a, grid, st);

@@ -4,8 +4,8 @@
 // Work line: the kv heads form NHG groups of HB heads (HB = the largest divisor of Hk up to
 // 8). The (sequence b, head group hg, token t) triples, t fastest, laid end to end make a line
 // of T = NHG * sum_b ctx_b. The line is cut into ranges of Q tokens (Q = ceil(T / W) over the
-// W resident workgroups, so every SIMD streams the same number of cache rows whatever the
-// context lengths; or a caller-fixed Q). A workgroup holds HB wavefronts, one per kv head of
+// W resident workgroups, but at least 64, so every SIMD streams the same number of cache rows
+// whatever the context lengths; or a caller-fixed Q). A workgroup holds HB wavefronts, one per kv head of
 // the group, which run the same tokens: together they read whole HB * D-byte pieces of every
 // slot row (all of it when HB = Hk), so the cache streams in long contiguous runs. A workgroup
 // runs its range as segments, one per (b, hg) the range touches. A segment that covers its
@@ -104,7 +104,7 @@ struct DecodeArgs {
   float* part_ml;   // [slots, G, 2]  (running max in log2 units, sum)
   float* part_acc;  // [slots, G, D]
   int64_t num_slots;
-  int64_t range;  // token-heads per work range; 0: ceil(T / W)
+  int64_t range;  // token-heads per work range; 0: max(ceil(T / W), kMinRange)
   int B, Hq, Hk, max_blocks, bs, bs_shift;  // bs_shift = log2(bs), or -1
   int HB, NHG;  // kv heads per workgroup, head groups (Hk = HB * NHG)
   int W;        // decode workgroups (all resident)
@@ -147,6 +147,17 @@ __device__ int64_t tokens_before(const DecodeArgs& a, int bend) {
   return uniform64(s);
 }
 
+// Token-heads per work range over a line of T: the caller's size, else an equal share per
+// resident workgroup but at least kMinRange. A shorter range is one round of loads whose
+// latency the split cannot hide, and it only adds partials to merge: at one sequence of 2048
+// tokens, 8-token ranges (the plain share over 256 workgroups) take 32 us, 64-token ones 17 us.
+constexpr int64_t kMinRange = 64;
+__device__ __forceinline__ int64_t range_len(const DecodeArgs& a, int64_t T) {
+  if (a.range > 0) return a.range;
+  const int64_t q = (T + a.W - 1) / a.W;
+  return q > kMinRange ? q : kMinRange;
+}
+
 // Work-range geometry shared by the decode and merge kernels.
 struct Ranges {
   int64_t T, Q, R;  // token-heads, token-heads per range, ranges
@@ -155,8 +166,7 @@ struct Ranges {
 __device__ __forceinline__ Ranges work_ranges(const DecodeArgs& a) {
   Ranges g;
   g.T = tokens_before(a, a.B) * a.NHG;
-  g.Q = a.range > 0 ? a.range : (g.T + a.W - 1) / a.W;
-  if (g.Q < 1) g.Q = 1;
+  g.Q = range_len(a, g.T);
   g.R = (g.T + g.Q - 1) / g.Q;
   return g;
 }
@@ -626,8 +636,7 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_kernel
     return;
   }
   const int64_t T = tot * a.NHG;
-  int64_t Q = a.range > 0 ? a.range : (T + a.W - 1) / a.W;
-  if (Q < 1) Q = 1;
+  const int64_t Q = range_len(a, T);
   const int hg = h / a.HB;
   const int64_t g0 = pre * a.NHG + hg * ctx;
   const int64_t j0 = g0 / Q, j1 = (g0 + ctx - 1) / Q;
@@ -691,8 +700,7 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_frag_k
     pre = uniform64(wave_sum_i64(pre));
     const int64_t ctx = uniform64(wave_sum_i64(cb));
     const int64_t T = tot * a.NHG;
-    int64_t Q = a.range > 0 ? a.range : (T + a.W - 1) / a.W;
-    if (Q < 1) Q = 1;
+    const int64_t Q = range_len(a, T);
     const int hg = h / a.HB;
     const int64_t g0 = pre * a.NHG + hg * ctx;
     const int64_t j0 = ctx > 0 ? g0 / Q : 0, j1 = ctx > 0 ? (g0 + ctx - 1) / Q : 0;

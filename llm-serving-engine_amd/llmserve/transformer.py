@@ -165,10 +165,14 @@ class QuantCausalLM(nn.Module):
     # (lm_head_f32_xfrag, within a few 1e-6 of fp32) instead of torch.mm (hipBLASLt).
     fp32_head_kernel = True
 
-    # Up to 4 rows the step runs one persistent launch per layer for the whole linear chain
-    # (o_proj .. next qkv, with the norms, silu * up, RoPE and the cache write:
-    # llmserve_decode_chain) instead of a launch per op.
+    # Up to chain_max_rows rows the step runs one persistent launch per layer for the whole
+    # linear chain (o_proj .. next qkv, with the norms, silu * up, RoPE and the cache write:
+    # llmserve_decode_chain) instead of a launch per op. The kernel takes up to 4 rows, but its
+    # dot products run on ~160 CUs' VALUs, so its time grows with the rows: per Qwen3-0.6B
+    # layer on MI355X, 19.5 us against 24.9 us per-op at 1 row, 26.2 / 27.5 at 2 and
+    # 40.5 / 31.7 at 4.
     use_chain = True
+    chain_max_rows = 2
     chain_spin_limit = 1 << 22  # polls per hand-off wait before the chain gives up
 
     def _chain_ok(self, rows: int) -> bool:
@@ -324,7 +328,7 @@ class QuantCausalLM(nn.Module):
         position is ctx - 1); ``block_tables`` [B, max_blocks] int64 holds the blocks of every
         position up to ctx - 1; ``kv_layers`` is ``KVCache.layers`` with int8 ``QuantizedKV``
         pairs. Writes this token's K and V into the caches. No host synchronization."""
-        if self._chain_ok(ids.numel()):
+        if self._chain_ok(ids.numel()) and ids.numel() <= self.chain_max_rows:
             return self._forward_decode_chain(ids, context_lens, block_tables, kv_layers,
                                               block_size)
         cfg = self.cfg

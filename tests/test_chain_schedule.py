@@ -4,9 +4,10 @@ decode_chain.hip), run before the kernel ever runs on a GPU.
 The kernel's workgroups are restated as Python generators that perform the same sequence of
 hand-off operations with the same index formulas: MLP group w puts o_proj rows 8w..8w+7 into
 ex1, takes all of ex1, puts silu * up channels [C w, C (w + 1)) into ex2, takes all of ex2, puts
-down rows 8w..8w+7 into ex3 and (last layer) takes all of ex3; a head group takes all of ex3 and
-ex1; every group then counts itself finished and the last one advances the tag base. A word is
-(tag, value); a take completes only when every word it needs carries the launch's tag.
+down rows 8w..8w+7 into ex3 and (last layer) takes all of ex3; a head group takes all of ex1,
+then all of ex3; every group then counts itself finished and the last one advances the tag
+base. A word is (tag, value); a take completes only when every word it needs carries the
+launch's tag.
 
 Checked, under many random interleavings (including workgroups that start late, and several
 launches in a row on one workspace): no schedule deadlocks while all groups are resident; every
@@ -23,12 +24,18 @@ import random
 import pytest
 
 WAVES = 8
+COPIES = 8  # each hand-off vector is written in 8 replicas; group g reads replica g % 8
 
 
 class Workspace:
     def __init__(self, H, I, rows=4):
-        self.ex = {1: [(0, None)] * (rows * H), 2: [(0, None)] * (rows * I), 3: [(0, None)] * (rows * H)}
+        n = {1: rows * H, 2: rows * I, 3: rows * H}
+        self.ex = {b: [[(0, None)] * n[b] for _ in range(COPIES)] for b in n}
         self.ctl = [0, 0, 0]  # tag base, finished groups, error
+
+    def put(self, buf, idx, word):
+        for c in range(COPIES):
+            self.ex[buf][c][idx] = word
 
 
 def tag_of(ctl0: int) -> int:
@@ -45,21 +52,21 @@ def mlp_group(ws, w, M, H, I, groups, last, launch, log):
     yield
     for wave in range(WAVES):
         for m in range(M):
-            ws.ex[1][m * H + 8 * w + wave] = (tag, ("o", launch, m, 8 * w + wave))
+            ws.put(1, m * H + 8 * w + wave, (tag, ("o", launch, m, 8 * w + wave)))
     got = yield ("take", 1, [m * H + k for m in range(M) for k in range(H)])
     if got is None:
         return
     log.append(("ex1", w, got))
     for m in range(M):
         for j in range(C):
-            ws.ex[2][m * I + C * w + j] = (tag, ("a", launch, m, C * w + j))
+            ws.put(2, m * I + C * w + j, (tag, ("a", launch, m, C * w + j)))
     got = yield ("take", 2, [m * I + k for m in range(M) for k in range(I)])
     if got is None:
         return
     log.append(("ex2", w, got))
     for wave in range(WAVES):
         for m in range(M):
-            ws.ex[3][m * H + 8 * w + wave] = (tag, ("d", launch, m, 8 * w + wave))
+            ws.put(3, m * H + 8 * w + wave, (tag, ("d", launch, m, 8 * w + wave)))
     if last:
         got = yield ("take", 3, [m * H + k for m in range(M) for k in range(H)])
         if got is None:
@@ -71,14 +78,14 @@ def head_group(ws, hh, M, H, mlp, launch, log):
     tag = tag_of(ws.ctl[0])
     yield
     if mlp:
-        got = yield ("take", 3, [m * H + k for m in range(M) for k in range(H)])
-        if got is None:
-            return
-        log.append(("ex3h", hh, got))
         got = yield ("take", 1, [m * H + k for m in range(M) for k in range(H)])
         if got is None:
             return
         log.append(("ex1h", hh, got))
+        got = yield ("take", 3, [m * H + k for m in range(M) for k in range(H)])
+        if got is None:
+            return
+        log.append(("ex3h", hh, got))
 
 
 def run_launch(ws, H, I, M, heads, mlp, last, launch, rng, spin_limit=10**9, dead=None,
@@ -86,6 +93,7 @@ def run_launch(ws, H, I, M, heads, mlp, last, launch, rng, spin_limit=10**9, dea
     """Runs one launch to completion with a random interleaving; returns the take log."""
     groups = H // 8 if mlp else 0
     log = []
+    # the workgroup index of each generator (MLP groups first, then head groups)
     gens = []
     for w in range(groups):
         gens.append(("mlp", w, mlp_group(ws, w, M, H, I, groups, last, launch, log)))
@@ -120,7 +128,8 @@ def run_launch(ws, H, I, M, heads, mlp, last, launch, rng, spin_limit=10**9, dea
                 s["req"] = g.send(None)
                 continue
             _, buf, idx = req
-            words = [ws.ex[buf][j] for j in idx]
+            copy = i % COPIES  # the generator index is the workgroup index
+            words = [ws.ex[buf][copy][j] for j in idx]
             if all(t == tag_at_start[i] for t, _ in words):
                 s["spins"] = 0
                 s["req"] = g.send([v for _, v in words])

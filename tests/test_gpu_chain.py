@@ -7,8 +7,9 @@ chain computes the same float32 operations in other summation orders, so logits 
 2e-5 of max|logits| (the tolerance of the GEMV step against the oracle; 2e-3 for two-layer
 models, see the test) and the int8 K/V rows
 it writes are within one quantization step (under 1% of values) at the same slots, every other
-slot unchanged. The step oracle comparison of tests/test_gpu_step.py runs the chain as well
-(its 2- and 4-row cases). Graph replays of chain steps are bit-identical to eager ones. A
+slot unchanged. These tests raise the model's chain_max_rows to the kernel's 4; the step
+oracle comparison of tests/test_gpu_step.py runs the chain at the default policy (its 1- and
+2-row cases) and the per-op step above it. Graph replays of chain steps are bit-identical to eager ones. A
 chain whose hand-off waits are given no poll budget gives up, sets its error word and the
 grid finishes; the next launch on the workspace is correct.
 """
@@ -41,6 +42,7 @@ def qwen_like_cfg(layers=2):
 def _step_both(cfg, ctx, seed):
     """(chain run, per-op run) of one step from the same state: logits, ids, caches."""
     model, cache, runner, host, ids, ctx, bt = setup(cfg, ctx, seed)
+    model.chain_max_rows = 4  # the kernel's limit (the default policy stops at 2 rows)
     assert model._chain_ok(len(ids))
     start = runner.snapshot()
     out = []
@@ -94,6 +96,7 @@ def test_chain_step_matches_per_op_step(gpu, cfg_fn, ctx, tol):
 def test_chain_graph_replays_equal_eager(gpu):
     cfg = tiny_cfg()
     _, cache, runner, _, _, _, _ = setup(cfg, [30, 150, 77], 23, extra=8)
+    runner.model.chain_max_rows = 4
     assert runner.model._chain_ok(3)
     start = runner.snapshot()
     eager = []

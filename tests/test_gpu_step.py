@@ -113,7 +113,8 @@ def check_step(cfg, model, cache, runner, host, ids, ctx, bt):
 @pytest.mark.parametrize("ctx,lm_int4,smooth", [
     ([1, 16, 17, 300, 77], False, True),     # 5 rows: the matrix-core linears
     ([1, 16, 17, 300], True, False),         # 4 rows: the GEMV linears, int4 LM head
-    ([9, 300], False, True),                 # 2 rows
+    ([9, 300], False, True),                 # 2 rows: the decode chain
+    ([700], True, True),                     # 1 row: the decode chain
     (list(range(20, 500, 20)), False, True),  # 24 rows: the matrix-core linears
     (list(range(20, 500, 20)), True, True),
 ])
