@@ -147,9 +147,9 @@ int llmserve_int4_gemm_pack(const uint8_t* nibbles, const float* g_scale, const 
 
 /*
  * Int4Linear's batched path (replaces quant.py:141-142 like llmserve_int4_linear_gemm) on a
- * packed weight: the same arithmetic (x' = x * inv_act_scale split into bf16 hi / lo, exact
- * bf16 products, fp32 accumulation; within a few 1e-6 relative of fp32) with the decode-batch
- * kernel, whose wavefronts issue all loads of their 1-3 K blocks before the first product.
+ * packed weight: x' = x * inv_act_scale split into three bf16 pieces (hi + mid + lo equals x'
+ * to ~2^-26 relative), exact bf16 products, fp32 accumulation, so the result is that of fp32
+ * arithmetic up to summation order, with the decode-batch kernel, whose wavefronts issue all loads of their 1-3 K blocks before the first product.
  * Any M, N >= 1; K and group_size multiples of 128. x, inv_act_scale and the packed weight
  * 16-byte aligned; `workspace` (16-byte aligned) holds
  * llmserve_int4_linear_gemm_packed_workspace_bytes(M, K) bytes.
@@ -161,8 +161,8 @@ int llmserve_int4_linear_gemm_packed(const float* x, const float* inv_act_scale 
                                      int64_t workspace_bytes, void* stream);
 
 /*
- * Activation fragments: x' = x * inv_act_scale as the packed kernel reads it (bf16 hi / lo
- * pieces in wavefront order, then fp32 sums of x' over every 128-channel block; rows up to M
+ * Activation fragments: x' = x * inv_act_scale as the packed kernel reads it (bf16 hi / mid /
+ * lo pieces in wavefront order, then fp32 sums of x' over every 128-channel block; rows up to M
  * rounded to 16, the extra rows zero). llmserve_int4_xfrag_bytes(M, K) bytes, 16-byte aligned.
  * Written by llmserve_int4_linear_gemm_packed's own split pass or by the fused producers
  * below (bit-identical for the same x'); read by llmserve_int4_linear_gemm_xfrag, which is
@@ -288,9 +288,9 @@ int llmserve_argmax_advance(const float* logits, int64_t T, int64_t V, int64_t* 
  * fp32 LM head on activation fragments (replaces the tied-embedding lm_head,
  * models/transformer.py:192-193): y[M, V] = x[M, K] . w[V, K]^T with w fp32 row-major and x
  * given as llmserve_int4_xfrag_bytes(M, K) bytes of fragments (written, e.g., by
- * llmserve_add_rmsnorm_xfrag with act_inv = NULL). Split-bf16 matrix-core products (x and w
- * each as bf16 hi + lo, four products, fp32 accumulation): within a few 1e-6 relative of
- * fp32. K a multiple of 128; xfrag, w and y 16-byte aligned.
+ * llmserve_add_rmsnorm_xfrag with act_inv = NULL). Split-bf16 matrix-core products (the hi and
+ * mid pieces of x, w as bf16 hi + lo, four products, fp32 accumulation): within a few 1e-6
+ * relative of fp32. K a multiple of 128; xfrag, w and y 16-byte aligned.
  */
 int llmserve_lm_head_f32_xfrag(const void* xfrag, const float* w, float* y, int64_t M, int64_t V,
                                int64_t K, void* stream);

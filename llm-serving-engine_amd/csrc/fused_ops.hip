@@ -86,7 +86,7 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_kernel(const float* __re
 // The norms above with the int4 linear's activation fragments as output (xfrag.h): the
 // first pass is rmsnorm_kernel's (same x update, same sum of squares, same inv); the second
 // computes h = w * (x * inv) as rmsnorm_kernel does, x' = h * act_inv (the next linear's AWQ
-// pre-scale, or h) and writes x' as bf16 hi / lo fragments and block sums, with 4 consecutive
+// pre-scale, or h) and writes x' as bf16 hi / mid / lo fragments and block sums, with 4 consecutive
 // channels per thread (32 threads per 128-channel block). One workgroup per fragment row:
 // rows past T write zeros. H is a multiple of 128.
 template <int MODE>
@@ -491,7 +491,7 @@ int launch_norm_frag(int mode, float* x, const float* r, const int64_t* ids, int
   LSH_CHECK(lsh::aligned16(xfrag), "%s: the fragment buffer must be 16-byte aligned", what);
   const int mp = static_cast<int>(lsh::frag_rows(T));
   __bf16* xf = static_cast<__bf16*>(xfrag);
-  float* xsum = reinterpret_cast<float*>(xf + 2 * static_cast<int64_t>(mp) * H);
+  float* xsum = lsh::frag_sums(xf, mp, H);
   const dim3 grid(static_cast<unsigned>(mp)), block(kRowThreads);
   hipStream_t st = lsh::as_stream(stream);
   const int Ti = static_cast<int>(T), Hi = static_cast<int>(H);
@@ -547,7 +547,7 @@ extern "C" int llmserve_silu_mul_xfrag(const float* gate_up, const float* act_in
   LSH_CHECK(lsh::aligned16(xfrag), "silu_mul_xfrag: the fragment buffer must be 16-byte aligned");
   const int mp = static_cast<int>(lsh::frag_rows(T));
   __bf16* xf = static_cast<__bf16*>(xfrag);
-  float* xsum = reinterpret_cast<float*>(xf + 2 * static_cast<int64_t>(mp) * I);
+  float* xsum = lsh::frag_sums(xf, mp, I);
   const int64_t items = static_cast<int64_t>(mp) * (I / lsh::kFragBlk);
   const int wpb = kRowThreads / kWave;
   lsh::launch(silu_mul_frag_kernel, dim3(static_cast<unsigned>((items + wpb - 1) / wpb)),

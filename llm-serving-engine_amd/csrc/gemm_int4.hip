@@ -6,7 +6,8 @@
 // so the matrix cores multiply only exact operands:
 //  * q in [0, 15] is exact in bf16;
 //  * x' = x * inv (fp32, rounded as the reference's separate multiply) is split by a pre-pass
-//    into bf16 xh = bf16(x') and xl = bf16(x' - xh): xh + xl equals x' to 2^-18 relative;
+//    into bf16 xh = bf16(x') and xl = bf16(x' - xh): xh + xl equals x' to 2^-17 relative
+//    (the decode-batch kernel int4_gemm_lat below reads three pieces, xfrag.h: fp32-faithful);
 //  * every product of two bf16 values is exact in fp32, and v_mfma_f32_16x16x32_bf16 adds
 //    them in fp32. The result is within a few 1e-6 (relative) of fp32 arithmetic.
 // The pre-pass also writes the channel sums of x' over every 128-channel block (the
@@ -237,8 +238,8 @@ __global__ __launch_bounds__(256) void int4_gemm_mfma(Int4GemmArgs a) {
 //  * scales:  [group][slab][fr][8 floats]: s of the rows 64 slab + 16 u + fr (u = 0..3), then
 //    z - 8 s of the same rows (the constant term of the group decomposition, rounded as the
 //    kernel would round it);
-//  * x:       [row tile][block][step q][hi, lo][lane][8 bf16]: lane (fr, fc) holds row
-//    16 t + fr (zero past M), channels 128 b + 32 fc + 8 q .. + 8, of xh and of xl.
+//  * x:       [row tile][block][step q][hi, mid, lo][lane][8 bf16] (xfrag.h): lane (fr, fc)
+//    holds row 16 t + fr (zero past M), channels 128 b + 32 fc + 8 q .. + 8, of each piece.
 constexpr int kPkTile = kWave * 16;           // bytes of one nibble tile (4 per slab and block)
 constexpr int kPkFrag = kWave * 8;            // bf16 of one x fragment
 
@@ -286,7 +287,7 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const float* __restric
   o[4 + u] = zz;
 }
 
-// x' = x * inv split into bf16 hi / lo fragments (xfrag.h) and xsum[b, m]. One workgroup
+// x' = x * inv split into bf16 hi / mid / lo fragments (xfrag.h) and xsum[b, m]. One workgroup
 // per (row tile, block): thread (row fr, segment s) handles channels 8 s .. + 8 of row
 // 16 t + fr; rows past M are zeros. xsum is the pairwise tree of the block's 128 channels.
 __global__ __launch_bounds__(256) void x_split_frag_kernel(
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
   for (int u = 0; u < kNT; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
   // Rounds of S x KB blocks (one round up to K = 3072 at S = 8, KB = 3).
   for (int base = 0; base < nblk; base += S * KB) {
-    u32x4 w[KB][kNT], xh[KB][4], xl[KB][4];
+    u32x4 w[KB][kNT], xh[KB][4], xm[KB][4], xl[KB][4];
     f32x4 xs[KB];
     float sc[KB][kNT], zc[KB][kNT];
 #pragma unroll
@@ -362,11 +363,13 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
 #pragma unroll
       for (int u = 0; u < kNT; ++u)
         w[kb][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wt + u * kPkTile));
-      const __bf16* xt = a.xh + ((static_cast<int64_t>(t) * nblk + b) * 8) * kPkFrag + 8 * lane;
+      constexpr int P = lsh::kFragPieces;
+      const __bf16* xt = a.xh + ((static_cast<int64_t>(t) * nblk + b) * 4 * P) * kPkFrag + 8 * lane;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        xh[kb][q] = *reinterpret_cast<const u32x4*>(xt + (2 * q) * kPkFrag);
-        xl[kb][q] = *reinterpret_cast<const u32x4*>(xt + (2 * q + 1) * kPkFrag);
+        xh[kb][q] = *reinterpret_cast<const u32x4*>(xt + (P * q) * kPkFrag);
+        xm[kb][q] = *reinterpret_cast<const u32x4*>(xt + (P * q + 1) * kPkFrag);
+        xl[kb][q] = *reinterpret_cast<const u32x4*>(xt + (P * q + 2) * kPkFrag);
       }
       const float* st = a.s + ((static_cast<int64_t>(g) * slabs + slab) * 16 + fr) * 8;
       const f32x4 s4 = *reinterpret_cast<const f32x4*>(st);
@@ -393,6 +396,7 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
         for (int q = 0; q < 4; ++q) {
           const bf16x8 bq = nibbles_bf16(w[kb][u][q]);
           d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xh[kb][q]), bq, d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xm[kb][q]), bq, d, 0, 0, 0);
           d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xl[kb][q]), bq, d, 0, 0, 0);
         }
         const float s1 = on * sc[kb][u];
@@ -593,7 +597,7 @@ extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv
   const int64_t mtiles = (M + kRows - 1) / kRows;
   const int mp = static_cast<int>(xsum_rows(M));
   __bf16* xf = static_cast<__bf16*>(workspace);
-  float* xsum = reinterpret_cast<float*>(xf + 2 * static_cast<int64_t>(mp) * K);
+  float* xsum = lsh::frag_sums(xf, mp, K);
   lsh::launch(x_split_frag_kernel, dim3(static_cast<unsigned>(mtiles * nb)), dim3(256), 0, st, false,
               x, inv_act_scale, xf, xsum, static_cast<int>(M), static_cast<int>(K), mp);
   const uint8_t* wpk = static_cast<const uint8_t*>(packed);
@@ -622,7 +626,7 @@ extern "C" int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* pa
   const int64_t mtiles = (M + kRows - 1) / kRows;
   const int mp = static_cast<int>(lsh::frag_rows(M));
   const __bf16* xf = static_cast<const __bf16*>(xfrag);
-  const float* xsum = reinterpret_cast<const float*>(xf + 2 * static_cast<int64_t>(mp) * K);
+  const float* xsum = lsh::frag_sums(xf, mp, K);
   const uint8_t* wpk = static_cast<const uint8_t*>(packed);
   const float* spk = reinterpret_cast<const float*>(wpk + (pk_weight_bytes(N, K) + 255) / 256 * 256);
   Int4GemmArgs a{xf, nullptr, xsum, wpk, spk, nullptr, y, static_cast<int>(M),

@@ -1,9 +1,11 @@
 // fp32 LM head of the decode step on activation fragments (replaces the tied-embedding
 // lm_head of models/transformer.py:192-193, F.linear(h, embed.weight)):
 //   y[m, v] = sum_k x[m, k] * W[v, k]      W fp32 [V, K] row-major (the embedding matrix)
-// x arrives as the bf16 hi / lo fragments of xfrag.h (x = xh + xl to 2^-16 relative); each W
-// value is split the same way in registers (W = wh + wl), and the four products
-// wh*xh + wh*xl + wl*xh + wl*xl go through v_mfma_f32_16x16x32_bf16 (each product of two bf16
+// x arrives as the bf16 fragments of xfrag.h, of which this kernel reads the hi and mid pieces
+// (x = xh + xm to 2^-17 relative: the head is the last operation of the step, where that
+// error is not amplified by later layers); each W value is split the same way in registers
+// (W = wh + wl), and the four products
+// wh*xh + wh*xm + wl*xh + wl*xm go through v_mfma_f32_16x16x32_bf16 (each product of two bf16
 // values is exact in fp32) with fp32 accumulation. Only the two split residuals are lost:
 // each product is within ~2^-15 of fp32, the sums within a few 1e-6 relative.
 //
@@ -30,8 +32,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 8;                 // wavefronts per workgroup
 constexpr int kVRows = 16 * kWaves;       // vocab rows per workgroup
 constexpr int kMaxTiles = 4;              // 16-row tiles of x per pass (64 rows)
-constexpr int kTilePieces = 512;          // 16-byte pieces of one (row tile, block) fragment
-constexpr int kBlkElems = 4 * 2 * kWave * 8;  // bf16 of one (row tile, block) fragment
+constexpr int kTilePieces = 512;  // 16-byte pieces of the hi and mid parts of one (row tile, block)
+constexpr int kBlkElems = 4 * lsh::kFragPieces * kWave * 8;  // bf16 of one (row tile, block)
 
 struct LmArgs {
   const __bf16* xf;  // fragments of x [mp, K]
@@ -40,7 +42,7 @@ struct LmArgs {
   int M, V, K, nblk;
 };
 
-// W row chunk -> bf16 hi / lo A operands of step q (8 channels).
+// W row chunk -> bf16 hi / lo A operands of step q (8 channels; W = hi + lo to 2^-17).
 __device__ __forceinline__ void split_w(const u32x4& p0, const u32x4& p1, bf16x8& hi, bf16x8& lo) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -71,14 +73,17 @@ __global__ __launch_bounds__(kWaves * kWave) void lm_head_f32_kernel(LmArgs a) {
   // W rows of step s: vocab tile blockIdx.x + (s / nblk) gridDim.x, block s % nblk
   auto vtile = [&](int s) { return static_cast<int>(blockIdx.x) + (s / a.nblk) * static_cast<int>(gridDim.x); };
 
-  // x staging: piece p = tid + 256 i of the T (row tile, block) fragments
+  // x staging: 16-byte piece p = tid + 512 i of the hi and mid parts of the T (row tile,
+  // block) fragments; within one, piece (2 q + h) * 64 + lane comes from step q, part h
   constexpr int kPer = T * kTilePieces / (kWaves * kWave);
   auto load_x = [&](int b, u32x4 (&r)[kPer]) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int p = tid + i * kWaves * kWave;
       const int t = p / kTilePieces, within = p % kTilePieces;
-      r[i] = xg[(static_cast<int64_t>(tile0 + t) * a.nblk + b) * kTilePieces + within];
+      const int qh = within / kWave, l = within % kWave;  // qh = 2 q + h
+      r[i] = xg[((static_cast<int64_t>(tile0 + t) * a.nblk + b) * 4 + qh / 2) *
+                    (lsh::kFragPieces * kWave) + (qh % 2) * kWave + l];
     }
   };
   auto store_x = [&](int buf, const u32x4 (&r)[kPer]) {

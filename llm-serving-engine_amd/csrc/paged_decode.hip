@@ -802,7 +802,7 @@ void launch_decode(const DecodeArgs& a, bool scalar, bool off32, const FragOut& 
       const int mp = static_cast<int>(lsh::frag_rows(a.B));
       const int64_t K = static_cast<int64_t>(a.Hq) * D;
       __bf16* xf = static_cast<__bf16*>(fo.xfrag);
-      float* xsum = reinterpret_cast<float*>(xf + static_cast<int64_t>(mp) * K * 2);
+      float* xsum = lsh::frag_sums(xf, mp, K);
       const int64_t items = static_cast<int64_t>(mp) * a.Hq;
       lsh::launch(paged_decode_merge_frag_kernel<D>,
                   dim3(static_cast<unsigned>((items + kMergeWaves - 1) / kMergeWaves)),

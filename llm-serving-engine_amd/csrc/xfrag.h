@@ -1,9 +1,14 @@
 // Activation fragments of the batched int4 linear (int4_gemm_lat): x' = x * inv_act_scale
-// split into bf16 hi = bf16(x') and lo = bf16(x' - hi), laid out in the order the matrix-core
-// wavefronts read them, plus the channel sums of x' over every 128-channel block.
+// split into three bf16 pieces hi = bf16(x'), mid = bf16(x' - hi), lo = bf16(x' - hi - mid),
+// laid out in the order the matrix-core wavefronts read them, plus the channel sums of x' over
+// every 128-channel block. Each difference is exact in fp32 and each piece takes the next 8
+// significant bits, so hi + mid + lo equals x' to ~2^-26 relative: below fp32's own rounding,
+// so that the products on the matrix cores are those of fp32 arithmetic (two pieces keep only
+// ~2^-17, an error that 28 decoder layers amplify into the logits' third digit).
 //
-//   fragments: [row tile t][block b][step q][hi, lo][lane][8 bf16]; lane = fr + 16 fc holds
-//              row 16 t + fr, channels 128 b + 32 fc + 8 q .. + 8 (rows past M are zero);
+//   fragments: [row tile t][block b][step q][hi, mid, lo][lane][8 bf16]; lane = fr + 16 fc
+//              holds row 16 t + fr, channels 128 b + 32 fc + 8 q .. + 8 (rows past M are
+//              zero);
 //   xsum:      [block][mp] fp32 after the fragments, mp = M rounded up to 16.
 //
 // Every producer (the split pass of llmserve_int4_linear_gemm_packed, the fused norms and
@@ -18,26 +23,43 @@
 namespace lsh {
 
 constexpr int kFragBlk = 128;       // channels of a block
-constexpr int kFragElems = 64 * 8;  // bf16 of one (step, hi / lo) fragment
+constexpr int kFragPieces = 3;      // hi, mid, lo
+constexpr int kFragElems = 64 * 8;  // bf16 of one (step, piece) fragment
 
 __host__ __device__ inline int64_t frag_rows(int64_t M) { return (M + 15) / 16 * 16; }
 
 // Bytes of fragments + channel sums for M rows and K channels (K a multiple of 128).
 inline int64_t frag_bytes(int64_t M, int64_t K) {
-  return frag_rows(M) * K * 4 + (K / kFragBlk) * frag_rows(M) * 4;
+  return frag_rows(M) * K * 2 * kFragPieces + (K / kFragBlk) * frag_rows(M) * 4;
 }
 
-// Element offset of the hi value of x'[m, c] (the lo value is kFragElems further).
+// The channel sums after the fragments of mp (padded) rows and K channels.
+__host__ __device__ inline float* frag_sums(void* xf, int64_t mp, int64_t K) {
+  return reinterpret_cast<float*>(static_cast<__bf16*>(xf) + kFragPieces * mp * K);
+}
+__host__ __device__ inline const float* frag_sums(const void* xf, int64_t mp, int64_t K) {
+  return reinterpret_cast<const float*>(static_cast<const __bf16*>(xf) + kFragPieces * mp * K);
+}
+
+// Element offset of the hi value of x'[m, c] (mid and lo follow, kFragElems apart).
 __device__ __forceinline__ int64_t frag_offset(int m, int c, int nblk) {
   const int t = m / 16, fr = m % 16, b = c / kFragBlk, cc = c % kFragBlk;
   const int fc = cc / 32, q = (cc % 32) / 8, e = cc % 8;
-  return ((((static_cast<int64_t>(t) * nblk + b) * 4 + q) * 2) * 64 + fr + 16 * fc) * 8 + e;
+  return ((((static_cast<int64_t>(t) * nblk + b) * 4 + q) * kFragPieces) * 64 + fr + 16 * fc) * 8 + e;
 }
 
-// hi / lo bf16 split of an fp32 value (round to nearest even; hi + lo equals v to 2^-18).
+// hi / lo bf16 split of an fp32 value (round to nearest even; hi + lo equals v to 2^-17).
 __device__ __forceinline__ void split_bf16(float v, __bf16& hi, __bf16& lo) {
   hi = static_cast<__bf16>(v);
   lo = static_cast<__bf16>(v - static_cast<float>(hi));
+}
+
+// hi / mid / lo bf16 split (each difference exact in fp32; the sum equals v to ~2^-26).
+__device__ __forceinline__ void split3_bf16(float v, __bf16& hi, __bf16& mid, __bf16& lo) {
+  hi = static_cast<__bf16>(v);
+  const float r = v - static_cast<float>(hi);
+  mid = static_cast<__bf16>(r);
+  lo = static_cast<__bf16>(r - static_cast<float>(mid));
 }
 
 // Writes N consecutive channels c .. c + N - 1 (within one 8-channel group) of row m.
@@ -45,17 +67,19 @@ template <int N>
 __device__ __forceinline__ void frag_store(__bf16* xf, int m, int c, int nblk, const float (&v)[N]) {
   static_assert(N == 2 || N == 4 || N == 8, "frag_store: 2, 4 or 8 channels");
   typedef __bf16 bfN __attribute__((ext_vector_type(N)));
-  bfN hi, lo;
+  bfN hi, mid, lo;
 #pragma unroll
   for (int e = 0; e < N; ++e) {
-    __bf16 h, l;
-    split_bf16(v[e], h, l);
+    __bf16 h, md, l;
+    split3_bf16(v[e], h, md, l);
     hi[e] = h;
+    mid[e] = md;
     lo[e] = l;
   }
   __bf16* p = xf + frag_offset(m, c, nblk);
   *reinterpret_cast<bfN*>(p) = hi;
-  *reinterpret_cast<bfN*>(p + kFragElems) = lo;
+  *reinterpret_cast<bfN*>(p + kFragElems) = mid;
+  *reinterpret_cast<bfN*>(p + 2 * kFragElems) = lo;
 }
 
 // Pairwise tree of N consecutive values in index order (the first levels of a block sum).

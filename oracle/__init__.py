@@ -3,7 +3,7 @@
 A CPU restatement of the reference's quantized decode path (Buland-Choudhary/
 llm-serving-engine, src/llmserve/): the quantizers in numpy (``oracle.quant``), the three CPU
 kernels in C (``oracle/cpu_kernels.c`` via ``oracle.cpu``) and float64 references of the same
-mathematics (``oracle.math_ref``). ``oracle/build_ref.py`` additionally compiles the
+mathematics (``oracle.math_ref``). ``oracle/build.py`` additionally compiles the
 reference's own C++ kernel sources into ``oracle/_ref/`` when ``/root/reference`` is present.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg may import

@@ -171,9 +171,10 @@ def _rope64(t, pos, theta):
 
 
 def decode_step_plain_f64(W: Weights, cfg, ids, ctx, block_tables, caches: list[LayerCache],
-                          block_size: int):
+                          block_size: int, write_kv: bool = True):
     """float64 plain forward of the same step; ``caches`` are updated in place (the new K/V
-    rows quantized by the float32 quantizer, the cache format). Returns logits float64."""
+    rows quantized by the float32 quantizer, the cache format; with ``write_kv=False`` they
+    must already hold this step's rows, as in ``decode_step``). Returns logits float64."""
     nq, nk, D, eps = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rms_norm_eps
     ids, ctx = np.asarray(ids, np.int64), np.asarray(ctx, np.int64)
     B = len(ids)
@@ -193,8 +194,9 @@ def decode_step_plain_f64(W: Weights, cfg, ids, ctx, block_tables, caches: list[
         if c.smooth is not None:
             k = k / np.asarray(c.smooth, np.float64)
             q = q * np.repeat(np.asarray(c.smooth, np.float64), nq // nk, axis=0)
-        c.kd[slots], c.ks[slots] = oq.kv_quantize(k.astype(F32))
-        c.vd[slots], c.vs[slots] = oq.kv_quantize(v.astype(F32))
+        if write_kv:
+            c.kd[slots], c.ks[slots] = oq.kv_quantize(k.astype(F32))
+            c.vd[slots], c.vs[slots] = oq.kv_quantize(v.astype(F32))
         o = mr.paged_decode_f64(q, mr.kv_dequantize(c.kd, c.ks), mr.kv_dequantize(c.vd, c.vs),
                                 block_tables, ctx, block_size, float(D) ** -0.5)
         x = x + _lin64(o.reshape(B, nq * D), L.o)

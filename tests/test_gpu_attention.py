@@ -166,8 +166,8 @@ def test_edge_contexts(gpu):
 ])
 def test_merge_writes_oproj_fragments(gpu, B, Hq, Hk, D, bs, part, with_inv, zero_ctx):
     """The decode whose merge writes o_proj's input fragments: its output equals the plain
-    decode's bit for bit, and its fragments (x' = out * inv_act_scale, bf16 hi / lo, block
-    sums) equal those the packed int4 linear's split pass makes of that output."""
+    decode's bit for bit, and its fragments (x' = out * inv_act_scale, bf16 hi / mid / lo,
+    block sums) equal those the packed int4 linear's split pass makes of that output."""
     c = make_case(B * 7 + D, B, Hq, Hk, D, bs, 1, 700)
     if zero_ctx:
         c["cl"][1] = 0

@@ -4,9 +4,10 @@ reference [N, K/2] layout and the decode-batch kernel on the packed weight, whos
 checked byte for byte by unpacking it on the host.
 
 Tolerance: max-abs error <= 2e-5 * max|y| and rel-L2 <= 2e-5 against the float64 mathematics.
-x' = x * inv_act_scale is carried as two bf16 terms (xh + xl equals x' to 2^-18 relative) and
-every matrix-core product is exact, so the error is a few 1e-6; 2e-5 stays inside the
-reference tests' own 2e-4 for int4 (tests/test_quant.py:116-118).
+x' = x * inv_act_scale is carried as bf16 terms (two by the reference-layout kernel: x' to
+2^-17 relative; three by the packed decode-batch kernel: x' to ~2^-26) and every matrix-core
+product is exact, so the error is a few 1e-6 or less; 2e-5 stays inside the reference tests'
+own 2e-4 for int4 (tests/test_quant.py:116-118).
 """
 
 from __future__ import annotations

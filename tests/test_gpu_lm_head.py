@@ -4,8 +4,8 @@ x and W are each split into bf16 hi + lo (exact to ~2^-16 relative) and the four
 accumulate in fp32, so the logits are within a few 1e-6 of fp32; the bound here is
 max-abs <= 2e-5 * max|ref| and rel-L2 <= 2e-5 against x . W^T in float64. Shapes cover a
 partial row tile (rows past M are zero fragments and are not stored), several 64-row passes
-plus a remainder, and vocab sizes that are not multiples of 64 or 4 (clamped loads, scalar
-stores). The decode step's use of it is checked against the step oracle in test_gpu_step.
+plus a remainder, vocab sizes that are not multiples of 64 or 4 (clamped loads, scalar
+stores), and the Qwen3-0.6B head (V = 151936, K = 1024) at 8 and 64 rows. The decode step's use of it is checked against the step oracle in test_gpu_step.
 """
 
 from __future__ import annotations
@@ -29,7 +29,8 @@ def _lm_head(xf, w, M):
 
 
 @pytest.mark.parametrize("M,V,K", [(5, 1000, 256), (64, 4096, 1024), (70, 777, 512),
-                                   (130, 2050, 384), (16, 4099, 128)])
+                                   (130, 2050, 384), (16, 4099, 128),
+                                   (8, 151936, 1024), (64, 151936, 1024)])  # Qwen3-0.6B head
 def test_lm_head_f32_matches_f64(gpu, M, V, K):
     rng = np.random.default_rng(M * 7 + V)
     x = rng.standard_normal((M, K)).astype(np.float32)

@@ -3,8 +3,8 @@ Int4Linear's GEMV and packed matrix-core rows, the product's AWQ search, and
 quantize_model + collect_linear_inputs on a small model.
 
 Tolerances: linears within 1e-5 of the float64 product over the oracle's dequantized weight
-(max-abs relative to max|y| and rel-L2), 1e-4 for the packed matrix-core kernel (TOL_MC); quantizer buffers bit-exact with the oracle given the
-scale; the AWQ search picks the golden alpha (computed with torch's CPU ops, the reference's
+(max-abs relative to max|y| and rel-L2), 2e-5 for the packed matrix-core kernel (TOL_MC);
+quantizer buffers bit-exact with the oracle given the scale; the AWQ search picks the golden alpha (computed with torch's CPU ops, the reference's
 arithmetic) and a scale within 2e-6 of the golden one (the GPU's fp32 reductions differ in
 order from the CPU's).
 """
@@ -23,11 +23,11 @@ from oracle import quant as oq
 pytestmark = pytest.mark.gpu
 F32 = np.float32
 TOL = 1e-5
-# The packed matrix-core kernel (Int4Linear above 4 rows) multiplies x' split into bf16 hi + lo
-# (x' to ~2^-16 relative) with exact products: a few 1e-5 against float64 with outlier
-# channels, inside the reference's int4 bar of 2e-4 (tests/test_quant.py:116-118) and the
-# 1e-4 stated for the matrix-core linears.
-TOL_MC = 1e-4
+# The packed matrix-core kernel (Int4Linear above 4 rows) multiplies x' split into bf16
+# hi + mid + lo (x' to ~2^-26 relative) with exact products: fp32 arithmetic up to the
+# summation order, so the GEMV's bar applies (inside the reference's int4 bar of 2e-4,
+# tests/test_quant.py:116-118).
+TOL_MC = 2e-5
 
 
 def _linear(n_out, n_in, seed):
