@@ -16,15 +16,21 @@ x + y) x steps / wall time of the K timed steps. `roofline` is for the dominant 
 gate_up GEMV): its algorithmic bytes per launch over its average launch duration, measured
 here with HIP events around graph replays of back-to-back launches (distinct weights) on the
 stream the kernel runs on — the per-dispatch interval a kernel-trace profiler reports.
+The same interval for a one-element fill kernel (`empty_kernel_us`) is the floor of such a
+measurement; `roofline.rocprof` holds what rocprofv3's kernel trace reports for both
+(profiles/launch_calibration.md), so the two clocks can be compared.
 `cpu_baseline` times the reference's own CPU kernels (oracle/_ref, built from the reference
 sources) — or the oracle's C restatement where that build is absent — on the host cores, on
-the same quantized weights, for about 10 s.
+the same quantized weights: config 2 on one thread per physical core of the GPU's NUMA node;
+`extra.cpu` adds configs 1 and 4 and a 4-thread run of all three, with the CPU model and its
+AVX-512 flag (about 25 s in all).
 Extra fields report M = 4 / 16 steps (the kernel Int4Linear runs at that batch: the GEMV up
 to 4 rows, the matrix-core kernel on the packed weight above) and configs 1 (int8 GEMV), 3
 (prefill int8 GEMM on the bf16 matrix cores, x conversion included), 4 (int8-KV decode) and
 5 (the full greedy decode step of a random-init int4-AWQ Qwen3-0.6B at batch 64 over the int8
 KV cache, one HIP graph replay per step: tokens/s, with the fp32 and the int4 LM head, and
-per-op times).
+per-op times; the same model at batch 1 and 4, with the persistent per-layer chain and
+without).
 """
 
 from __future__ import annotations
@@ -202,56 +208,178 @@ def read_traffic(kernel: str) -> dict | None:
     return None
 
 
-def cpu_baseline(torch, model, calib, budget_s: float = 10.0) -> dict:
-    """The reference's CPU int4 kernel (Int4Linear.forward's small-batch path: x * inv then
-    int4_linear) over one copy of the 112 linears, M = 1, for about `budget_s` seconds."""
+def host_info(torch) -> dict:
+    """The host cores this process may run on: CPU model, AVX-512, the allowed logical CPUs,
+    their physical cores (one logical CPU per core) by NUMA node, and the GPU's NUMA node
+    (from the PCI device of cuda:0 when the driver exposes it)."""
+    info = {"model": None, "avx512f": False, "allowed_cpus": sorted(os.sched_getaffinity(0))}
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name") and info["model"] is None:
+                info["model"] = line.split(":", 1)[1].strip()
+            if line.startswith("flags") and " avx512f" in line:
+                info["avx512f"] = True
+    except OSError:
+        pass
+    cores = {}  # (node, package, core) -> first allowed logical CPU
+    for c in info["allowed_cpus"]:
+        base = Path(f"/sys/devices/system/cpu/cpu{c}")
+        try:
+            pkg = int((base / "topology/physical_package_id").read_text())
+            core = int((base / "topology/core_id").read_text())
+        except (OSError, ValueError):
+            pkg, core = 0, c
+        nodes = sorted(base.glob("node[0-9]*"))
+        node = int(nodes[0].name[4:]) if nodes else 0
+        cores.setdefault((node, pkg, core), c)
+    by_node = {}
+    for (node, _, _), c in sorted(cores.items()):
+        by_node.setdefault(node, []).append(c)
+    info["physical_cores_by_node"] = {str(n): v for n, v in by_node.items()}
+    gpu_node = None
+    try:
+        pr = torch.cuda.get_device_properties(0)
+        dom, bus, dv = (getattr(pr, "pci_domain_id", 0), getattr(pr, "pci_bus_id", None),
+                        getattr(pr, "pci_device_id", None))
+        if bus is not None and dv is not None:
+            f = Path(f"/sys/bus/pci/devices/{dom:04x}:{bus:02x}:{dv:02x}.0/numa_node")
+            gpu_node = int(f.read_text())
+    except Exception:  # pragma: no cover - depends on the box
+        gpu_node = None
+    info["gpu_numa_node"] = gpu_node
+    return info
+
+
+def read_launch_calibration() -> dict | None:
+    """The rocprofv3 kernel-trace figures of the same two measurements (the gate_up GEMV and
+    the fill kernel, each 224 launches per graph replay) from profiles/launch_calibration.md:
+    table rows `| name | dispatches | avg us | median us |`."""
+    p = REPO / "profiles" / "launch_calibration.md"
+    if not p.is_file():
+        return None
+    out = {}
+    for line in p.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] in ("gate_up GEMV", "fill kernel"):
+            try:
+                out[cells[0]] = {"avg_us": float(cells[2]), "median_us": float(cells[3])}
+            except ValueError:
+                pass
+    return out or None
+
+
+def cpu_baseline(torch, model, calib, dev, budget_s: float = 4.0) -> tuple[dict, dict]:
+    """The reference's own CPU kernels (oracle/_ref, compiled from its sources; the oracle's C
+    restatement where that build is absent) on the host cores, for configs 1 (int8_linear,
+    6144 x 1024, M = 1), 2 (int4_linear over the 112 Qwen3-0.6B linears, M = 1, x * inv first
+    as Int4Linear.forward does) and 4 (paged_attention_decode_int8 over config 4's cache, q
+    pre-multiplied by the smoothing vector as attention.py does): each for about `budget_s`
+    seconds, once with one thread per physical core of the GPU's NUMA node (of the cores this
+    process may use; the node with most of them when the GPU's is unknown) and once with 4
+    threads, the threads pinned to those cores. Returns (the config-2 line on the node's
+    cores, all runs)."""
     import numpy as np
 
     from oracle import cpu as ocpu
 
+    info = host_info(torch)
+    by_node = info["physical_cores_by_node"]
+    node = str(info["gpu_numa_node"]) if str(info["gpu_numa_node"]) in by_node else \
+        max(by_node, key=lambda n: len(by_node[n]))
+    node_cores = by_node[node]
+    kind = "reference" if ocpu.ref_available() else "port"
+    if kind == "reference":
+        gm, pm = ocpu.ref_module("llmserve_int8_gemv"), ocpu.ref_module("llmserve_paged_attention")
+    else:
+        log("[bench] reference CPU kernels unavailable; timing the C restatement")
+
+    # config 2: one copy of the 112 linears
     host = [{n: tuple(t.cpu() for t in lin[n]) for n in SHAPES} for lin in model[0]]
     xs = {n: calib[n][:1].cpu().contiguous() for n in SHAPES}
-    kind, fn = "port", None
-    try:
-        if ocpu.ref_available():
-            mod = ocpu.ref_module("llmserve_int8_gemv")
-            kind = "reference"
 
-            def fn(x, nib, gs, gz, inv):
-                return mod.int4_linear((x * inv).contiguous(), nib, gs, gz, GROUP)
-    except Exception as e:  # pragma: no cover - depends on the box
-        log(f"[bench] reference CPU kernels unavailable ({e}); timing the C restatement")
-    if fn is None:
-        def fn(x, nib, gs, gz, inv):
-            return ocpu.int4_linear(x.numpy(), nib.numpy(), gs.numpy(), gz.numpy(), GROUP,
-                                    inv.numpy())
-    step_bytes = LAYERS * sum(int4_bytes(N, K, 1) for N, K in SHAPES.values())
-
-    def step():
+    def c2():
         for lin in host:
             for n in SHAPES:
                 nib, gs, gz, inv = lin[n]
-                fn(xs[n], nib, gs, gz, inv)
+                if kind == "reference":
+                    gm.int4_linear((xs[n] * inv).contiguous(), nib, gs, gz, GROUP)
+                else:
+                    ocpu.int4_linear(xs[n].numpy(), nib.numpy(), gs.numpy(), gz.numpy(), GROUP,
+                                     inv.numpy())
+    c2_bytes = LAYERS * sum(int4_bytes(N, K, 1) for N, K in SHAPES.values())
 
-    step()  # warm-up
-    steps, t0 = 0, time.perf_counter()
-    best = float("inf")
-    while time.perf_counter() - t0 < budget_s:
-        t = time.perf_counter()
-        step()
-        best = min(best, time.perf_counter() - t)
-        steps += 1
-    elapsed = time.perf_counter() - t0
-    threads = torch.get_num_threads() if kind == "reference" else ocpu.get_threads()
-    return {
-        "value": round(step_bytes * steps / elapsed / 1e9, 3),
+    # config 1: 6144 x 1024 int8 weights, 64 copies (400 MB: past the last-level cache)
+    from llmserve.kernels import load_quant
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    q1 = [tuple(t.cpu() for t in load_quant().int8_quantize(
+        torch.randn(6144, 1024, device=dev, generator=g) * 0.02)) for _ in range(64)]
+    x1 = torch.randn(1, 1024)
+    it1 = [0]
+
+    def c1():
+        w, sc = q1[it1[0] % len(q1)]
+        it1[0] += 1
+        if kind == "reference":
+            gm.int8_linear(x1, w, sc)
+        else:
+            ocpu.int8_linear(x1.numpy(), w.numpy(), sc.numpy())
+    c1_bytes = int8_bytes(6144, 1024, 1)
+
+    # config 4: one copy of its cache
+    copies, q, cl, qm, bs, D, c4_bytes = c4_inputs(torch, dev, ncopies=1)
+    kq, vq, ks, vs, bt = (t.cpu() for t in copies[0])
+    qh, clh = (q * qm).cpu(), cl.cpu()
+    del copies
+
+    def c4():
+        if kind == "reference":
+            pm.paged_attention_decode_int8(qh, kq, vq, ks, vs, bt, clh, bs, D ** -0.5, 0)
+        else:
+            ocpu.paged_decode_int8(qh.numpy(), kq.numpy(), vq.numpy(), ks.numpy(), vs.numpy(),
+                                   bt.numpy(), clh.numpy(), bs, D ** -0.5, 0)
+
+    def timed(fn, nbytes):
+        fn()  # warm-up
+        n, t0, best = 0, time.perf_counter(), float("inf")
+        while time.perf_counter() - t0 < budget_s:
+            t = time.perf_counter()
+            fn()
+            best = min(best, time.perf_counter() - t)
+            n += 1
+        el = time.perf_counter() - t0
+        return {"GBps": round(nbytes * n / el / 1e9, 3), "calls": n, "s": round(el, 2),
+                "best_ms": round(best * 1e3, 3)}
+
+    saved_aff, saved_threads = os.sched_getaffinity(0), torch.get_num_threads()
+    runs = {}
+    try:
+        for label, cores in (("node_physical_cores", node_cores), ("4_threads", node_cores[:4])):
+            os.sched_setaffinity(0, cores)
+            torch.set_num_threads(len(cores))
+            ocpu.set_threads(len(cores))
+            runs[label] = {"threads": len(cores), "cpus": cores,
+                           "c1_int8_gemv": timed(c1, c1_bytes),
+                           "c2_int4_112_gemvs": timed(c2, c2_bytes),
+                           "c4_int8kv_paged_decode": timed(c4, c4_bytes)}
+            log(f"[bench] cpu {label}: {runs[label]}")
+    finally:
+        os.sched_setaffinity(0, saved_aff)
+        torch.set_num_threads(saved_threads)
+    main_run = runs["node_physical_cores"]
+    line = {
+        "value": main_run["c2_int4_112_gemvs"]["GBps"],
         "unit": "GB/s",
-        "cores": threads,
+        "cores": main_run["threads"],
         "kind": kind,
-        "sample": (f"{steps} steps x 112 int4 g128 GEMVs (M=1, all 28 Qwen3-0.6B layers, one "
-                   f"250 MB weight copy), {elapsed:.1f} s; best step {best * 1e3:.1f} ms; host "
-                   f"{os.cpu_count()} logical CPUs, ISA {ocpu.host_isa()}"),
+        "sample": (f"{main_run['c2_int4_112_gemvs']['calls']} steps x 112 int4 g128 GEMVs (M=1, "
+                   f"all 28 Qwen3-0.6B layers, one 250 MB weight copy) in "
+                   f"{main_run['c2_int4_112_gemvs']['s']} s, one thread per physical core of "
+                   f"NUMA node {node} ({info['model']}, AVX-512 "
+                   f"{'yes' if info['avx512f'] else 'no'}); 4-thread and configs 1 / 4 runs in "
+                   f"extra.cpu"),
     }
+    return line, {"host": info, "numa_node": node, "kind": kind, "runs": runs}
 
 
 def extra_configs(torch, dev) -> dict:
@@ -375,7 +503,62 @@ def c5_decode(torch, dev, steps: int, warmup: int) -> dict:
         runner.graph = None
     model.lm_head = None
     out["per_op"] = c5_per_op(torch, dev, model, lm4, cache, runner)
+    del runner, cache
+    out["small_batch"] = {str(b): small_batch_decode(torch, dev, model, b, steps)
+                          for b in (1, 4)}
     return out
+
+
+def small_batch_decode(torch, dev, model, B: int, steps: int) -> dict:
+    """The config-5 model's greedy decode step at batch B (1 or 4), contexts ~ U[1024, 4096],
+    one graph replay per step; at 1 and 2 rows the step runs one persistent launch per layer
+    for the linear chain (QuantCausalLM.chain_max_rows), compared here with the launch-per-op
+    step (use_chain False). tok/s = B x steps / wall time."""
+    import numpy as np
+
+    from llmserve.kv_cache import KVCache
+    from llmserve.model_runner import DecodeRunner
+
+    cfg = model.cfg
+    bs = 16
+    rng = np.random.default_rng(60 + B)
+    ctx = rng.integers(1024, 4097, B).astype(np.int64)
+    nblk = -(-(ctx + 2 * steps + 16) // bs)
+    width, total = int(nblk.max()), int(nblk.sum())
+    perm = rng.permutation(total)
+    bt = np.zeros((B, width), np.int64)
+    used = 0
+    for i, n in enumerate(nblk):
+        bt[i, :n] = perm[used:used + n]
+        used += n
+    cache = KVCache(cfg, total, bs, device=dev, kv_dtype="int8")
+    g = torch.Generator(device=dev).manual_seed(61)
+    for k, v in cache.layers:
+        for t in (k, v):
+            t.data.random_(-127, 128, generator=g)
+            t.scale.uniform_(0.005, 0.05, generator=g)
+    ids = torch.from_numpy(rng.integers(0, cfg.vocab_size, B)).to(dev)
+    runner = DecodeRunner(model, cache, ids, torch.from_numpy(ctx), torch.from_numpy(bt))
+    res = {}
+    for mode in ("chain", "per_op"):
+        model.use_chain = mode == "chain"
+        if mode == "chain" and not (model._chain_ok(B) and B <= model.chain_max_rows):
+            continue
+        runner.capture(keep_state=False)
+        for _ in range(3):
+            runner.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps // 2):
+            runner.replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        n = steps // 2
+        res[mode] = {"tok_per_s": round(B * n / wall, 1), "us_per_step": round(wall / n * 1e6, 1)}
+        runner.graph = None
+    model.use_chain = True
+    log(f"[bench] c5 model at batch {B}: {res}")
+    return res
 
 
 def nn_linear(torch, w):
@@ -478,9 +661,9 @@ def c5_per_op(torch, dev, model, lm4, cache, runner) -> dict:
     return res
 
 
-def c4_inputs(torch, dev):
-    """Config 4: 4 copies (~1.1 GB) of an int8 KV cache for 32 sequences, ctx ~ U[512, 8192],
-    block tables a random permutation of the physical blocks."""
+def c4_inputs(torch, dev, ncopies: int = 4):
+    """Config 4: `ncopies` copies (~280 MB each) of an int8 KV cache for 32 sequences, ctx ~
+    U[512, 8192], block tables a random permutation of the physical blocks."""
     import numpy as np
 
     rng = np.random.default_rng(2024)
@@ -490,7 +673,7 @@ def c4_inputs(torch, dev):
     total = int(nblk.sum())
     width = int(nblk.max())
     copies = []
-    for _ in range(4):
+    for _ in range(ncopies):
         perm = rng.permutation(total)
         bt = np.zeros((B, width), np.int64)
         used = 0
@@ -634,14 +817,20 @@ def main() -> int:
         gemv.int4_linear(xs["gate_up"], nib, gs, gz, GROUP, inv)
 
     avg_us = kernel_avg_us(torch, gate_up, 224)
+    # the per-dispatch floor of this measurement: a one-element fill kernel timed the same way
+    tiny = [torch.zeros(1, device=dev) for _ in range(8)]
+    empty_us = kernel_avg_us(torch, lambda i: tiny[i % 8].fill_(float(i)), 224)
     kb = int4_bytes(N, K, 1)
     achieved = kb / avg_us / 1e3
     traffic = read_traffic("gemv_lat int4 gate_up M=1")
+    prof = read_launch_calibration()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None if traffic is None else int(traffic["fetch"] + traffic["write"]),
                 "kernel": "gemv_lat int4 (gate_up 1024->6144, M=1)",
-                "bytes_per_launch": kb, "avg_launch_us": round(avg_us, 3)}
+                "bytes_per_launch": kb, "avg_launch_us": round(avg_us, 3),
+                "empty_kernel_us": round(empty_us, 3),
+                "rocprof": prof}
     log(f"[bench] roofline: {roofline}")
 
     extra = {} if args.no_extra else extra_configs(torch, dev)
@@ -651,8 +840,8 @@ def main() -> int:
         log(f"[bench] extra: {extra}")
     cpu = None
     if not args.no_cpu:
-        log("[bench] CPU baseline (about 10 s)")
-        cpu = cpu_baseline(torch, model, calib)
+        log("[bench] CPU baselines (about 25 s)")
+        cpu, extra["cpu"] = cpu_baseline(torch, model, calib, dev)
         log(f"[bench] cpu: {cpu}")
 
     gbs, ms, steps, step_bytes = headline

@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void x_split_frag_kernel(
 
 // Decode-sized batches (up to a few 16-row tiles). The time goes to each CU's memory
 // requests, not to bandwidth or matrix-core throughput: int4_gemm_lat gives a wavefront
-// only KB <= 3 blocks of K per round (one round up to K = 3072), issues every load of them
+// only KB <= 2 blocks of K per round (one round up to K = 2048), issues every load of them
 // (nibbles, x fragments, channel sums, group scales and zeros) before the first use, and
 // lets S wavefronts of a workgroup split the K blocks of one 16 x 64 slab; their partial sums meet in LDS and each output tile is
 // finished by one wavefront adding the S partials in a fixed order (deterministic).
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
   f32x4 acc[kNT];
 #pragma unroll
   for (int u = 0; u < kNT; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Rounds of S x KB blocks (one round up to K = 3072 at S = 8, KB = 3).
+  // Rounds of S x KB blocks (one round up to K = 2048 at S = 8, KB = 2).
   for (int base = 0; base < nblk; base += S * KB) {
     u32x4 w[KB][kNT], xh[KB][4], xm[KB][4], xl[KB][4];
     f32x4 xs[KB];
@@ -444,15 +444,19 @@ void launch_lat_ks(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, hipStre
               static_cast<int>(slabs_pad), static_cast<int>(mtiles));
 }
 
-// Blocks per wavefront and round KB = ceil(nb / 8) (at most 3), then the fewest of 1, 2, 4, 8
+// Blocks per wavefront and round KB = ceil(nb / 8) (at most 2: three blocks of three-piece x
+// fragments take more than the 256 registers a wavefront of an 8-wavefront workgroup has, and
+// the spills cost more than a second round: down 3072->1024 at 64 rows 15.5 against 14.3 us),
+// then the fewest of 1, 2, 4, 8
 // wavefronts that cover the nb blocks (8 when more than one round is needed); the exceptions
 // below.
 void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb, hipStream_t st) {
-  int KB = std::min(3, (nb + 7) / 8);
+  int KB = std::min(2, (nb + 7) / 8);
   int S = 1;
   while (S < 8 && S * KB < nb) S *= 2;
-  // 9..16 blocks on a narrow output: 16 wavefronts of one block each (4 per SIMD) keep more
-  // loads in flight per CU than 8 of two blocks (o_proj at M = 64: 6.3 against 6.7 us)
+  // more than 8 blocks on a narrow output: 16 wavefronts of one block each (4 per SIMD) keep
+  // more loads in flight per CU than 8 of two blocks (o_proj at M = 64: 6.3 against 6.7 us;
+  // down, 24 blocks, takes two such rounds)
   if (KB == 2 && S == 8 && slabs * mtiles < 256) {
     KB = 1;
     S = 16;
@@ -465,7 +469,7 @@ void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb, hi
 #define LSH_LAT(kb, s) \
   if (KB == kb && S == s) return launch_lat_ks<kb, s>(a, slabs, mtiles, st);
   LSH_LAT(1, 1) LSH_LAT(1, 2) LSH_LAT(1, 4) LSH_LAT(1, 8)
-  LSH_LAT(2, 4) LSH_LAT(2, 8) LSH_LAT(3, 8) LSH_LAT(1, 16)
+  LSH_LAT(2, 4) LSH_LAT(2, 8) LSH_LAT(1, 16)
 #undef LSH_LAT
 }
 
