@@ -465,6 +465,32 @@ int llmserve_paged_attention_decode_int8_noalloc(
     int64_t block_size, float scale, int64_t partition_size, const float* q_mult /* nullable */,
     void* stream);
 
+/*
+ * Batched token sampler (replaces the body of sampling.sample, sampling.py:151-189, for a
+ * logits batch on the GPU): one workgroup per row of logits [B, V] (float32, row-major,
+ * V < 2^24). Per row, in the reference's order: presence / frequency penalties over the
+ * row's generated tokens (CSR out_ptr [B + 1] / out_ids / out_cnt: distinct ids and their
+ * counts), then the repetition penalty over its prompt + generated tokens (seen_ptr /
+ * seen_ids, distinct), both written into `logits` (apply_penalties, sampling.py:100-120); the
+ * allowed set when has_allow[b] (allow_ptr / allow_ids: every other token -inf) and the
+ * banned tokens (ban_ptr / ban_ids: -inf), also in place (sampling.py:165-170). A row with
+ * temperature < 1e-5 takes the first index of its maximum (NaN above every number). Any other
+ * row samples argmax p / E: p the softmax of logits / temperature after the top-k / top-p
+ * cut (when use_topkp, the batch-wide switch of _top_k_top_p_min_p, sampling.py:123-143;
+ * top_k -1 is off; the cut is the reference's up to the rounding of the mass before a token
+ * at top_p) and the min-p cut (when use_minp), E its Exp(1) noise row noise[noise_row[b]]
+ * (sampling.py:183-187). Writes tokens [B] (int64). Greedy-only batches still pass a valid
+ * noise buffer (it is not read).
+ */
+int llmserve_sample(float* logits, int64_t B, int64_t V, const float* temperature,
+                    const int* top_k, const float* top_p, const float* min_p,
+                    const float* presence, const float* frequency, const float* repetition,
+                    const int64_t* out_ptr, const int64_t* out_ids, const int* out_cnt,
+                    const int64_t* seen_ptr, const int64_t* seen_ids, const int64_t* allow_ptr,
+                    const int64_t* allow_ids, const uint8_t* has_allow, const int64_t* ban_ptr,
+                    const int64_t* ban_ids, const float* noise, const int64_t* noise_row,
+                    int use_topkp, int use_minp, int64_t* tokens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

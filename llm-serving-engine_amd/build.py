@@ -55,6 +55,7 @@ HIP_SOURCES = [
     "gemm_prefill.hip",
     "gemm_int4.hip",
     "fused_ops.hip",
+    "sampling.hip",
     "paged_decode.hip",
     "attn_meta.hip",
     "decode_chain.hip",
