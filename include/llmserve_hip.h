@@ -295,6 +295,15 @@ int llmserve_argmax_advance(const float* logits, int64_t T, int64_t V, int64_t* 
 int llmserve_lm_head_f32_xfrag(const void* xfrag, const float* w, float* y, int64_t M, int64_t V,
                                int64_t K, void* stream);
 
+/*
+ * The same fp32 LM head for a decode batch of 1-4 rows (models/transformer.py:192-193 at batch
+ * 1-4, where the reference's F.linear is a GEMV over the whole matrix): y[M, V] = x[M, K] .
+ * w[V, K]^T in exact fp32 arithmetic (up to summation order), streaming w once. K = 256, 512
+ * or 1024; x and w 16-byte aligned.
+ */
+int llmserve_lm_head_f32(const float* x, const float* w, float* y, int64_t M, int64_t V, int64_t K,
+                         void* stream);
+
 /* ---- int8-KV paged decode attention ------------------------------------------------------ */
 
 /*

@@ -198,6 +198,105 @@ void launch_lm(const LmArgs& a, int passes, bool last, hipStream_t st) {
               dim3(kWaves * kWave), 0, st, last, a);
 }
 
+// ---- the fp32 head at 1-4 rows: a plain fp32 GEMV --------------------------------------------
+// At a decode batch of 1-4 rows the 622 MB matrix is read once for a few dot products per
+// row: a GEMV, bound by HBM. Each wavefront takes kGvRows vocab rows at a time; lane l holds
+// channels [16 NF l, 16 NF (l + 1)) ... as NF float4 chunks at stride 64 float4 (so a load
+// instruction reads 1 KB of a row contiguously), multiplies them by the same channels of the
+// M x rows (held in registers for the whole launch) and the row sums are reduced over the
+// wavefront. All the loads of a group of rows go out before its first product; the rows of
+// the next group are loaded while this group is reduced (two register sets). Exact fp32
+// products and sums (up to the summation order).
+constexpr int kGvWaves = 8;   // wavefronts per workgroup
+constexpr int kGvRows = 4;    // vocab rows per wavefront and group
+
+template <int M, int NF>
+__global__ __launch_bounds__(kGvWaves * kWave) void lm_head_gemv_kernel(const float* __restrict__ x,
+                                                                          const float* __restrict__ w,
+                                                                          float* __restrict__ y, int V) {
+  constexpr int K = NF * 4 * kWave;
+  const int lane = threadIdx.x % kWave;
+  const int gw = blockIdx.x * kGvWaves + static_cast<int>(threadIdx.x) / kWave;
+  const int nw = gridDim.x * kGvWaves;
+  f32x4 xv[M][NF];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      xv[m][f] = *reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(m) * K + (f * kWave + lane) * 4);
+  auto load = [&](int v0, f32x4 (&r)[kGvRows][NF]) {
+#pragma unroll
+    for (int i = 0; i < kGvRows; ++i) {
+      const int v = v0 + i < V ? v0 + i : V - 1;  // in bounds; the sums of rows past V are dropped
+      const f32x4* p = reinterpret_cast<const f32x4*>(w + static_cast<int64_t>(v) * K) + lane;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) r[i][f] = __builtin_nontemporal_load(p + f * kWave);
+    }
+  };
+  auto reduce_store = [&](int v0, const f32x4 (&r)[kGvRows][NF]) {
+#pragma unroll
+    for (int i = 0; i < kGvRows; ++i) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float d = 0.f;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          const f32x4 a = r[i][f], b = xv[m][f];
+          d += a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+        }
+        d = lsh::group_total<kWave>(d);
+        if (lane == kWave - 1 && v0 + i < V) y[static_cast<int64_t>(m) * V + v0 + i] = d;
+      }
+    }
+  };
+  f32x4 r0[kGvRows][NF], r1[kGvRows][NF];
+  int v = gw * kGvRows;
+  const int step = nw * kGvRows;
+  if (v >= V) return;
+  load(v, r0);
+  for (;;) {
+    const int vn = v + step;
+    if (vn < V) load(vn, r1);
+    reduce_store(v, r0);
+    if (vn >= V) break;
+    v = vn;
+    const int vm = v + step;
+    if (vm < V) load(vm, r0);
+    reduce_store(v, r1);
+    if (vm >= V) break;
+    v = vm;
+  }
+}
+
+template <int M, int NF>
+void launch_gemv_head(const float* x, const float* w, float* y, int V, hipStream_t st) {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, lm_head_gemv_kernel<M, NF>,
+                                                     kGvWaves * kWave, 0) != hipSuccess || per < 1)
+      per = 1;
+    cached[dev] = cus * per;
+  }
+  const int groups = (V + kGvRows * kGvWaves - 1) / (kGvRows * kGvWaves);
+  const int g = groups < cached[dev] ? groups : cached[dev];
+  lsh::launch(lm_head_gemv_kernel<M, NF>, dim3(static_cast<unsigned>(g)), dim3(kGvWaves * kWave), 0,
+              st, true, x, w, y, V);
+}
+
+template <int NF>
+void gemv_head_rows(int64_t M, const float* x, const float* w, float* y, int V, hipStream_t st) {
+  switch (M) {
+    case 1: launch_gemv_head<1, NF>(x, w, y, V, st); break;
+    case 2: launch_gemv_head<2, NF>(x, w, y, V, st); break;
+    case 3: launch_gemv_head<3, NF>(x, w, y, V, st); break;
+    default: launch_gemv_head<4, NF>(x, w, y, V, st); break;
+  }
+}
+
 }  // namespace
 
 extern "C" int llmserve_lm_head_f32_xfrag(const void* xfrag, const float* w, float* y, int64_t M,
@@ -237,4 +336,25 @@ extern "C" int llmserve_lm_head_f32_xfrag(const void* xfrag, const float* w, flo
     launch_lm<3>(a, 1, true, st);
   }
   return lsh::launch_status("lm_head_f32_xfrag");
+}
+
+// The fp32 LM head for a decode batch of 1-4 rows (the same product as llmserve_lm_head_f32_xfrag
+// in exact fp32 arithmetic, on x itself).
+extern "C" int llmserve_lm_head_f32(const float* x, const float* w, float* y, int64_t M,
+                                    int64_t V, int64_t K, void* stream) {
+  LSH_CHECK(M >= 0 && M <= 4, "lm_head_f32: 1 to 4 rows (got %lld)", (long long)M);
+  LSH_CHECK(V >= 1 && V < (1LL << 31) && V * K < (1LL << 40), "lm_head_f32: bad V");
+  LSH_CHECK(K == 256 || K == 512 || K == 1024,
+            "lm_head_f32: K must be 256, 512 or 1024 (got %lld)", (long long)K);
+  if (M == 0) return LLMSERVE_OK;
+  LSH_CHECK(x && w && y, "lm_head_f32: null pointer");
+  LSH_CHECK(lsh::aligned16(x) && lsh::aligned16(w), "lm_head_f32: x and w must be 16-byte aligned");
+  hipStream_t st = lsh::as_stream(stream);
+  const int Vi = static_cast<int>(V);
+  switch (K) {
+    case 256: gemv_head_rows<1>(M, x, w, y, Vi, st); break;
+    case 512: gemv_head_rows<2>(M, x, w, y, Vi, st); break;
+    default: gemv_head_rows<4>(M, x, w, y, Vi, st); break;
+  }
+  return lsh::launch_status("lm_head_f32");
 }

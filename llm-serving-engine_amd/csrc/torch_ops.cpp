@@ -521,6 +521,19 @@ at::Tensor int4_linear_gemm_xfrag(const at::Tensor& xfrag, const at::Tensor& pac
 
 // ---- int8-KV paged decode -------------------------------------------------------------------
 
+at::Tensor lm_head_f32(const at::Tensor& x, const at::Tensor& w) {
+  check_f32(x, "x");
+  TORCH_CHECK(w.scalar_type() == at::kFloat && w.is_contiguous() && w.dim() == 2,
+              "lm_head_f32: w must be a contiguous float32 [V, K] tensor");
+  check_device(x, {&w}, "lm_head_f32");
+  TORCH_CHECK(x.dim() == 2 && x.size(1) == w.size(1), "lm_head_f32: x [M, K] and w [V, K]");
+  const c10::DeviceGuard guard(x.device());
+  auto y = at::empty({x.size(0), w.size(0)}, x.options());
+  check_status(llmserve_lm_head_f32(x.data_ptr<float>(), w.data_ptr<float>(), y.data_ptr<float>(),
+                                    x.size(0), w.size(0), w.size(1), stream_of(x)));
+  return y;
+}
+
 at::Tensor lm_head_f32_xfrag(const at::Tensor& xfrag, const at::Tensor& w, int64_t M) {
   TORCH_CHECK(xfrag.scalar_type() == at::kByte && xfrag.is_contiguous(),
               "lm_head_f32_xfrag: xfrag must be a contiguous uint8 fragment buffer");
@@ -785,6 +798,7 @@ TORCH_LIBRARY(llmserve_hip, m) {
         " -> Tensor");
   m.def("silu_mul(Tensor gate_up) -> Tensor");
   m.def("lm_head_f32_xfrag(Tensor xfrag, Tensor w, int M) -> Tensor");
+  m.def("lm_head_f32(Tensor x, Tensor w) -> Tensor");
   m.def("rope_qk_(Tensor(a!) qkv, Tensor cos, Tensor sin, int n_q, int n_k, int head_dim,"
         " Tensor? q_w=None, Tensor? k_w=None, float eps=1e-6) -> ()");
   m.def("decode_qkv_kv(Tensor qkv, Tensor cos_table, Tensor sin_table, Tensor context_lens,"
@@ -827,6 +841,7 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("int4_linear_gemm_xfrag", &int4_linear_gemm_xfrag);
   m.impl("silu_mul", &silu_mul);
   m.impl("lm_head_f32_xfrag", &lm_head_f32_xfrag);
+  m.impl("lm_head_f32", &lm_head_f32);
   m.impl("rope_qk_", &rope_qk_);
   m.impl("decode_qkv_kv", &decode_qkv_kv);
   m.impl("argmax_advance", &argmax_advance);

@@ -115,6 +115,7 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
         [_P] * 8 + [_I64] * 7 + [_F32, _I64, _P, _P],
     ),
     "llmserve_sample": (_I32, [_P, _I64, _I64] + [_P] * 19 + [_I32, _I32, _P, _P]),
+    "llmserve_lm_head_f32": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P]),
 }
 
 

@@ -162,7 +162,8 @@ class QuantCausalLM(nn.Module):
     # matrix-core kernel on them: one launch less per linear, same result bits.
     fuse_xfrag = True
     # With fragments, the fp32 LM head runs the split-bf16 matrix-core kernel
-    # (lm_head_f32_xfrag, within a few 1e-6 of fp32) instead of torch.mm (hipBLASLt).
+    # (lm_head_f32_xfrag, within a few 1e-6 of fp32) instead of torch.mm (hipBLASLt); at 1-4
+    # rows the fp32 GEMV lm_head_f32 (exact fp32, reads the matrix once at HBM speed).
     fp32_head_kernel = True
 
     # Up to chain_max_rows rows the step runs one persistent launch per layer for the whole
@@ -404,6 +405,10 @@ class QuantCausalLM(nn.Module):
                                                            m.group_size)
         if self.lm_head is not None:
             return self.lm_head(hidden)
+        fo = load_fused_ops() if hidden.is_cuda else None
+        if (fo is not None and self.fp32_head_kernel and 1 <= hidden.shape[0] <= 4
+                and hidden.shape[1] in (256, 512, 1024)):
+            return fo.lm_head_f32(hidden.contiguous(), self.lm_weight)  # exact fp32 GEMV
         return torch.mm(hidden, self.lm_weight.t())
 
     def weight_bytes(self, rows: int) -> dict[str, int]:
