@@ -411,36 +411,47 @@ int llmserve_attention_metadata(const int64_t* seq_info, const int64_t* block_ta
                                 void* stream);
 
 /*
- * The linear chain of one decoder layer for a decode batch of M <= 4 sequences, as one
- * persistent launch (replaces, for small batches, the reference's per-op sequence of
- * _forward_fused, models/transformer.py:157-189, with Int4Linear.forward, quant.py:134-151,
- * and the cache write of paged_attention, attention.py:241-246):
+ * One decoder layer for a decode batch of M <= 4 sequences as one persistent launch:
+ * this layer's attention, its linear chain and the next layer's qkv (replaces, for small
+ * batches, the reference's per-op sequence of _forward_fused, models/transformer.py:157-189,
+ * with the decode attention of paged_attention_decode_int8, paged_attention.cpp:191-420,
+ * Int4Linear.forward, quant.py:134-151, and the cache write of paged_attention,
+ * attention.py:241-246):
+ *   attn = paged decode attention of q_in [M, n_q, 128] (times q_mult [n_q, 128] when given)
+ *          over this layer's int8 caches attn_k_cache / attn_v_cache [num_slots, n_k, 128]
+ *          with scales attn_k_scale / attn_v_scale [num_slots, n_k], the first
+ *          context_lens[m] tokens of row m (softmax scale `scale`; a row with no context
+ *          gives NaN)
  *   x1 = x_in + o_proj(attn);  h = rmsnorm(x1) * post_w;  a = silu(gate(h)) * up(h)
  *   x_out = x1 + down(a);      h2 = rmsnorm(x_out) * next_w
  *   then, when qkv_nib is given (not the last layer): the next layer's qkv = qkv_proj(h2),
  *   per-head RMSNorm (q_w / k_w, nullable) and rotate-half RoPE of q and k at position
  *   p = context_lens[m] - 1 (rows p of cos_t / sin_t [max_pos, 128]), q -> q_out [M, n_q, 128],
- *   k / k_smooth (nullable) and v int8-quantized into the caches at slot
- *   block_tables[m, p / block_size] * block_size + p % block_size (the quantizer of
- *   llmserve_kv_quantize_write; a position outside the tables leaves the cache and gives a NaN
- *   q row); otherwise h_out (nullable) = h2, the final norm's output.
- * Embedding mode (attn == NULL): x_out = embed[ids] (an id outside [0, vocab) gives a NaN
+ *   k / k_smooth (nullable) and v int8-quantized into the caches k_cache / v_cache (the next
+ *   layer's) at slot block_tables[m, p / block_size] * block_size + p % block_size (the
+ *   quantizer of llmserve_kv_quantize_write; a position outside the tables leaves the cache
+ *   and gives a NaN q row); otherwise h_out (nullable) = h2, the final norm's output.
+ * Embedding mode (q_in == NULL): x_out = embed[ids] (an id outside [0, vocab) gives a NaN
  * row), then the qkv part for layer 0 with next_w = its input norm.
  * int4 weights are the Int4Linear buffers (nibbles [N, K/2], g_scale / g_zero [N, K/128],
  * inv_act_scale [K] nullable); o_proj [H, n_q*128], gate_up [2I, H], down [H, I], qkv
  * [(n_q + 2 n_k) * 128, H]. Requires head_dim = group_size = 128, H a multiple of 128 in
- * [256, 1024] and of 4 * (n_q + 2 n_k), n_q * 128 <= 2048, I a multiple of 256 and of H / 4
- * with I / (H / 4) a multiple of 4 and at most 16, 16-byte aligned weights, activations and
- * norm weights; x_out must not alias x_in. The (H / 4 [+ n_q + 2 n_k]) workgroups hand
- * activations to each other through `workspace` (llmserve_decode_chain_workspace_bytes(H, I)
- * bytes, 16-byte aligned, zero before its first use and then owned by the chain: launches
- * that overlap on one workspace race) and must all be resident at once (checked). Each
- * hand-off wait gives up after `spin_limit` polls, sets the workspace's error word
- * (llmserve_decode_chain_error) and lets the grid finish. No counterpart in the reference.
+ * [256, 1024] and of 2 (n_q + 2 n_k), n_q * 128 <= 2048, I a multiple of 512 and of H / 8,
+ * at most 4096, with I / (H / 8) a multiple of 8 and at most 32, 16-byte aligned weights,
+ * activations and norm weights; x_out must not alias x_in and q_out must not alias q_in.
+ * The attention needs n_q = 2 n_k, n_k <= 8, block_size a power of two >= 8, caches of under
+ * 2^32 bytes and M n_q <= the grid. The H / 8 [+ n_q + 2 n_k] workgroups hand data to each
+ * other through `workspace` (llmserve_decode_chain_workspace_bytes(H, I) bytes, 16-byte
+ * aligned, zero before its first use and then owned by the chain: launches that overlap on
+ * one workspace race) and must all be resident at once (checked). Each hand-off wait gives up
+ * after `spin_limit` polls, sets the workspace's error word (llmserve_decode_chain_error) and
+ * lets the grid finish. No counterpart in the reference.
  */
 int64_t llmserve_decode_chain_workspace_bytes(int64_t H, int64_t I);
 int llmserve_decode_chain(
-    const float* attn, const float* x_in, const int64_t* ids, const float* embed, int64_t vocab,
+    const float* q_in, const int8_t* attn_k_cache, const int8_t* attn_v_cache,
+    const float* attn_k_scale, const float* attn_v_scale, const float* q_mult, float scale,
+    const float* x_in, const int64_t* ids, const float* embed, int64_t vocab,
     float* x_out, float* h_out, const uint8_t* o_nib, const float* o_s, const float* o_z,
     const float* o_inv, const float* post_w, const uint8_t* gu_nib, const float* gu_s,
     const float* gu_z, const float* gu_inv, const uint8_t* dn_nib, const float* dn_s,

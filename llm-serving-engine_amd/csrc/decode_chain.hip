@@ -1,15 +1,18 @@
-// The linear chain of one decoder layer for a decode batch of at most 4 sequences, as ONE
-// persistent launch: the layer's o_proj, residual add + post-attention RMSNorm, gate_up and
-// silu * up, down_proj, residual add + the next layer's input RMSNorm, then the next layer's
-// qkv projection with its q/k RMSNorm, RoPE at each sequence's position and the int8 K/V
-// write (the reference's _forward_fused order, models/transformer.py:157-189, with the int4
-// linears of quant.py:134-151 and the cache write of attention.py:241-246). At one to four
-// rows each of these matrices is 1-3 MB: a kernel per op spends its time in launch and
-// dependent-latency gaps (~3 us each, eight per layer), not in HBM. Here the weights of every
-// stage are requested when the kernel starts, and the stages hand their small activation
-// vectors to each other inside the launch.
+// One decoder layer for a decode batch of at most 4 sequences, as ONE persistent launch: the
+// layer's attention over its int8 paged cache, o_proj, residual add + post-attention RMSNorm,
+// gate_up and silu * up, down_proj, residual add + the next layer's input RMSNorm, then the
+// next layer's qkv projection with its q/k RMSNorm, RoPE at each sequence's position and the
+// int8 K/V write (the reference's _forward_fused order, models/transformer.py:157-189, with
+// the decode attention of paged_attention.cpp:191-420, the int4 linears of quant.py:134-151
+// and the cache write of attention.py:241-246). At one to four rows each of these matrices is
+// 1-3 MB: a kernel per op spends its time in launch and dependent-latency gaps (~3 us each,
+// ten per layer), not in HBM. Here the weights of every stage are requested as soon as a
+// workgroup is free, and the stages hand their small vectors to each other inside the launch.
 //
 // Workgroups (512 threads = 8 wavefronts, one per CU, all resident at once):
+//   attention first:        workgroup w < M R runs one range of Q tokens of one row (a
+//                           wavefront per kv head), the last M n_q workgroups merge one
+//                           (row, query head) each (see "this layer's attention" below);
 //   MLP groups w < H / 8:   o_proj rows 8w..8w+7 (a wavefront per row), gate rows and up rows
 //                           of channels [C w, C (w + 1)) (C = I / (H / 8)), down rows
 //                           8w..8w+7; for the last layer also those residual channels and
@@ -20,21 +23,25 @@
 // Hand-offs: a producer stores each output value as one 8-byte word (float bits | launch tag
 // << 32) with a device-scope store; a consumer polls the words it needs with device-scope
 // loads until every one carries this launch's tag, so data and readiness travel together and
-// no counter or fence is needed. Three hand-offs per layer: o_proj out (ex1, H words per row),
-// silu * up (ex2, I words), down_proj out (ex3, H words). Every wait is bounded by
-// `spin_limit` polls; a wait that runs out sets the error word and the workgroup returns, so
-// the grid always drains. The launch tag is ctl[0] + 1 (never 0, the value of cleared words);
-// the last workgroup to finish (ctl[1] counts them) resets the count and advances ctl[0], so
-// the next launch on the stream uses a new tag. The caller's workspace holds ctl and the three
-// exchange buffers; launches that overlap on one workspace race.
+// no counter or fence is needed. Five hand-offs per layer: attention partials (exa), merged
+// attention rows (exb, Kq words per row), o_proj out (ex1, H words), silu * up (ex2, I words),
+// down_proj out (ex3, H words). Every wait is bounded by `spin_limit` polls; a wait that runs
+// out sets the error word and the workgroup returns, so the grid always drains. The launch tag
+// is ctl[0] + 1 (never 0, the value of cleared words); the last workgroup to finish (ctl[1]
+// counts them) resets the count and advances ctl[0], so the next launch on the stream uses a
+// new tag. The caller's workspace holds ctl and the exchange buffers; launches that overlap
+// on one workspace race.
 //
 // Layouts: int4 weights are the reference buffers (nibbles [N, K/2], even channel low;
 // group scale / zero [N, K/128]); x' = x * inv_act_scale is staged in LDS with each
 // 32-channel slice's eight 16-byte chunks rotated by the slice index (conflict-free
 // ds_read_b128); a lane holds 16-byte weight chunks (32 channels of one group) and computes
 // s * sum x'q + (z - 8 s) * sum x' (int8_gemv.cpp:48-52), partial sums reduced with DPP.
+#include <cmath>
+
 #include "common.h"
 #include "kv_quant.h"
+#include "paged_core.h"
 #include "rope.h"
 
 namespace {
@@ -51,12 +58,27 @@ constexpr int kMaxKq = 2048;  // o_proj input: one 64-chunk wavefront
 constexpr int kMaxI = 4096;   // down_proj input: at most two chunks per lane
 constexpr int kMaxGuPass = 4; // gate_up rows per workgroup <= 16 * kMaxGuPass
 constexpr int kHeadPasses = kHeadDim / (2 * kWaves);  // 8: two qkv rows per wavefront per pass
+constexpr int kGqa = 2;                   // query heads per kv head
+constexpr int kPartWords = kHeadDim + 2;  // an attention partial: running max, sum, accumulator
+constexpr int kMaxRanges = 128;           // attention ranges per row
+constexpr int kMinRange = 64;             // tokens per attention range, at least
+constexpr int kAccPerWave = kMaxRanges / kWaves;  // partials a merge wavefront accumulates
+// words of the attention partials: [kMaxRows][kMaxRanges][kWaves][kGqa][kPartWords]
+constexpr int64_t kExaWords = static_cast<int64_t>(kMaxRows) * kMaxRanges * kWaves * kGqa * kPartWords;
+
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct ChainArgs {
-  // residual stream, attention output, outputs
-  const float* attn;   // [M, Kq] this layer's attention output (MLP part)
+  // this layer's attention (MLP part): q [M, nq, D] as the previous launch wrote it, the
+  // layer's int8 cache and the smoothing product q_mult [nq, D] (nullable)
+  const float* q_in;
+  const int8_t *akc, *avc;
+  const float *aks, *avs;
+  const float* q_mult;
+  float qscale;     // softmax scale * log2(e)
+  int bs_shift;     // log2(bs)
+  // residual stream and outputs
   const float* x_in;   // [M, H] residual stream before this layer's o_proj (MLP part)
   const int64_t* ids;  // [M] token ids: embedding mode (no MLP part)
   const float* embed;  // [V, H]
@@ -87,6 +109,8 @@ struct ChainArgs {
   float *ks, *vs;
   // hand-offs and control words
   uint64_t *ex1, *ex2, *ex3;  // [kCopies][kMaxRows][H], [..][I], [..][H] words
+  uint64_t* exa;              // attention partials, kExaWords words
+  uint64_t* exb;              // merged attention rows [kCopies][kMaxRows][Kq] words
   uint32_t* ctl;              // tag base, finished workgroups, error
   uint32_t spin_limit;
   int M, H, Kq, I, nq, nk;
@@ -103,6 +127,8 @@ struct ChainArgs {
 // load (each 8-byte word is stored whole, so each half of a load is one word as stored).
 
 constexpr int kCopies = 8;
+// words of the merged attention rows: [kCopies][kMaxRows][kMaxKq]
+constexpr int64_t kExbWords = static_cast<int64_t>(kCopies) * kMaxRows * kMaxKq;
 constexpr int kPolicyDevice = 16;  // buffer-load cache policy: device scope (sc1)
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
@@ -147,6 +173,37 @@ __device__ bool take(__amdgpu_buffer_rsrc_t src, uint32_t need, uint32_t tag, co
     }
     __builtin_amdgcn_s_sleep(1);
   }
+}
+
+// True in every thread when `v` is true in any thread of the block. `slots` holds kWaves ints
+// of LDS that no other code uses. (The runtime's __syncthreads_or reads the workgroup size
+// from the dispatch packet with a global load on every call: a memory round trip on the
+// critical path after each hand-off.)
+__device__ __forceinline__ bool block_any(bool v, int* slots) {
+  const bool w = __builtin_amdgcn_ballot_w64(v) != 0;
+  __syncthreads();  // the previous call's reads are done
+  if (threadIdx.x % kWave == 0) slots[threadIdx.x / kWave] = w;
+  __syncthreads();
+  int r = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) r |= slots[i];
+  return r != 0;
+}
+
+// A long wait, thinned: wavefront 0 alone polls a few sentinel pairs (take's `need` and
+// `off` for its lanes) while the other wavefronts wait at the barrier; the full take that
+// follows then normally completes in its first round. Device-scope polls are served beyond
+// the XCD's L2, so a whole workgroup polling every word it needs through a wait of several
+// microseconds puts megabytes per round on the fabric, in the way of the loads of the
+// workgroups still computing. (Polling the sentinels faster, several rounds in flight, was
+// measured slower for the same reason.) Returns the block-wide verdict (false: the error word
+// is set).
+template <int N, typename Off>
+__device__ bool gate(__amdgpu_buffer_rsrc_t src, uint32_t need, uint32_t tag, const ChainArgs& a,
+                     Off off, int* flags) {
+  bool ok = true;
+  if (threadIdx.x < kWave) ok = take<N>(src, need, tag, a, off, [](int, float, float) {});
+  return !block_any(!ok, flags);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t replica(const uint64_t* base, int64_t words) {
@@ -277,21 +334,6 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
 }
 
-// True in every thread when `v` is true in any thread of the block. `slots` holds kWaves ints
-// of LDS that no other code uses. (The runtime's __syncthreads_or reads the workgroup size
-// from the dispatch packet with a global load on every call: a memory round trip on the
-// critical path after each hand-off.)
-__device__ __forceinline__ bool block_any(bool v, int* slots) {
-  const bool w = __builtin_amdgcn_ballot_w64(v) != 0;
-  __syncthreads();  // the previous call's reads are done
-  if (threadIdx.x % kWave == 0) slots[threadIdx.x / kWave] = w;
-  __syncthreads();
-  int r = 0;
-#pragma unroll
-  for (int i = 0; i < kWaves; ++i) r |= slots[i];
-  return r != 0;
-}
-
 // Residual rows: thread t holds channels 2t and 2t + 1 of rows m < MT.
 template <int MT>
 struct Resid {
@@ -392,6 +434,181 @@ __device__ __forceinline__ uint32_t launch_tag(const ChainArgs& a) {
 // Bits 0 .. n-1.
 __device__ __forceinline__ uint32_t low_bits(int n) { return n >= 32 ? ~0u : (1u << n) - 1u; }
 
+// ---- this layer's attention -----------------------------------------------------------------
+// The rows' contexts are cut into ranges of Q tokens, R per row (Q from the longest context,
+// the same in every workgroup): workgroup w < M R runs range j = w % R of row m = w / R,
+// tokens [j Q, (j + 1) Q), its wavefront h < nk taking kv head h (the split-context decode of
+// paged_core.h: a range's eight wavefronts read each token's whole row of kv heads). Each
+// (m, j, h, g) leaves a partial of kPartWords tagged words (running max, sum, accumulator) in
+// exa. Ranges past a row's context write nothing: the merge reads only the ceil(ctx / Q)
+// ranges with tokens.
+
+__device__ __forceinline__ int64_t part_word(const ChainArgs& a, int m, int j, int h, int g) {
+  return ((((static_cast<int64_t>(m) * kMaxRanges + j) * a.nk + h) * kGqa) + g) * kPartWords;
+}
+
+__device__ __forceinline__ int row_context(const ChainArgs& a, int m) {
+  const int64_t cap = a.max_blocks * a.bs;
+  const int64_t c = uniform64(a.ctx[m]);
+  return static_cast<int>(c < 0 ? 0 : (c > cap ? cap : c));
+}
+
+// Q: at least kMinRange tokens, at most floor(grid / M) ranges per row (so that the M R
+// ranges have a workgroup each) and at most kMaxRanges; a multiple of 16.
+struct AttnPlan {
+  int Q, R;
+};
+
+__device__ __forceinline__ AttnPlan attn_plan(const ChainArgs& a) {
+  int mx = 0;
+  for (int m = 0; m < a.M; ++m) mx = max(mx, row_context(a, m));
+  const int per = a.grid / a.M;
+  int q = max(kMinRange, max((mx + per - 1) / per, (mx + kMaxRanges - 1) / kMaxRanges));
+  q = (q + 15) & ~15;
+  return {q, (mx + q - 1) / q};
+}
+
+__device__ void attention_range(const ChainArgs& a, const AttnPlan& pl, uint32_t tag) {
+  const int w = blockIdx.x;
+  if (w >= a.M * pl.R) return;
+  const int m = w / pl.R, j = w % pl.R;
+  const int h = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (h >= a.nk) return;
+  const int ctx = row_context(a, m);
+  const int t0 = j * pl.Q;
+  if (t0 >= ctx) return;
+  const int t1 = min(t0 + pl.Q, ctx);
+  DecodeArgs d{};
+  d.q = a.q_in;
+  d.kc = a.akc;
+  d.vc = a.avc;
+  d.ks = a.aks;
+  d.vs = a.avs;
+  d.bt = a.bt;
+  d.row_tab = nullptr;
+  d.cl = a.ctx;
+  d.q_mult = a.q_mult;
+  d.num_slots = a.num_slots;
+  d.B = a.M;
+  d.Hq = a.nq;
+  d.Hk = a.nk;
+  d.max_blocks = static_cast<int>(a.max_blocks);
+  d.bs = static_cast<int>(a.bs);
+  d.bs_shift = a.bs_shift;
+  d.qscale = a.qscale;
+  SegState<kGqa> st;
+  segment_state<int8_t, kHeadDim, kGqa, true, true>(d, m, h, t0, t1, st);
+  constexpr int LPR = kHeadDim / 16;
+  const int r = lane / LPR, seg = lane % LPR;
+  if (r == 0) {
+#pragma unroll
+    for (int g = 0; g < kGqa; ++g) {
+      uint64_t* p = a.exa + part_word(a, m, j, h, g) + 2 + seg * 16;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint64_t wv = (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, st.acc[g][i]);
+        __hip_atomic_store(p + i, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (lane < kGqa) {
+    const float mm = lane == 0 ? st.m[0] : st.m[1];
+    const float ll = lane == 0 ? st.lt[0] : st.lt[1];
+    uint64_t* p = a.exa + part_word(a, m, j, h, lane);
+    __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, mm),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 1, (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, ll),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Merge i = grid - 1 - w of (row m, query head qh), i < M nq, by all 8 wavefronts of workgroup
+// w (the last workgroups, whose own weights are needed last): wavefront 0 first waits for the
+// (max, sum) words of the row's np partials (the producers store them after the
+// accumulators), then every wavefront takes the (max, sum) words (lane p) and the
+// accumulators of partials v, v + 8, ... (wavefront v) in one polling round, and the merge is
+// the decode merge's (paged_decode.hip, merge_partials): M = max_p m_p, w_p = exp2(m_p - M) (0
+// where the sum is 0), out = (sum_p w_p acc_p) / (sum_p w_p l_p), the wavefronts' sums added
+// in wavefront order (a row without context gets NaN). The row goes to exb (all replicas) for
+// the o_proj stage. `red2` is 2 kThreads floats of LDS. Returns false when a wait ran out of
+// polls.
+__device__ bool merge_attention(const ChainArgs& a, const AttnPlan& pl, uint32_t tag, float* red2,
+                                int* flags) {
+  const int i = a.grid - 1 - static_cast<int>(blockIdx.x);
+  if (i < 0 || i >= a.M * a.nq) return true;
+  const int m = i / a.nq, qh = i % a.nq, h = qh / kGqa, g = qh % kGqa;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int ctx = row_context(a, m);
+  const int np = (ctx + pl.Q - 1) / pl.Q;
+  const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+      a.exa, 0, static_cast<int>(kExaWords * 8), 0x00020000);
+  // pairs 0, 1: (max, sum) of partials lane and lane + 64; pairs 2..: this lane's accumulator
+  // pair (dims 2 lane, 2 lane + 1) of partials wave + 8 t
+  const int64_t ml0 = part_word(a, m, lane, h, g) * 8;
+  const int64_t ml_step = part_word(a, 0, kWave, 0, 0) * 8;  // 64 partials further on
+  const uint32_t need_ml = (lane < np ? 1u : 0u) | (lane + kWave < np ? 2u : 0u);
+  if (!gate<2>(src, need_ml, tag, a, [=](int k) { return ml0 + k * ml_step; }, flags))
+    return false;
+  constexpr int N = 2 + kAccPerWave;
+  uint32_t need = need_ml;
+  for (int t = 0; t < kAccPerWave; ++t)
+    if (wave + kWaves * t < np) need |= 1u << (2 + t);
+  float pm[2] = {kNegBig, kNegBig}, ps[2] = {0.f, 0.f};
+  float av[kAccPerWave][2] = {};
+  const bool ok = take<N>(
+      src, need, tag, a,
+      [&](int k) {
+        if (k < 2) return ml0 + k * ml_step;
+        return (part_word(a, m, wave + kWaves * (k - 2), h, g) + 2 + 2 * lane) * 8;
+      },
+      [&](int k, float v0, float v1) {
+        if (k < 2) {
+          pm[k] = v0;
+          ps[k] = v1;
+        } else {
+          av[k - 2][0] = v0;
+          av[k - 2][1] = v1;
+        }
+      });
+  float mx = fmaxf(pm[0], pm[1]);
+  mx = lsh::wave_max_from<1>(mx);
+  float wt[2], L = 0.f;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    wt[k] = ps[k] == 0.f ? 0.f : __builtin_amdgcn_exp2f(pm[k] - mx);
+    L += wt[k] * ps[k];
+  }
+  L = lsh::group_sum<kWave>(L);
+  float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int t = 0; t < kAccPerWave; ++t) {
+    const int p = wave + kWaves * t;
+    const float wp = __shfl(p < kWave ? wt[0] : wt[1], p % kWave, kWave);
+    if (p < np) {
+      o0 += wp * av[t][0];
+      o1 += wp * av[t][1];
+    }
+  }
+  __syncthreads();
+  red2[(wave * kWave + lane) * 2] = o0;
+  red2[(wave * kWave + lane) * 2 + 1] = o1;
+  __syncthreads();
+  if (wave == 0) {
+    float s0 = red2[lane * 2], s1 = red2[lane * 2 + 1];
+    for (int v = 1; v < kWaves; ++v) {
+      s0 += red2[(v * kWave + lane) * 2];
+      s1 += red2[(v * kWave + lane) * 2 + 1];
+    }
+    const float inv = np > 0 ? 1.f / L : __builtin_nanf("");
+    const int64_t s = static_cast<int64_t>(kMaxRows) * a.Kq;
+    const int64_t at = static_cast<int64_t>(m) * a.Kq + qh * kHeadDim + 2 * lane;
+    put(a.exb, s, at, np > 0 ? s0 * inv : inv, tag);
+    put(a.exb, s, at + 1, np > 0 ? s1 * inv : inv, tag);
+  }
+  __syncthreads();
+  return ok;
+}
+
 // ---- the two kinds of workgroup ----------------------------------------------------------------
 
 template <int MT>
@@ -407,13 +624,19 @@ __device__ void mlp_group(const ChainArgs& a, float* xs, float* cs, float* rows,
   const int64_t s1 = static_cast<int64_t>(kMaxRows) * H, s2 = static_cast<int64_t>(kMaxRows) * I;
   constexpr int kPairs = kMaxI / 2 / kThreads;  // down-input word pairs per thread per row
 
-  // 1. o_proj's weights and the attention rows first (the first stage waits only for them),
-  //    then gate_up's and down's weights, the residual rows and every small vector a later
-  //    stage needs, so that no stage after a hand-off waits for memory
+  constexpr int kOPairs = kMaxKq / 2 / kThreads;  // o_proj-input word pairs per thread per row
+
+  // 1. every weight and small vector a stage needs, so that no stage after a hand-off waits
+  //    for memory
   const int orow = 8 * w + wave;
   const Chunk fo = fetch(a.o_nib, a.o_s, a.o_z, Kq, orow, lane, lane < Kq / 32);
-  Staged<MT> st;
-  stage_load(st, a.attn, a.o_inv, Kq, M);
+  float2 o_inv[kOPairs];
+#pragma unroll
+  for (int i = 0; i < kOPairs; ++i) {
+    const int pr = static_cast<int>(threadIdx.x) + i * kThreads;  // channels 2pr, 2pr + 1
+    o_inv[i] = (a.o_inv && 2 * pr < Kq) ? *reinterpret_cast<const float2*>(a.o_inv + 2 * pr)
+                                        : make_float2(1.f, 1.f);
+  }
   Chunk fg[kMaxGuPass];
 #pragma unroll
   for (int p = 0; p < kMaxGuPass; ++p) {
@@ -436,10 +659,45 @@ __device__ void mlp_group(const ChainArgs& a, float* xs, float* cs, float* rows,
                                          : make_float2(1.f, 1.f);
   }
   const uint32_t tag = launch_tag(a);
-  stage_store(st, xs, cs, Kq);
-  __syncthreads();
 
-  // 2. o_proj row 8w + wave -> ex1
+  // 2. the merged attention rows times o_proj's inv -> LDS (xoff) with their chunk sums
+  {
+    uint32_t need = 0;
+#pragma unroll
+    for (int i = 0; i < MT * kOPairs; ++i)
+      if (i / kOPairs < M && 2 * (static_cast<int>(threadIdx.x) + (i % kOPairs) * kThreads) < Kq)
+        need |= 1u << i;
+    const int64_t sb = static_cast<int64_t>(kMaxRows) * Kq;
+    const __amdgpu_buffer_rsrc_t rb = replica(a.exb, sb);
+    // sentinels: the first pair of each merged head row (lane i: row i / nq, head i % nq)
+    const int soff = ((lane / a.nq) * Kq + (lane % a.nq) * kHeadDim) * 8;
+    if (!gate<1>(rb, lane < M * a.nq ? 1u : 0u, tag, a, [=](int) { return soff; }, flags))
+      return finish(a);
+    const bool ok = take<MT * kOPairs>(
+        rb, need, tag, a,
+        [&](int i) {
+          return ((i / kOPairs) * Kq + 2 * (static_cast<int>(threadIdx.x) + (i % kOPairs) * kThreads)) * 8;
+        },
+        [&](int i, float v0, float v1) {
+          const int k = 2 * (static_cast<int>(threadIdx.x) + (i % kOPairs) * kThreads);
+          const float2 iv = o_inv[i % kOPairs];
+          *reinterpret_cast<float2*>(xs + (i / kOPairs) * Kq + xoff(k)) =
+              a.o_inv ? make_float2(__fmul_rn(v0, iv.x), __fmul_rn(v1, iv.y)) : make_float2(v0, v1);
+        });
+    if (block_any(!ok, flags)) return finish(a);
+#pragma unroll
+    for (int i = 0; i < MT * kOPairs; ++i) {
+      const int pr = static_cast<int>(threadIdx.x) + (i % kOPairs) * kThreads;
+      const bool in = (need >> i) & 1u;
+      float2 v = make_float2(0.f, 0.f);
+      if (in) v = *reinterpret_cast<const float2*>(xs + (i / kOPairs) * Kq + xoff(2 * pr));
+      const float sum = lsh::group_sum<16>(v.x + v.y);
+      if (in && pr % 16 == 0) cs[(i / kOPairs) * (Kq >> 5) + (pr >> 4)] = sum;
+    }
+    __syncthreads();
+  }
+
+  // 3. o_proj row 8w + wave -> ex1
   {
     float v[MT];
     chunk_terms<MT>(fo, lane, xs, cs, Kq, v);
@@ -450,7 +708,7 @@ __device__ void mlp_group(const ChainArgs& a, float* xs, float* cs, float* rows,
     }
   }
 
-  // 3. x += o (all channels, all rows), post-attention norm times gate_up's inv -> LDS
+  // 4. x += o (all channels, all rows), post-attention norm times gate_up's inv -> LDS
   {
     float o[MT][2];
     const bool ok = take<MT>(
@@ -470,7 +728,7 @@ __device__ void mlp_group(const ChainArgs& a, float* xs, float* cs, float* rows,
     __syncthreads();
   }
 
-  // 4. gate_up rows (16 per pass), silu(gate) * up of the workgroup's C channels -> ex2
+  // 5. gate_up rows (16 per pass), silu(gate) * up of the workgroup's C channels -> ex2
   {
 #pragma unroll
     for (int p = 0; p < kMaxGuPass; ++p) {
@@ -492,7 +750,7 @@ __device__ void mlp_group(const ChainArgs& a, float* xs, float* cs, float* rows,
     }
   }
 
-  // 5. down_proj row 8w + wave over the I channels of silu * up -> ex3
+  // 6. down_proj row 8w + wave over the I channels of silu * up -> ex3
   {
     uint32_t need = 0;
 #pragma unroll
@@ -534,7 +792,7 @@ __device__ void mlp_group(const ChainArgs& a, float* xs, float* cs, float* rows,
     }
   }
 
-  // 6. the last layer: x += down, the residual channels 8w..8w+7 and their final norm
+  // 7. the last layer: x += down, the residual channels 8w..8w+7 and their final norm
   if (a.head_groups == 0) {
     float dv[MT][2];
     const bool ok = take<MT>(
@@ -629,8 +887,14 @@ __device__ void head_group(const ChainArgs& a, float* xs, float* cs, float* out,
     load_rows(a.x_in, H, M, x);
     float dv[MT][2], ov[MT][2];
     // o_proj's hand-off completes long before down_proj's: it is taken first, while down_proj
-    // still runs (taken second, it would add a poll round trip after the last hand-off)
-    bool ok = take<MT>(
+    // still runs (taken second, it would add a poll round trip after the last hand-off). The
+    // wait for it spans this layer's attention: gated on one pair per MLP group (the first two
+    // rows of group w, written by its wavefronts 0 and 1, in the last sequence row).
+    const uint32_t need = (lane < a.mlp_groups ? 1u : 0u) | (lane + kWave < a.mlp_groups ? 2u : 0u);
+    const int off0 = ((M - 1) * H + 8 * lane) * 8;  // bytes; the next sentinel 64 groups on
+    bool ok = gate<2>(replica(a.ex1, s1), need, tag, a,
+                      [=](int k) { return off0 + k * (8 * kWave * 8); }, flags);
+    ok = ok && take<MT>(
         replica(a.ex1, s1), k0 < H ? low_bits(M) : 0u, tag, a,
         [&](int r) { return (r * H + k0) * 8; },
         [&](int r, float v0, float v1) {
@@ -723,6 +987,15 @@ __global__ __launch_bounds__(kThreads) void decode_chain_kernel(ChainArgs a) {
   __shared__ __align__(16) float rows[kHeadDim * MT];
   __shared__ float red[kWaves];
   __shared__ int flags[kWaves];
+  if (a.mlp_groups > 0) {
+    // this layer's attention first (before any workgroup requests its weights): its ranges,
+    // then the merges of the last workgroups. The tag is read with the contexts, its round
+    // trip overlapping theirs.
+    const uint32_t tag = launch_tag(a);
+    const AttnPlan pl = attn_plan(a);
+    attention_range(a, pl, tag);
+    if (block_any(!merge_attention(a, pl, tag, xs, flags), flags)) return finish(a);
+  }
   if (static_cast<int>(blockIdx.x) < a.mlp_groups)
     mlp_group<MT>(a, xs, cs, rows, red, flags);
   else
@@ -749,13 +1022,18 @@ int launch_chain(const ChainArgs& a, int grid, hipStream_t st) {
 
 }  // namespace
 
+// Workspace words: control, the three linear hand-offs (kCopies replicas each), the merged
+// attention rows (kCopies replicas) and the attention partials.
+
 extern "C" int64_t llmserve_decode_chain_workspace_bytes(int64_t H, int64_t I) {
   if (H <= 0 || I <= 0) return 0;
-  return 256 + static_cast<int64_t>(kCopies) * kMaxRows * (2 * H + I) * 8;
+  return 256 + (static_cast<int64_t>(kCopies) * kMaxRows * (2 * H + I) + kExbWords + kExaWords) * 8;
 }
 
 extern "C" int llmserve_decode_chain(
-    const float* attn, const float* x_in, const int64_t* ids, const float* embed, int64_t vocab,
+    const float* q_in, const int8_t* attn_k_cache, const int8_t* attn_v_cache,
+    const float* attn_k_scale, const float* attn_v_scale, const float* q_mult, float scale,
+    const float* x_in, const int64_t* ids, const float* embed, int64_t vocab,
     float* x_out, float* h_out, const uint8_t* o_nib, const float* o_s, const float* o_z,
     const float* o_inv, const float* post_w, const uint8_t* gu_nib, const float* gu_s,
     const float* gu_z, const float* gu_inv, const uint8_t* dn_nib, const float* dn_s,
@@ -767,7 +1045,7 @@ extern "C" int llmserve_decode_chain(
     float* k_scale, float* v_scale, int64_t num_slots, int64_t M, int64_t H, int64_t I,
     int64_t n_q, int64_t n_k, int64_t head_dim, int64_t group_size, float eps, void* workspace,
     int64_t workspace_bytes, int64_t spin_limit, void* stream) {
-  const bool mlp = attn != nullptr, next = qkv_nib != nullptr;
+  const bool mlp = q_in != nullptr, next = qkv_nib != nullptr;
   LSH_CHECK(M >= 1 && M <= kMaxRows, "decode_chain: 1 to %d rows (got %lld)", kMaxRows, (long long)M);
   LSH_CHECK(head_dim == kHeadDim && group_size == kGroup,
             "decode_chain: head_dim and group_size must be 128 (got %lld, %lld)",
@@ -793,6 +1071,25 @@ extern "C" int llmserve_decode_chain(
     LSH_CHECK(x_in && o_nib && o_s && o_z && post_w && gu_nib && gu_s && gu_z && dn_nib && dn_s &&
                   dn_z && next_w,
               "decode_chain: null MLP pointer");
+    // this layer's attention: a wavefront per kv head, kGqa query heads each, steps of 8 slot
+    // rows inside one block, 32-bit offsets into the caches, a merge workgroup per query head
+    LSH_CHECK(attn_k_cache && attn_v_cache && attn_k_scale && attn_v_scale && context_lens &&
+                  block_tables,
+              "decode_chain: null attention pointer");
+    LSH_CHECK(n_q == kGqa * n_k && n_k <= kWaves,
+              "decode_chain: the fused attention needs n_q = %d n_k and n_k <= %d (got %lld, %lld)",
+              kGqa, kWaves, (long long)n_q, (long long)n_k);
+    LSH_CHECK(block_size >= 8 && (block_size & (block_size - 1)) == 0,
+              "decode_chain: block_size %lld must be a power of two >= 8", (long long)block_size);
+    LSH_CHECK(max_blocks >= 1 && max_blocks * block_size < (int64_t{1} << 31),
+              "decode_chain: block tables of %lld x %lld tokens", (long long)max_blocks,
+              (long long)block_size);
+    LSH_CHECK(num_slots >= block_size && num_slots * n_k * head_dim < (int64_t{1} << 32),
+              "decode_chain: KV cache of %lld slots not addressable with 32-bit offsets",
+              (long long)num_slots);
+    LSH_CHECK(M * n_q <= mlp_groups + (next ? n_q + 2 * n_k : 0),
+              "decode_chain: %lld attention merges do not fit the grid", (long long)(M * n_q));
+    LSH_CHECK(std::isfinite(scale) && scale > 0.f, "decode_chain: bad softmax scale");
   } else {
     LSH_CHECK(ids && embed && vocab > 0, "decode_chain: the embedding mode needs ids and embed");
   }
@@ -810,13 +1107,21 @@ extern "C" int llmserve_decode_chain(
             "decode_chain: workspace of %lld bytes needed",
             (long long)llmserve_decode_chain_workspace_bytes(H, I));
   auto al = [](const void* p) { return p == nullptr || lsh::aligned16(p); };
-  LSH_CHECK(al(attn) && al(x_in) && al(embed) && al(o_nib) && al(gu_nib) && al(dn_nib) &&
+  LSH_CHECK(al(q_in) && al(q_mult) && al(attn_k_cache) && al(attn_v_cache) && al(x_in) && al(embed) && al(o_nib) && al(gu_nib) && al(dn_nib) &&
                 al(qkv_nib) && al(o_inv) && al(gu_inv) && al(dn_inv) && al(qkv_inv) &&
                 al(post_w) && al(next_w),
             "decode_chain: weights, activations and norm weights must be 16-byte aligned");
 
   ChainArgs a{};
-  a.attn = attn;
+  a.q_in = q_in;
+  a.akc = attn_k_cache;
+  a.avc = attn_v_cache;
+  a.aks = attn_k_scale;
+  a.avs = attn_v_scale;
+  a.q_mult = q_mult;
+  a.qscale = scale * kLog2e;
+  a.bs_shift = 0;
+  while ((int64_t{1} << a.bs_shift) < block_size) ++a.bs_shift;
   a.x_in = x_in;
   a.ids = ids;
   a.embed = embed;
@@ -862,6 +1167,8 @@ extern "C" int llmserve_decode_chain(
   a.ex1 = reinterpret_cast<uint64_t*>(ws + 256);  // kCopies replicas of each
   a.ex2 = a.ex1 + static_cast<int64_t>(kCopies) * kMaxRows * H;
   a.ex3 = a.ex2 + static_cast<int64_t>(kCopies) * kMaxRows * I;
+  a.exb = a.ex3 + static_cast<int64_t>(kCopies) * kMaxRows * H;
+  a.exa = a.exb + kExbWords;
   a.spin_limit = static_cast<uint32_t>(spin_limit < 0 ? 0 : (spin_limit > 0x7fffffff ? 0x7fffffff : spin_limit));
   a.M = static_cast<int>(M);
   a.H = static_cast<int>(H);

@@ -100,11 +100,12 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
     "llmserve_decode_chain_workspace_bytes": (_I64, [_I64, _I64]),
     "llmserve_decode_chain": (
         _I32,
-        # attn, x_in, ids, embed, vocab, x_out, h_out; 22 weight / norm / RoPE pointers;
-        # max_pos, context_lens, block_tables, max_blocks, block_size, k_smooth, q_out, caches
-        # and scales, num_slots; M, H, I, n_q, n_k, head_dim, group_size; eps, workspace,
-        # workspace_bytes, spin_limit, stream
-        [_P, _P, _P, _P, _I64, _P, _P] + [_P] * 22
+        # q_in, this layer's caches and scales, q_mult, scale; x_in, ids, embed, vocab, x_out,
+        # h_out; 22 weight / norm / RoPE pointers; max_pos, context_lens, block_tables,
+        # max_blocks, block_size, k_smooth, q_out, the next layer's caches and scales,
+        # num_slots; M, H, I, n_q, n_k, head_dim, group_size; eps, workspace, workspace_bytes,
+        # spin_limit, stream
+        [_P] * 6 + [_F32] + [_P, _P, _P, _I64, _P, _P] + [_P] * 22
         + [_I64, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64] + [_I64] * 7
         + [_F32, _P, _I64, _I64, _P],
     ),

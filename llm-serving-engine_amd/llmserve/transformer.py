@@ -189,7 +189,18 @@ class QuantCausalLM(nn.Module):
         if not (I % 512 == 0 and I <= 4096 and I % (H // 8) == 0):
             return False
         C = I // (H // 8)
-        return C % 8 == 0 and C <= 32
+        return (C % 8 == 0 and C <= 32 and cfg.num_attention_heads == 2 * cfg.num_key_value_heads
+                and cfg.num_key_value_heads <= 8)
+
+    @staticmethod
+    def _chain_attn_ok(kv_layers, block_size: int, block_tables: torch.Tensor) -> bool:
+        """The chain's fused attention: int8 caches addressable with 32-bit offsets, blocks of
+        a power of two >= 8 tokens."""
+        kc = kv_layers[0][0]
+        if not (hasattr(kc, "scale") and kc.data.dtype == torch.int8):
+            return False
+        return (block_size >= 8 and block_size & (block_size - 1) == 0
+                and kc.data.numel() < 2**32 and block_tables.shape[1] * block_size < 2**31)
 
     def chain_workspace(self) -> torch.Tensor:
         """The chain's hand-off workspace (zeroed once, then owned by the chain launches of
@@ -213,11 +224,12 @@ class QuantCausalLM(nn.Module):
                                                  ctypes.byref(err)))
         return err.value
 
-    def _chain(self, *, rows, x_out, attn=None, x_in=None, ids=None, layer=None, nxt=None,
-               h_out=None, q_out=None, caches=None, context_lens=None, block_tables=None,
-               block_size=16, spin_limit=None) -> None:
-        """One llmserve_decode_chain launch: layer ``layer``'s MLP half (None: embedding mode)
-        and ``nxt``'s qkv part (None: the last layer, writing ``h_out``)."""
+    def _chain(self, *, rows, x_out, q_in=None, attn_caches=None, x_in=None, ids=None,
+               layer=None, nxt=None, h_out=None, q_out=None, caches=None, context_lens=None,
+               block_tables=None, block_size=16, spin_limit=None) -> None:
+        """One llmserve_decode_chain launch: layer ``layer``'s attention (of ``q_in`` over
+        ``attn_caches``) and MLP half (None: embedding mode) and ``nxt``'s qkv part (None: the
+        last layer, writing ``h_out``). ``q_out`` must not be ``q_in``."""
         from llmserve._native import capi, check
 
         cfg = self.cfg
@@ -232,7 +244,15 @@ class QuantCausalLM(nn.Module):
         kc = vc = None
         if nxt is not None:
             kc, vc = caches
-        args = [p(attn), p(x_in), p(ids), p(self.embed), cfg.vocab_size, p(x_out), p(h_out)]
+        if layer is not None:
+            ak, av = attn_caches
+            args = [p(q_in), p(ak.data), p(av.data), p(ak.scale), p(av.scale), p(ak._q_mult),
+                    ctypes.c_float(self.scale)]
+            slots = ak.data.shape[0]
+        else:
+            args = [None] * 6 + [ctypes.c_float(self.scale)]
+            slots = kc.data.shape[0]
+        args += [p(x_in), p(ids), p(self.embed), cfg.vocab_size, p(x_out), p(h_out)]
         args += lin(layer.o_proj if layer else None)
         args += [p(layer.post_attention_layernorm) if layer else None]
         args += lin(layer.gate_up_proj if layer else None)
@@ -245,7 +265,7 @@ class QuantCausalLM(nn.Module):
                  block_size, p(kc.smooth) if kc is not None else None, p(q_out),
                  p(kc.data) if kc is not None else None, p(vc.data) if vc is not None else None,
                  p(kc.scale) if kc is not None else None, p(vc.scale) if vc is not None else None,
-                 kc.data.shape[0] if kc is not None else 0, rows, cfg.hidden_size,
+                 slots, rows, cfg.hidden_size,
                  cfg.intermediate_size, cfg.num_attention_heads, cfg.num_key_value_heads,
                  cfg.head_dim, self.group_size, ctypes.c_float(cfg.rms_norm_eps), p(ws), ws.numel(),
                  self.chain_spin_limit if spin_limit is None else spin_limit,
@@ -253,10 +273,10 @@ class QuantCausalLM(nn.Module):
         check(capi().llmserve_decode_chain(*args))
 
     def _forward_decode_chain(self, ids, context_lens, block_tables, kv_layers, block_size):
-        """forward_decode for 1..4 rows: an embedding + layer-0 qkv launch, then per layer the
-        paged decode and one chain launch (the last one writes the final norm's output)."""
+        """forward_decode for 1..4 rows: an embedding + layer-0 qkv launch, then one launch
+        per layer for its attention, linear chain and the next layer's qkv (the last one
+        writes the final norm's output)."""
         cfg = self.cfg
-        pa = load_paged_attention()
         B, H = ids.numel(), cfg.hidden_size
         nq, D = cfg.num_attention_heads, cfg.head_dim
         dev = self.embed.device
@@ -267,20 +287,17 @@ class QuantCausalLM(nn.Module):
                     context_lens=context_lens, block_tables=block_tables, block_size=block_size)
         h = None
         for i, L in enumerate(self.layers):
-            kc, vc = kv_layers[i]
-            attn = pa.paged_attention_decode_int8(q, kc.data, vc.data, kc.scale, vc.scale,
-                                                  block_tables, context_lens, block_size,
-                                                  self.scale, 0, kc._q_mult)
             nxt = self.layers[i + 1] if i + 1 < n else None
             x_new = torch.empty(B, H, device=dev)
-            q = torch.empty(B, nq, D, device=dev) if nxt is not None else None
+            q_new = torch.empty(B, nq, D, device=dev) if nxt is not None else None
             if nxt is None:
                 h = torch.empty(B, H, device=dev)
-            self._chain(rows=B, x_out=x_new, attn=attn.view(B, nq * D), x_in=x, layer=L, nxt=nxt,
-                        h_out=h, q_out=q, caches=kv_layers[i + 1] if nxt is not None else None,
+            self._chain(rows=B, x_out=x_new, q_in=q, attn_caches=kv_layers[i], x_in=x, layer=L,
+                        nxt=nxt, h_out=h, q_out=q_new,
+                        caches=kv_layers[i + 1] if nxt is not None else None,
                         context_lens=context_lens, block_tables=block_tables,
                         block_size=block_size)
-            x = x_new
+            x, q = x_new, q_new
         return h
 
     def _xfrag_ok(self, rows: int) -> bool:
@@ -329,7 +346,8 @@ class QuantCausalLM(nn.Module):
         position is ctx - 1); ``block_tables`` [B, max_blocks] int64 holds the blocks of every
         position up to ctx - 1; ``kv_layers`` is ``KVCache.layers`` with int8 ``QuantizedKV``
         pairs. Writes this token's K and V into the caches. No host synchronization."""
-        if self._chain_ok(ids.numel()) and ids.numel() <= self.chain_max_rows:
+        if (self._chain_ok(ids.numel()) and ids.numel() <= self.chain_max_rows
+                and self._chain_attn_ok(kv_layers, block_size, block_tables)):
             return self._forward_decode_chain(ids, context_lens, block_tables, kv_layers,
                                               block_size)
         cfg = self.cfg

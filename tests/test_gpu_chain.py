@@ -130,11 +130,12 @@ def test_chain_gives_up_without_poll_budget(gpu):
     nq, D = cfg.num_attention_heads, cfg.head_dim
     dev = torch.device("cuda")
     x = torch.randn(B, H, device=dev)
-    attn = torch.randn(B, nq * D, device=dev)
+    q_in = torch.randn(B, nq, D, device=dev)
     x_out = torch.empty(B, H, device=dev)
     q = torch.empty(B, nq, D, device=dev)
-    kw = dict(rows=B, attn=attn, x_in=x, layer=model.layers[0], nxt=model.layers[1], q_out=q,
-              caches=cache.layers[1], context_lens=runner.context_lens,
+    kw = dict(rows=B, q_in=q_in, attn_caches=cache.layers[0], x_in=x, layer=model.layers[0],
+              nxt=model.layers[1], q_out=q, caches=cache.layers[1],
+              context_lens=runner.context_lens,
               block_tables=runner.block_tables, block_size=BS)
     failed = 0
     for _ in range(20):  # one poll is rarely enough for all groups
@@ -152,6 +153,7 @@ def test_chain_gives_up_without_poll_budget(gpu):
 
 
 def test_chain_rejects_bad_geometry(gpu):
+    from llmserve.attention import QuantizedKV
     from llmserve.transformer import ModelConfig, QuantCausalLM
 
     cfg = ModelConfig(vocab_size=512, hidden_size=384, intermediate_size=1024,
@@ -159,7 +161,11 @@ def test_chain_rejects_bad_geometry(gpu):
                       head_dim=128, max_position_embeddings=256)
     m = QuantCausalLM(cfg, 128, seed=1)
     assert not m._chain_ok(1)  # I = 1024 is not a multiple of H / 8 = 48
+    kv = (QuantizedKV(64, 2, 128, "cuda"), QuantizedKV(64, 2, 128, "cuda"))
+    ctx = torch.ones(1, dtype=torch.long, device="cuda")
+    bt = torch.zeros(1, 4, dtype=torch.long, device="cuda")
     with pytest.raises(RuntimeError, match="intermediate size"):
         m._chain(rows=1, x_out=torch.empty(1, 384, device="cuda"),
-                 attn=torch.zeros(1, 512, device="cuda"), x_in=torch.zeros(1, 384, device="cuda"),
-                 layer=m.layers[0], h_out=torch.empty(1, 384, device="cuda"))
+                 q_in=torch.zeros(1, 4, 128, device="cuda"), attn_caches=kv,
+                 x_in=torch.zeros(1, 384, device="cuda"), layer=m.layers[0],
+                 h_out=torch.empty(1, 384, device="cuda"), context_lens=ctx, block_tables=bt)
