@@ -69,7 +69,7 @@ struct DecodeArgs {
   float* part_ml;   // [slots, G, 2]  (running max in log2 units, sum)
   float* part_acc;  // [slots, G, D]
   int64_t num_slots;
-  int64_t range;  // token-heads per work range; 0: max(ceil(T / W), kMinRange)
+  int64_t range;  // tokens per work range; 0: the balanced plan (paged_decode.hip)
   int B, Hq, Hk, max_blocks, bs, bs_shift;  // bs_shift = log2(bs), or -1
   int HB, NHG;  // kv heads per workgroup, head groups (Hk = HB * NHG)
   int W;        // decode workgroups (all resident)

@@ -1,19 +1,15 @@
 // int8-KV paged decode attention: the context split evenly over the GPU's wavefronts, an
 // online softmax per wavefront, and a merge of the sequences that were split.
 //
-// Work line: the kv heads form NHG groups of HB heads (HB = the largest divisor of Hk up to
-// 8). The (sequence b, head group hg, token t) triples, t fastest, laid end to end make a line
-// of T = NHG * sum_b ctx_b. The line is cut into ranges of Q tokens (Q = ceil(T / W) over the
-// W resident workgroups, but at least 64, so every SIMD streams the same number of cache rows
-// whatever the context lengths; or a caller-fixed Q). A workgroup holds HB wavefronts, one per kv head of
+// Work split: the kv heads form NHG groups of HB heads (HB = the largest divisor of Hk up to
+// 8). Each (sequence b, head group hg) unit is cut into ranges of at most Q tokens that never
+// straddle two units; Q is chosen so that the ranges fit the W resident workgroups (the work
+// plan below; or a caller-fixed range size). A workgroup holds HB wavefronts, one per kv head of
 // the group, which run the same tokens: together they read whole HB * D-byte pieces of every
-// slot row (all of it when HB = Hk), so the cache streams in long contiguous runs. A workgroup
-// runs its range as segments, one per (b, hg) the range touches. A segment that covers its
-// whole (b, hg) writes the output rows; the others write a partial (running max, sum, acc) per
-// head to slot ((b * NHG + hg) + j) * HB + head-in-group (j = range index; distinct for
-// distinct segments since the ranges of one (b, hg) have consecutive j and the next (b, hg)
-// starts at a j no smaller than the last one of this (b, hg)). The merge kernel combines the
-// partials of every split (b, hg).
+// slot row (all of it when HB = Hk), so the cache streams in long contiguous runs. A range that
+// is its unit's only one writes the output rows; the others write a partial (running max, sum,
+// acc) per head to slot j * HB + head-in-group (j = range index), and the merge kernel combines
+// the partials of every split unit.
 //
 // Lane layout inside a wavefront (D = head dim, LPR = D / 16 lanes per token row):
 //   lane = r * LPR + seg : row slot r of the RPW = 64 / LPR tokens of one step, dims
@@ -54,68 +50,203 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
   return v;
 }
 
-// Sum of the contexts of sequences [0, bend) (wave-uniform).
-__device__ int64_t tokens_before(const DecodeArgs& a, int bend) {
-  const int lane = threadIdx.x % kWave;
+// ---- the work plan ------------------------------------------------------------------------------
+// Ranges never straddle two (sequence b, head group hg) units: unit (b, hg) gets
+// n_b = ceil(ctx_b / Q) ranges, numbered unit by unit in (b, hg) order. With a caller's fixed
+// partition size P (the reference's partitions) Q = P and the ranges hold P tokens, the last
+// one the rest. The balanced default equalises the ranges of a unit (ceil(ctx_b / n_b) tokens
+// each) and takes Q between max(ceil(T / W), kMinRange), T = NHG * sum_b ctx_b, and
+// ceil(T / (W - units)) (which always fits: each unit rounds up by less than one range) so
+// that the R = NHG * sum_b n_b ranges fit the W resident workgroups: the lower end if it fits,
+// else the feasible end of kPlanSteps bisections. Every workgroup derives the same plan from
+// the contexts, with DPP / readlane reductions (no LDS crossbar round trips: the plan is on
+// every range's critical path). A range that started a second unit would pay that unit's
+// start-up (its context, then q and block ids, then the first K/V loads) as dependent round
+// trips in a saturated memory system, microseconds each: measured, ranges that crossed a
+// sequence boundary ended ~10 us after the others.
+constexpr uint32_t kMinRange = 64;
+constexpr int kPlanSteps = 5;
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {  // lanes without a source get 0
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROWS, 0xF, false));
+}
+
+// Inclusive prefix sum over the wavefront's lanes (row shifts, then row broadcasts).
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+  v += dpp_u32<0x111, 0xF>(v);  // row_shr:1
+  v += dpp_u32<0x112, 0xF>(v);  // row_shr:2
+  v += dpp_u32<0x114, 0xF>(v);  // row_shr:4
+  v += dpp_u32<0x118, 0xF>(v);  // row_shr:8
+  v += dpp_u32<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
+  v += dpp_u32<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
+// Sum over the wavefront (wave-uniform).
+__device__ __forceinline__ uint32_t wave_total_u32(uint32_t v) {
+  return __builtin_amdgcn_readlane(wave_scan_u32(v), kWave - 1);
+}
+
+// Max over the wavefront (wave-uniform): row mirrors, then the four rows' lanes.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  auto mx = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+  v = mx(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, true)));
+  v = mx(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4E, 0xF, 0xF, true)));
+  v = mx(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x141, 0xF, 0xF, true)));
+  v = mx(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x140, 0xF, 0xF, true)));
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return mx(mx(r0, r1), mx(r2, r3));
+}
+
+// Context of row b0 + lane (0 past B); contexts are below 2^31 (checked on the host).
+__device__ __forceinline__ uint32_t lane_ctx(const DecodeArgs& a, int b0) {
+  const int b = b0 + static_cast<int>(threadIdx.x % kWave);
+  return b < a.B ? static_cast<uint32_t>(seq_ctx(a, b)) : 0u;
+}
+
+__device__ __forceinline__ uint32_t ranges_of(uint32_t c, uint32_t Q) {
+  return c == 0 ? 0u : (c - 1) / Q + 1;
+}
+
+struct Plan {
+  uint32_t Q;   // range size bound (fixed partition: the range size)
+  int64_t R;    // ranges
+  bool fixed;
+  uint32_t c0;  // context of row `lane` when B <= 64 (held for the range lookups)
+};
+
+// NHG * sum_b ceil(ctx_b / Q) (wave-uniform). One row per lane up to 64 rows: with Q >= 64 the
+// 64 counts sum below 2^31.
+__device__ int64_t count_ranges(const DecodeArgs& a, uint32_t Q, uint32_t c0) {
+  if (a.B <= kWave && Q >= kMinRange)
+    return static_cast<int64_t>(wave_total_u32(ranges_of(c0, Q))) * a.NHG;
   int64_t s = 0;
-  for (int b0 = 0; b0 < bend; b0 += kWave) {
-    const int b = b0 + lane;
-    s += wave_sum_i64(b < bend ? seq_ctx(a, b) : 0);
+  for (int b0 = 0; b0 < a.B; b0 += kWave)
+    s += uniform64(wave_sum_i64(ranges_of(a.B <= kWave ? c0 : lane_ctx(a, b0), Q)));
+  return s * a.NHG;
+}
+
+__device__ Plan make_plan(const DecodeArgs& a) {
+  Plan p;
+  p.c0 = a.B <= kWave ? lane_ctx(a, 0) : 0u;
+  if (a.range > 0) {
+    p.Q = static_cast<uint32_t>(a.range < 0x7fffffff ? a.range : 0x7fffffff);
+    p.R = count_ranges(a, p.Q, p.c0);
+    p.fixed = true;
+    return p;
   }
-  return uniform64(s);
+  p.fixed = false;
+  int64_t tot = 0, nz = 0;
+  uint32_t mx = 0;
+  for (int b0 = 0; b0 < a.B; b0 += kWave) {
+    const uint32_t c = a.B <= kWave ? p.c0 : lane_ctx(a, b0);
+    tot += uniform64(wave_sum_i64(c));
+    nz += wave_total_u32(c != 0 ? 1u : 0u);
+    const uint32_t m = wave_max_u32(c);
+    mx = m > mx ? m : mx;
+  }
+  const int64_t T = tot * a.NHG, units = nz * a.NHG;
+  const int64_t even = (T + a.W - 1) / a.W;
+  uint32_t lo = even > kMinRange ? static_cast<uint32_t>(even < 0x7fffffff ? even : 0x7fffffff)
+                                 : kMinRange;
+  if (lo >= mx) {
+    p.Q = lo;  // every unit is one range
+  } else if (units >= a.W) {
+    p.Q = mx;  // the units alone fill the workgroups: one range each, workgroups loop
+  } else {
+    const int64_t f = (T + (a.W - units) - 1) / (a.W - units);
+    uint32_t hi = f < mx ? static_cast<uint32_t>(f) : mx;  // fits
+    if (hi < lo) hi = lo;
+    if (count_ranges(a, lo, p.c0) <= a.W) {
+      hi = lo;
+    } else {
+      for (int it = 0; it < kPlanSteps && lo + 1 < hi; ++it) {  // (lo infeasible, hi feasible)
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (count_ranges(a, mid, p.c0) <= a.W)
+          hi = mid;
+        else
+          lo = mid;
+      }
+    }
+    p.Q = hi;
+  }
+  p.R = count_ranges(a, p.Q, p.c0);
+  return p;
 }
 
-// Token-heads per work range over a line of T: the caller's size, else an equal share per
-// resident workgroup but at least kMinRange. A shorter range is one round of loads whose
-// latency the split cannot hide, and it only adds partials to merge: at one sequence of 2048
-// tokens, 8-token ranges (the plain share over 256 workgroups) take 32 us, 64-token ones 17 us.
-constexpr int64_t kMinRange = 64;
-__device__ __forceinline__ int64_t range_len(const DecodeArgs& a, int64_t T) {
-  if (a.range > 0) return a.range;
-  const int64_t q = (T + a.W - 1) / a.W;
-  return q > kMinRange ? q : kMinRange;
-}
-
-// Work-range geometry shared by the decode and merge kernels.
-struct Ranges {
-  int64_t T, Q, R;  // token-heads, token-heads per range, ranges
+// Range j of the plan: unit (b, hg), its tokens [t0, t1) and its unit's number of ranges n.
+struct RangePos {
+  int b, hg;
+  int t0, t1;
+  uint32_t n;
 };
 
-__device__ __forceinline__ Ranges work_ranges(const DecodeArgs& a) {
-  Ranges g;
-  g.T = tokens_before(a, a.B) * a.NHG;
-  g.Q = range_len(a, g.T);
-  g.R = (g.T + g.Q - 1) / g.Q;
-  return g;
-}
-
-// The sequence whose line part [NHG * pre, NHG * (pre + ctx)) holds line index g (g < T).
-struct SeqPos {
-  int b;
-  int64_t pre, ctx;
-};
-
-__device__ SeqPos locate(const DecodeArgs& a, int64_t g) {
+__device__ RangePos find_range(const DecodeArgs& a, const Plan& p, int64_t j) {
   const int lane = threadIdx.x % kWave;
   int64_t base = 0;
   for (int b0 = 0; b0 < a.B; b0 += kWave) {
-    const int b = b0 + lane;
-    const int64_t c = b < a.B ? seq_ctx(a, b) : 0;
-    int64_t incl = c;
+    const uint32_t c = a.B <= kWave ? p.c0 : lane_ctx(a, b0);
+    const uint32_t n = ranges_of(c, p.Q);
+    int64_t incl;
+    if (a.B <= kWave && !p.fixed) {
+      incl = static_cast<int64_t>(wave_scan_u32(n)) * a.NHG;  // below 2^31 (see count_ranges)
+    } else {
+      incl = static_cast<int64_t>(n) * a.NHG;
 #pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int64_t u = __shfl_up(incl, d, kWave);
-      if (lane >= d) incl += u;
+      for (int d = 1; d < kWave; d <<= 1) {
+        const int64_t u = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += u;
+      }
     }
-    const uint64_t hit = __ballot(b < a.B && (base + incl) * a.NHG > g);
+    const uint64_t hit = __ballot(b0 + lane < a.B && base + incl > j);
     if (hit != 0) {
       const int i = __builtin_ctzll(hit);
-      const int64_t ci = __shfl(c, i, kWave), ii = __shfl(incl, i, kWave);
-      return {b0 + i, uniform64(base + ii - ci), uniform64(ci)};
+      RangePos r;
+      r.b = b0 + i;
+      const uint32_t cb = __builtin_amdgcn_readlane(c, i);
+      r.n = __builtin_amdgcn_readlane(n, i);
+      if (r.n == 0) break;  // unreachable: the first row whose prefix passes j has ranges
+      const int64_t pre = base + uniform64(__shfl(incl, i, kWave)) - static_cast<int64_t>(r.n) * a.NHG;
+      const int64_t rel = j - pre;
+      if (rel < 0 || rel >= static_cast<int64_t>(r.n) * a.NHG) break;  // unreachable
+      r.hg = static_cast<int>(rel / r.n);
+      const uint32_t k = static_cast<uint32_t>(rel - static_cast<int64_t>(r.hg) * r.n);
+      const uint32_t L = p.fixed ? p.Q : (cb - 1) / r.n + 1;
+      const uint32_t t0 = k * L, t1 = t0 + L < cb ? t0 + L : cb;
+      r.t0 = static_cast<int>(t0);
+      r.t1 = static_cast<int>(t1);
+      return r;
     }
-    base += __shfl(incl, kWave - 1, kWave);
+    base += uniform64(__shfl(incl, kWave - 1, kWave));
   }
-  return {a.B, uniform64(base), 0};
+  return RangePos{a.B, 0, 0, 0, 0};  // unreachable for j < R
+}
+
+// Row b's context, its number of ranges per head group and the first range of its unit
+// (b, 0) (its unit (b, hg) starts hg * n later).
+struct RowPlan {
+  uint32_t ctx, n;
+  int64_t pre;
+};
+
+__device__ RowPlan row_plan(const DecodeArgs& a, const Plan& p, int b) {
+  const int lane = threadIdx.x % kWave;
+  int64_t pre = 0;
+  uint32_t cb = 0;
+  for (int b0 = 0; b0 < a.B; b0 += kWave) {
+    const uint32_t c = a.B <= kWave ? p.c0 : lane_ctx(a, b0);
+    const int bb = b0 + lane;
+    pre += uniform64(wave_sum_i64(bb < b ? static_cast<int64_t>(ranges_of(c, p.Q)) : 0));
+    if (b >= b0 && b < b0 + kWave) cb = __builtin_amdgcn_readlane(c, b - b0);
+  }
+  RowPlan r;
+  r.pre = pre * a.NHG;
+  r.ctx = cb;
+  r.n = ranges_of(r.ctx, p.Q);
+  return r;
 }
 
 // Runs tokens [t0, t1) of (b, h) and writes the output rows (whole) or partial `slot`.
@@ -168,43 +299,18 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
 }
 
 // Decode kernel: workgroup w runs work ranges w, w + W, ... (one range each with the
-// balanced default); its wavefront i takes kv head hg * HB + i. Waves proceed independently
-// (no barriers).
+// balanced default unless the units outnumber the workgroups); its wavefront i takes kv head
+// hg * HB + i. Waves proceed independently (no barriers). A range that is its unit's only one
+// writes the output rows, the others their partial at slot j * HB + i.
 template <typename E, int D, int G, bool kScalarBlk, bool kOff32>
 __global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_kernel(DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
-  const Ranges rg = work_ranges(a);
-  for (int64_t j = blockIdx.x; j < rg.R; j += a.W) {
-    int64_t g = j * rg.Q;
-    const int64_t ge = g + rg.Q < rg.T ? g + rg.Q : rg.T;
-    const SeqPos sp = locate(a, g);
-    int b = sp.b;
-    int64_t gb = sp.pre * a.NHG;  // line index of (b, 0, 0)
-    int64_t ctx = sp.ctx;
-    if (b >= a.B || ctx <= 0) return;  // unreachable for g < T
-    for (;;) {
-      const int64_t rel = g - gb;
-      const int hg = static_cast<int>(rel / ctx);
-      const int64_t t0 = rel - hg * ctx;
-      const int64_t hend = gb + (hg + 1) * ctx;
-      const int64_t send = ge < hend ? ge : hend;
-      const int64_t t1 = t0 + (send - g);
-      const int h = hg * a.HB + wave;
-      const bool whole = t0 == 0 && t1 == ctx;
-      const int64_t slot = ((static_cast<int64_t>(b) * a.NHG + hg) + j) * a.HB + wave;
-      decode_segment<E, D, G, kScalarBlk, kOff32>(a, b, h, static_cast<int>(t0),
-                                                  static_cast<int>(t1), whole, slot);
-      g = send;
-      if (g >= ge) break;
-      if (hg + 1 == a.NHG) {  // next sequence with a non-empty context
-        gb += a.NHG * ctx;
-        do {
-          ++b;
-          ctx = b < a.B ? seq_ctx(a, b) : 1;
-        } while (ctx == 0);
-        if (b >= a.B) return;  // unreachable for g < T
-      }
-    }
+  const Plan p = make_plan(a);
+  for (int64_t j = blockIdx.x; j < p.R; j += a.W) {
+    const RangePos rp = find_range(a, p, j);
+    if (rp.b >= a.B) continue;  // unreachable for j < R
+    decode_segment<E, D, G, kScalarBlk, kOff32>(a, rp.b, rp.hg * a.HB + wave, rp.t0, rp.t1,
+                                                rp.n == 1, j * a.HB + wave);
   }
 }
 
@@ -290,32 +396,19 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_kernel
   const int h = hq / G, g = hq % G;
   float* out = a.out + item * D;
 
-  int64_t tot = 0, pre = 0, cb = 0;
-  for (int b0 = 0; b0 < a.B; b0 += kWave) {
-    const int bb = b0 + lane;
-    const int64_t c = bb < a.B ? seq_ctx(a, bb) : 0;
-    tot += c;
-    pre += bb < b ? c : 0;
-    cb += bb == b ? c : 0;
-  }
-  tot = uniform64(wave_sum_i64(tot));
-  pre = uniform64(wave_sum_i64(pre));
-  const int64_t ctx = uniform64(wave_sum_i64(cb));
-  if (ctx == 0) {
+  const Plan p = make_plan(a);
+  const RowPlan rp = row_plan(a, p, b);
+  if (rp.ctx == 0) {
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       if (lane + i * kWave < D) out[lane + i * kWave] = __builtin_nanf("");
     return;
   }
-  const int64_t T = tot * a.NHG;
-  const int64_t Q = range_len(a, T);
+  if (rp.n == 1) return;  // written whole by the decode kernel
+  // partial of range first + k: slot base + k * HB; lane holds dims lane + 64 i
   const int hg = h / a.HB;
-  const int64_t g0 = pre * a.NHG + hg * ctx;
-  const int64_t j0 = g0 / Q, j1 = (g0 + ctx - 1) / Q;
-  if (j0 == j1) return;
-  // partial of range j0 + p: slot base + p * HB; lane holds dims lane + 64 i
-  const int64_t base = ((static_cast<int64_t>(b) * a.NHG + hg) + j0) * a.HB + h % a.HB;
-  const int np = static_cast<int>(j1 - j0 + 1);
+  const int64_t base = (rp.pre + static_cast<int64_t>(hg) * rp.n) * a.HB + h % a.HB;
+  const int np = static_cast<int>(rp.n);
   const int dl = lane < D ? lane : 0;  // D < 64: lanes past D read dim 0 and write nothing
   float o[PER];
   const float L = merge_partials<PER, kWave>(
@@ -360,34 +453,21 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_frag_k
     const int G = a.Hq / a.Hk;
     const int h = hq / G, g = hq % G;
     float* out = a.out + item * D + lane * CPL;
-    int64_t tot = 0, pre = 0, cb = 0;
-    for (int b0 = 0; b0 < a.B; b0 += kWave) {
-      const int bb = b0 + lane;
-      const int64_t c = bb < a.B ? seq_ctx(a, bb) : 0;
-      tot += c;
-      pre += bb < b ? c : 0;
-      cb += bb == b ? c : 0;
-    }
-    tot = uniform64(wave_sum_i64(tot));
-    pre = uniform64(wave_sum_i64(pre));
-    const int64_t ctx = uniform64(wave_sum_i64(cb));
-    const int64_t T = tot * a.NHG;
-    const int64_t Q = range_len(a, T);
+    const Plan p = make_plan(a);
+    const RowPlan rp = row_plan(a, p, b);
     const int hg = h / a.HB;
-    const int64_t g0 = pre * a.NHG + hg * ctx;
-    const int64_t j0 = ctx > 0 ? g0 / Q : 0, j1 = ctx > 0 ? (g0 + ctx - 1) / Q : 0;
-    if (ctx == 0) {
+    if (rp.ctx == 0) {
 #pragma unroll
       for (int e = 0; e < CPL; ++e) {
         x[e] = __builtin_nanf("");
         out[e] = x[e];
       }
-    } else if (j0 == j1) {  // written whole by the decode kernel
+    } else if (rp.n == 1) {  // written whole by the decode kernel
 #pragma unroll
       for (int e = 0; e < CPL; ++e) x[e] = out[e];
     } else {
-      const int64_t base = ((static_cast<int64_t>(b) * a.NHG + hg) + j0) * a.HB + h % a.HB;
-      const int np = static_cast<int>(j1 - j0 + 1);
+      const int64_t base = (rp.pre + static_cast<int64_t>(hg) * rp.n) * a.HB + h % a.HB;
+      const int np = static_cast<int>(rp.n);
       float o[CPL];
       const float L = merge_partials<CPL, 1>(
           np, [&](int p) { return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2; },
@@ -529,17 +609,20 @@ int grid_blocks(int64_t D, int64_t G, int64_t Hk, int64_t block_size, int off32 
   return w8 > w32 ? w8 : w32;
 }
 
-// Partial slots the workspace holds: HB per (b, head group) plus HB per work range (the
-// balanced split uses one range per resident workgroup; a fixed range size is bounded by the
-// longest possible work line).
+// Partial slots the workspace holds: HB per work range. The balanced split has at most one
+// range per resident workgroup, or one per (b, head group) when those outnumber the
+// workgroups; a fixed range size P gives each (b, head group) at most ceil(max context / P).
 int64_t partial_slots(int64_t B, int64_t Hk, int64_t D, int64_t G, int64_t max_blocks,
                       int64_t block_size, int64_t partition_size) {
   const int64_t hb = heads_per_block(Hk), nhg = Hk / hb;
-  const int64_t ranges =
-      partition_size > 0
-          ? (B * nhg * max_blocks * block_size + partition_size - 1) / partition_size
-          : grid_blocks(D, G, Hk, block_size);
-  return (B * nhg + ranges) * hb;
+  int64_t ranges;
+  if (partition_size > 0) {
+    ranges = B * nhg * ((max_blocks * block_size + partition_size - 1) / partition_size);
+  } else {
+    ranges = grid_blocks(D, G, Hk, block_size);
+    if (B * nhg > ranges) ranges = B * nhg;
+  }
+  return ranges * hb;
 }
 
 }  // namespace
