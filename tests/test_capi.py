@@ -76,15 +76,16 @@ def test_paged_attention_workspace_size(lib):
     ws = lib.llmserve_paged_attention_workspace_bytes
 
     def expect(B, Hq, Hk, D, max_blocks, bs, P, HB):
-        # (B * NHG + ranges) * HB partial slots of G (m, l, acc[D]) rows; with a fixed range
-        # size the ranges are bounded by the longest work line, B * NHG * max_blocks * bs
+        # ranges * HB partial slots of G (m, l, acc[D]) rows; with a fixed range size every
+        # (b, head group) unit has at most ceil(max_blocks * bs / P) ranges (ranges never
+        # straddle two units)
         nhg, G = Hk // HB, Hq // Hk
-        ranges = -(-B * nhg * max_blocks * bs // P)
-        return (B * nhg + ranges) * HB * G * (D + 2) * 4
+        ranges = B * nhg * -(-max_blocks * bs // P)
+        return ranges * HB * G * (D + 2) * 4
 
-    # 8 kv heads share a workgroup; one range covers the whole line
+    # 8 kv heads share a workgroup; one range covers a whole unit
     assert ws(4, 16, 8, 128, 4, 16, 10_000) == expect(4, 16, 8, 128, 4, 16, 10_000, 8)
-    # 32-token ranges over a 2 x 256-token bound: 16 ranges
+    # 32-token ranges over 256-token units: 8 per unit, 16 ranges
     assert ws(2, 16, 8, 128, 16, 16, 32) == expect(2, 16, 8, 128, 16, 16, 32, 8)
     # 6 kv heads: groups of 6
     assert ws(1, 12, 6, 64, 2, 16, 16) == expect(1, 12, 6, 64, 2, 16, 16, 6)
