@@ -597,13 +597,20 @@ def c5_per_op(torch, dev, model, lm4, cache, runner) -> dict:
                  q, kc0.data, vc0.data, kc0.scale, vc0.scale, bt, ctx, bs, D ** -0.5, 0,
                  kc0._q_mult, None)[1]}
 
-    def frag_gemm(name, lin_of, N, K, per_step=L):
-        """the step's GEMM on activation fragments (their producer timed on its own)"""
+    def frag_gemm(name, lin_of, N, K, per_step=L, planes=False):
+        """the step's GEMM on activation fragments (their producer timed on its own); planes:
+        the K-split form the step uses before a residual norm (output planes)"""
         xf = frags[K]
+        P = fo.int4_xfrag_splits(B, N, K) if planes else 1
 
         def launch(i):
-            fo.int4_linear_gemm_xfrag(xf, lin_of(i).gemm_packed, B, N, K, GROUP)
-        return name, launch, int4_bytes(N, K, B), 2.0 * B * N * K, per_step
+            if P > 1:
+                fo.int4_linear_gemm_xfrag_split(xf, lin_of(i).gemm_packed, B, N, K, GROUP, P)
+            else:
+                fo.int4_linear_gemm_xfrag(xf, lin_of(i).gemm_packed, B, N, K, GROUP)
+        if P > 1:
+            name = f"{name[:-1]}, K split in {P} planes)"
+        return name, launch, int4_bytes(N, K, B) + 4 * B * N * (P - 1), 2.0 * B * N * K, per_step
 
     def lin(attr):
         return lambda i: getattr(lay[i % L], attr)
@@ -629,7 +636,8 @@ def c5_per_op(torch, dev, model, lm4, cache, runner) -> dict:
          + 2 * B * nk * (D + 4), 0.0, L),
         ("paged_attention_decode_int8_xfrag (+ merge writing o_proj's fragments)", attn,
          kv_read + 8 * B * nq * D + 4 * B * nq * D, 0.0, L),
-        frag_gemm("o_proj (int4 GEMM on fragments, 2048->1024)", lin("o_proj"), H, nq * D),
+        frag_gemm("o_proj (int4 GEMM on fragments, 2048->1024)", lin("o_proj"), H, nq * D,
+                  planes=True),
         ("add_rmsnorm_xfrag_ (residual + norm + next split)",
          lambda i: fo.add_rmsnorm_xfrag_(resid, x[H], lay[i % L].input_layernorm,
                                          lay[i % L].gate_up_proj.inv_act_scale, eps),
@@ -638,7 +646,8 @@ def c5_per_op(torch, dev, model, lm4, cache, runner) -> dict:
                   2 * I, H),
         ("silu_mul_xfrag (silu * up + down's split)",
          lambda i: fo.silu_mul_xfrag(gu, lay[i % L].down_proj.inv_act_scale), 4 * B * 3 * I, 0.0, L),
-        frag_gemm("down_proj (int4 GEMM on fragments, 3072->1024)", lin("down_proj"), H, I),
+        frag_gemm("down_proj (int4 GEMM on fragments, 3072->1024)", lin("down_proj"), H, I,
+                  planes=True),
         ("lm_head fp32 (hipBLASLt, torch.mm)", lambda i: torch.mm(x[H], model.lm_weight.t()),
          model.embed.numel() * 4 + 4 * B * (H + cfg.vocab_size), 2.0 * B * cfg.vocab_size * H, 1),
         ("lm_head fp32 (split-bf16 matrix cores on fragments: the step's)",

@@ -174,6 +174,20 @@ int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* packed, float
                                     int64_t N, int64_t K, int64_t group_size, void* stream);
 
 /*
+ * llmserve_int4_linear_gemm_xfrag with K split across workgroups for narrow outputs (o_proj,
+ * down_proj at decode batches, whose 64-channel slabs alone occupy a quarter of the GPU): y is
+ * [splits, M, N], plane p the sum over the K blocks [p ceil(nb / splits), ...) (nb = K / 128),
+ * and the linear's output is the planes added in order (llmserve_add_rmsnorm_split_xfrag does
+ * that as it adds the residual). llmserve_int4_xfrag_splits gives the split count used by the
+ * decode step (1 when the output fills the GPU without it); splits in [1, 8]. No counterpart
+ * in the reference: a work split of Int4Linear.forward (quant.py:141-142).
+ */
+int64_t llmserve_int4_xfrag_splits(int64_t M, int64_t N, int64_t K);
+int llmserve_int4_linear_gemm_xfrag_split(const void* xfrag, const void* packed, float* y,
+                                          int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                          int64_t splits, void* stream);
+
+/*
  * Prefill-sized int8 weight-only linear on the bf16 matrix cores (replaces Int8Linear's
  * large-M path, quant.py:71-72 with dequantize quant.py:78-79: x @ (q * scale[:, None]).T):
  *   y[m, n] = scale[n] * sum_k bf16(x[m, k]) * q[n, k]      (fp32 accumulate)
@@ -224,6 +238,12 @@ int llmserve_rmsnorm_xfrag(const float* x, const float* w, const float* act_inv,
                            int64_t T, int64_t H, float eps, void* stream);
 int llmserve_add_rmsnorm_xfrag(float* x, const float* r, const float* w, const float* act_inv,
                                void* xfrag, int64_t T, int64_t H, float eps, void* stream);
+/* llmserve_add_rmsnorm_xfrag whose residual r is `planes` partial sums [planes, T, H] (the
+ * output planes of llmserve_int4_linear_gemm_xfrag_split): x += (r_0 + r_1 + ... in plane
+ * order), then the norm and the fragments as llmserve_add_rmsnorm_xfrag; planes in [1, 64]. */
+int llmserve_add_rmsnorm_split_xfrag(float* x, const float* r, int64_t planes, const float* w,
+                                     const float* act_inv, void* xfrag, int64_t T, int64_t H,
+                                     float eps, void* stream);
 int llmserve_embed_rmsnorm_xfrag(const int64_t* ids, const float* embed, int64_t V,
                                  const float* w, const float* act_inv, float* x, void* xfrag,
                                  int64_t T, int64_t H, float eps, void* stream);

@@ -88,12 +88,14 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_kernel(const float* __re
 // computes h = w * (x * inv) as rmsnorm_kernel does, x' = h * act_inv (the next linear's AWQ
 // pre-scale, or h) and writes x' as bf16 hi / mid / lo fragments and block sums, with 4 consecutive
 // channels per thread (32 threads per 128-channel block). One workgroup per fragment row:
-// rows past T write zeros. H is a multiple of 128.
+// rows past T write zeros. H is a multiple of 128. The residual r may come as `planes` partial
+// sums [planes, T, H] (a K-split linear's output planes): they are added in plane order, then
+// to x.
 template <int MODE>
 __global__ __launch_bounds__(kRowThreads) void rmsnorm_frag_kernel(
     float* __restrict__ x, const float* __restrict__ r, const int64_t* __restrict__ ids, int64_t V,
     const float* __restrict__ w, const float* __restrict__ act_inv, __bf16* __restrict__ xf,
-    float* __restrict__ xsum, int T, int H, int mp, float eps) {
+    float* __restrict__ xsum, int T, int H, int mp, float eps, int planes) {
   __shared__ float red[kRowThreads / kWave];
   const int t = blockIdx.x;
   const int nblk = H / lsh::kFragBlk;
@@ -114,9 +116,14 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_frag_kernel(
     src = r + (bad ? 0 : id) * H;
   }
   float ss = 0.f;
+  const int64_t pstride = static_cast<int64_t>(T) * H;
   for (int i = threadIdx.x; i < H; i += kRowThreads) {
     float v = src[i];
-    if (MODE == kNormAdd) v += r[static_cast<int64_t>(t) * H + i];
+    if (MODE == kNormAdd) {
+      float rs = r[static_cast<int64_t>(t) * H + i];
+      for (int p = 1; p < planes; ++p) rs += r[p * pstride + static_cast<int64_t>(t) * H + i];
+      v += rs;
+    }
     if (MODE == kNormGather && bad) v = __builtin_nanf("");
     if (MODE != kNormPlain) xr[i] = v;
     ss += v * v;
@@ -481,7 +488,7 @@ namespace {
 
 int launch_norm_frag(int mode, float* x, const float* r, const int64_t* ids, int64_t V,
                      const float* w, const float* act_inv, void* xfrag, int64_t T, int64_t H,
-                     float eps, void* stream, const char* what) {
+                     float eps, void* stream, const char* what, int planes = 1) {
   LSH_CHECK(T >= 0 && H >= lsh::kFragBlk && H % lsh::kFragBlk == 0 && T < (1LL << 24) &&
                 H < (1LL << 24),
             "%s: T=%lld, H=%lld (H a multiple of 128)", what, (long long)T, (long long)H);
@@ -498,15 +505,15 @@ int launch_norm_frag(int mode, float* x, const float* r, const int64_t* ids, int
   switch (mode) {
     case kNormAdd:
       lsh::launch(rmsnorm_frag_kernel<kNormAdd>, grid, block, 0, st, true, x, r, ids, V, w, act_inv,
-                  xf, xsum, Ti, Hi, mp, eps);
+                  xf, xsum, Ti, Hi, mp, eps, planes);
       break;
     case kNormGather:
       lsh::launch(rmsnorm_frag_kernel<kNormGather>, grid, block, 0, st, true, x, r, ids, V, w,
-                  act_inv, xf, xsum, Ti, Hi, mp, eps);
+                  act_inv, xf, xsum, Ti, Hi, mp, eps, 1);
       break;
     default:
       lsh::launch(rmsnorm_frag_kernel<kNormPlain>, grid, block, 0, st, true, x, r, ids, V, w,
-                  act_inv, xf, xsum, Ti, Hi, mp, eps);
+                  act_inv, xf, xsum, Ti, Hi, mp, eps, 1);
       break;
   }
   return lsh::launch_status(what);
@@ -526,6 +533,15 @@ extern "C" int llmserve_add_rmsnorm_xfrag(float* x, const float* r, const float*
                                           float eps, void* stream) {
   return launch_norm_frag(kNormAdd, x, r, nullptr, 0, w, act_inv, xfrag, T, H, eps, stream,
                           "add_rmsnorm_xfrag");
+}
+
+extern "C" int llmserve_add_rmsnorm_split_xfrag(float* x, const float* r, int64_t planes,
+                                                const float* w, const float* act_inv, void* xfrag,
+                                                int64_t T, int64_t H, float eps, void* stream) {
+  LSH_CHECK(planes >= 1 && planes <= 64, "add_rmsnorm_split_xfrag: planes %lld not in [1, 64]",
+            (long long)planes);
+  return launch_norm_frag(kNormAdd, x, r, nullptr, 0, w, act_inv, xfrag, T, H, eps, stream,
+                          "add_rmsnorm_split_xfrag", static_cast<int>(planes));
 }
 
 extern "C" int llmserve_embed_rmsnorm_xfrag(const int64_t* ids, const float* embed, int64_t V,

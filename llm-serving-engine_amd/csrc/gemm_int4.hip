@@ -46,6 +46,7 @@ constexpr int kRows = 16 * kMT;        // activation rows per wavefront
 constexpr int kCols = 16 * kNT;        // output channels per wavefront
 constexpr int kWaves = 4;              // wavefronts of the x-split workgroups
 constexpr int kSplitWaves = 4;         // largest K split
+constexpr int kMaxPlanes = 8;          // largest K split across workgroups (output planes)
 
 // x' = x * inv -> xh, xl (bf16, round to nearest even) and xsum[b, m] = sum of x' over block
 // b. One wavefront per (m, b): lane i holds channels 2i, 2i + 1 of the block. xsum rows are
@@ -334,11 +335,17 @@ __global__ __launch_bounds__(256) void x_split_frag_kernel(
 // Workgroups are numbered so that the row tiles of one slab run on the same XCD: the slab's
 // nibbles come from HBM into that XCD's L2 once. Operands are the packed ones (a.w, a.s and
 // a.xh as above; a.z and a.xl are unused).
+// K split across workgroups (narrow outputs, whose slabs alone leave most CUs idle): plane p
+// of the grid takes the blocks [p bpp, (p + 1) bpp) and writes its sums to y + p M N; the
+// consumer adds the planes in order (llmserve_add_rmsnorm_split_xfrag). bpp = nblk: one plane.
 template <int KB, int S>
-__global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int slabs_pad, int mtiles) {
+__global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int slabs_pad, int mtiles,
+                                                           int bpp) {
   extern __shared__ f32x4 red[];  // S > 1: [S][kNT][64]
   const int lane = threadIdx.x % kWave, ks = threadIdx.x / kWave;
-  const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+  const int per_plane = slabs_pad * mtiles;
+  const int plane = blockIdx.x / per_plane, wg = blockIdx.x % per_plane;
+  const int xcd = wg % 8, j = wg / 8;
   const int t = j % mtiles;
   const int slab = (j / mtiles) * 8 + xcd;
   const int n0 = slab * kCols, m0 = t * kRows;
@@ -346,18 +353,20 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
   const int fr = lane % 16, fc = lane / 16;
   const int nblk = a.K / kBlk;
   const int slabs = (a.N + kCols - 1) / kCols;
+  const int b0 = plane * bpp, b1 = min(b0 + bpp, nblk);  // this plane's blocks
+  float* y = a.y + static_cast<int64_t>(plane) * a.M * a.N;
 
   f32x4 acc[kNT];
 #pragma unroll
   for (int u = 0; u < kNT; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
   // Rounds of S x KB blocks (one round up to K = 2048 at S = 8, KB = 2).
-  for (int base = 0; base < nblk; base += S * KB) {
+  for (int base = b0; base < b1; base += S * KB) {
     u32x4 w[KB][kNT], xh[KB][4], xm[KB][4], xl[KB][4];
     f32x4 xs[KB];
     float sc[KB][kNT], zc[KB][kNT];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      const int b = min(base + ks * KB + kb, nblk - 1);  // clamped: loads stay unconditional
+      const int b = min(base + ks * KB + kb, b1 - 1);  // clamped: loads stay unconditional
       const int g = b / a.bpg;
       const uint8_t* wt = a.w + ((static_cast<int64_t>(slab) * nblk + b) * kNT) * kPkTile + 16 * lane;
 #pragma unroll
@@ -388,7 +397,7 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
     // weighted by 0: no branch, so that the compiler keeps every load ahead of the first use.
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      const float on = base + ks * KB + kb < nblk ? 1.f : 0.f;
+      const float on = base + ks * KB + kb < b1 ? 1.f : 0.f;
 #pragma unroll
       for (int u = 0; u < kNT; ++u) {
         f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -428,7 +437,7 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = m0 + 4 * fc + r;
-      if (m < a.M) a.y[static_cast<int64_t>(m) * a.N + n] = v[r];
+      if (m < a.M) y[static_cast<int64_t>(m) * a.N + n] = v[r];
     }
   }
 }
@@ -436,12 +445,13 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
 int64_t xsum_rows(int64_t M) { return (M + kRows - 1) / kRows * kRows; }
 
 template <int KB, int S>
-void launch_lat_ks(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, hipStream_t st) {
+void launch_lat_ks(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int planes, int bpp,
+                   hipStream_t st) {
   const int64_t slabs_pad = (slabs + 7) / 8 * 8;
-  const dim3 grid(static_cast<unsigned>(slabs_pad * mtiles)), block(S * kWave);
+  const dim3 grid(static_cast<unsigned>(slabs_pad * mtiles * planes)), block(S * kWave);
   const size_t lds = S > 1 ? static_cast<size_t>(S) * kNT * kWave * sizeof(f32x4) : 0;
   lsh::launch(int4_gemm_lat<KB, S>, grid, block, lds, st, true, a,
-              static_cast<int>(slabs_pad), static_cast<int>(mtiles));
+              static_cast<int>(slabs_pad), static_cast<int>(mtiles), bpp);
 }
 
 // Blocks per wavefront and round KB = ceil(nb / 8) (at most 2: three blocks of three-piece x
@@ -450,24 +460,27 @@ void launch_lat_ks(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, hipStre
 // then the fewest of 1, 2, 4, 8
 // wavefronts that cover the nb blocks (8 when more than one round is needed); the exceptions
 // below.
-void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb, hipStream_t st) {
+void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all, hipStream_t st,
+                int planes = 1) {
+  const int bpp = (nb_all + planes - 1) / planes;  // blocks per plane
+  const int nb = bpp;
   int KB = std::min(2, (nb + 7) / 8);
   int S = 1;
   while (S < 8 && S * KB < nb) S *= 2;
   // more than 8 blocks on a narrow output: 16 wavefronts of one block each (4 per SIMD) keep
   // more loads in flight per CU than 8 of two blocks (o_proj at M = 64: 6.3 against 6.7 us;
   // down, 24 blocks, takes two such rounds)
-  if (KB == 2 && S == 8 && slabs * mtiles < 256) {
+  if (KB == 2 && S == 8 && slabs * mtiles * planes < 256) {
     KB = 1;
     S = 16;
   }
   // very large outputs (an LM head) fill the GPU anyway: fewer, longer wavefronts
-  if (KB == 1 && S == 8 && slabs * mtiles * S > 16384) {
+  if (KB == 1 && S == 8 && slabs * mtiles * planes * S > 16384) {
     KB = 2;
     S = 4;
   }
 #define LSH_LAT(kb, s) \
-  if (KB == kb && S == s) return launch_lat_ks<kb, s>(a, slabs, mtiles, st);
+  if (KB == kb && S == s) return launch_lat_ks<kb, s>(a, slabs, mtiles, planes, bpp, st);
   LSH_LAT(1, 1) LSH_LAT(1, 2) LSH_LAT(1, 4) LSH_LAT(1, 8)
   LSH_LAT(2, 4) LSH_LAT(2, 8) LSH_LAT(1, 16)
 #undef LSH_LAT
@@ -638,4 +651,48 @@ extern "C" int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* pa
                  static_cast<int>(group_size / kBlk), mp};
   launch_lat(a, pk_slabs(N), mtiles, nb, lsh::as_stream(stream));
   return lsh::launch_status("int4_linear_gemm_xfrag");
+}
+
+// K planes for a decode-batch linear on fragments: enough that the slab tiles of all planes
+// give every CU a workgroup, with at least 4 blocks of K per plane; 1 when the slabs alone fill
+// the GPU (qkv, gate_up at Qwen3-0.6B shapes). o_proj and down_proj at 64 rows (N = 1024: 64
+// slab tiles) take 4.
+extern "C" int64_t llmserve_int4_xfrag_splits(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K < kBlk) return 1;
+  const int64_t tiles = pk_slabs(N) * ((M + kRows - 1) / kRows), nb = K / kBlk;
+  int64_t P = 1;
+  while (P < kMaxPlanes && tiles * P < 256 && nb >= 4 * 2 * P) P *= 2;
+  return P;
+}
+
+extern "C" int llmserve_int4_linear_gemm_xfrag_split(const void* xfrag, const void* packed,
+                                                     float* y, int64_t M, int64_t N, int64_t K,
+                                                     int64_t group_size, int64_t splits,
+                                                     void* stream) {
+  LSH_CHECK(splits >= 1 && splits <= kMaxPlanes,
+            "int4_linear_gemm_xfrag_split: splits %lld not in [1, %d]", (long long)splits,
+            kMaxPlanes);
+  LSH_CHECK(M >= 0 && N >= 1 && K >= 1 && group_size >= 2,
+            "int4_linear_gemm_xfrag_split: bad shape");
+  LSH_CHECK(K % kBlk == 0 && group_size % kBlk == 0 && K % group_size == 0,
+            "int4_linear_gemm_xfrag_split: K and group_size must be multiples of 128 (K %% group == 0)");
+  LSH_CHECK(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31) && M * K < (1LL << 40) &&
+                N * K < (1LL << 41) && splits * M * N < (1LL << 40),
+            "int4_linear_gemm_xfrag_split: shape too large");
+  if (M == 0) return LLMSERVE_OK;
+  LSH_CHECK(xfrag && packed && y, "int4_linear_gemm_xfrag_split: null pointer");
+  LSH_CHECK(lsh::aligned16(xfrag) && lsh::aligned16(packed),
+            "int4_linear_gemm_xfrag_split: the fragments and the packed weight must be 16-byte aligned");
+  const int nb = static_cast<int>(K / kBlk);
+  const int64_t mtiles = (M + kRows - 1) / kRows;
+  const int mp = static_cast<int>(lsh::frag_rows(M));
+  const __bf16* xf = static_cast<const __bf16*>(xfrag);
+  const float* xsum = lsh::frag_sums(xf, mp, K);
+  const uint8_t* wpk = static_cast<const uint8_t*>(packed);
+  const float* spk = reinterpret_cast<const float*>(wpk + (pk_weight_bytes(N, K) + 255) / 256 * 256);
+  Int4GemmArgs a{xf, nullptr, xsum, wpk, spk, nullptr, y, static_cast<int>(M),
+                 static_cast<int>(N), static_cast<int>(K), static_cast<int>(K / group_size),
+                 static_cast<int>(group_size / kBlk), mp};
+  launch_lat(a, pk_slabs(N), mtiles, nb, lsh::as_stream(stream), static_cast<int>(splits));
+  return lsh::launch_status("int4_linear_gemm_xfrag_split");
 }

@@ -454,16 +454,24 @@ at::Tensor add_rmsnorm_xfrag_(at::Tensor& x, const at::Tensor& r, const at::Tens
   check_f32(r, "r");
   check_f32(w, "w");
   check_device(x, {&r, &w}, "add_rmsnorm_xfrag_");
-  TORCH_CHECK(x.sizes() == r.sizes() && x.dim() == 2, "add_rmsnorm_xfrag_: x, r [T, H]");
+  // r [T, H], or [P, T, H]: the output planes of a K-split linear, added in plane order
+  TORCH_CHECK(x.dim() == 2 && ((r.dim() == 2 && r.sizes() == x.sizes()) ||
+                               (r.dim() == 3 && r.size(1) == x.size(0) && r.size(2) == x.size(1))),
+              "add_rmsnorm_xfrag_: x [T, H], r [T, H] or [P, T, H]");
   const int64_t T = x.size(0), H = x.size(1);
   TORCH_CHECK(w.numel() == H, "add_rmsnorm_xfrag_: weight must have H entries");
   check_act_inv(x, act_inv, H, "add_rmsnorm_xfrag_");
   const c10::DeviceGuard guard(x.device());
   auto xf = new_xfrag(x, T, H, "add_rmsnorm_xfrag_");
-  check_status(llmserve_add_rmsnorm_xfrag(x.data_ptr<float>(), r.data_ptr<float>(),
-                                          w.data_ptr<float>(), opt_ptr<float>(act_inv),
-                                          xf.data_ptr(), T, H, static_cast<float>(eps),
-                                          stream_of(x)));
+  if (r.dim() == 3)
+    check_status(llmserve_add_rmsnorm_split_xfrag(
+        x.data_ptr<float>(), r.data_ptr<float>(), r.size(0), w.data_ptr<float>(),
+        opt_ptr<float>(act_inv), xf.data_ptr(), T, H, static_cast<float>(eps), stream_of(x)));
+  else
+    check_status(llmserve_add_rmsnorm_xfrag(x.data_ptr<float>(), r.data_ptr<float>(),
+                                            w.data_ptr<float>(), opt_ptr<float>(act_inv),
+                                            xf.data_ptr(), T, H, static_cast<float>(eps),
+                                            stream_of(x)));
   return xf;
 }
 
@@ -517,6 +525,30 @@ at::Tensor int4_linear_gemm_xfrag(const at::Tensor& xfrag, const at::Tensor& pac
                                                y.data_ptr<float>(), M, N, K, group_size,
                                                stream_of(xfrag)));
   return y;
+}
+
+// The same linear with K split into `splits` output planes [splits, M, N] (their sum, in plane
+// order, is the linear's output).
+at::Tensor int4_linear_gemm_xfrag_split(const at::Tensor& xfrag, const at::Tensor& packed,
+                                        int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                        int64_t splits) {
+  TORCH_CHECK(xfrag.scalar_type() == at::kByte && xfrag.is_contiguous() &&
+                  xfrag.numel() == llmserve_int4_xfrag_bytes(M, K),
+              "int4_linear_gemm_xfrag_split: xfrag must hold the fragments of [M, K]");
+  TORCH_CHECK(packed.scalar_type() == at::kByte && packed.is_contiguous() &&
+                  packed.numel() == llmserve_int4_gemm_pack_bytes(N, K, group_size),
+              "int4_linear_gemm_xfrag_split: packed buffer does not match N, K, group_size");
+  check_device(xfrag, {&packed}, "int4_linear_gemm_xfrag_split");
+  const c10::DeviceGuard guard(xfrag.device());
+  auto y = at::empty({splits, M, N}, xfrag.options().dtype(at::kFloat));
+  check_status(llmserve_int4_linear_gemm_xfrag_split(xfrag.data_ptr(), packed.data_ptr(),
+                                                     y.data_ptr<float>(), M, N, K, group_size,
+                                                     splits, stream_of(xfrag)));
+  return y;
+}
+
+int64_t int4_xfrag_splits(int64_t M, int64_t N, int64_t K) {
+  return llmserve_int4_xfrag_splits(M, N, K);
 }
 
 // ---- int8-KV paged decode -------------------------------------------------------------------
@@ -796,6 +828,9 @@ TORCH_LIBRARY(llmserve_hip, m) {
   m.def("silu_mul_xfrag(Tensor gate_up, Tensor? act_inv) -> Tensor");
   m.def("int4_linear_gemm_xfrag(Tensor xfrag, Tensor packed, int M, int N, int K, int group_size)"
         " -> Tensor");
+  m.def("int4_linear_gemm_xfrag_split(Tensor xfrag, Tensor packed, int M, int N, int K,"
+        " int group_size, int splits) -> Tensor");
+  m.def("int4_xfrag_splits(int M, int N, int K) -> int", &int4_xfrag_splits);
   m.def("silu_mul(Tensor gate_up) -> Tensor");
   m.def("lm_head_f32_xfrag(Tensor xfrag, Tensor w, int M) -> Tensor");
   m.def("lm_head_f32(Tensor x, Tensor w) -> Tensor");
@@ -836,6 +871,7 @@ TORCH_LIBRARY_IMPL(llmserve_hip, CUDA, m) {
   m.impl("add_rmsnorm_", &add_rmsnorm_);
   m.impl("embed_rmsnorm", &embed_rmsnorm);
   m.impl("add_rmsnorm_xfrag_", &add_rmsnorm_xfrag_);
+  m.impl("int4_linear_gemm_xfrag_split", &int4_linear_gemm_xfrag_split);
   m.impl("embed_rmsnorm_xfrag", &embed_rmsnorm_xfrag);
   m.impl("silu_mul_xfrag", &silu_mul_xfrag);
   m.impl("int4_linear_gemm_xfrag", &int4_linear_gemm_xfrag);

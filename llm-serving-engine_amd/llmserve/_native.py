@@ -59,8 +59,11 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
     "llmserve_int4_linear_gemm_packed": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
     "llmserve_int4_xfrag_bytes": (_I64, [_I64, _I64]),
     "llmserve_int4_linear_gemm_xfrag": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "llmserve_int4_xfrag_splits": (_I64, [_I64, _I64, _I64]),
+    "llmserve_int4_linear_gemm_xfrag_split": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "llmserve_rmsnorm_xfrag": (_I32, [_P, _P, _P, _P, _I64, _I64, _F32, _P]),
     "llmserve_add_rmsnorm_xfrag": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _F32, _P]),
+    "llmserve_add_rmsnorm_split_xfrag": (_I32, [_P, _P, _I64, _P, _P, _P, _I64, _I64, _F32, _P]),
     "llmserve_embed_rmsnorm_xfrag": (_I32, [_P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _F32, _P]),
     "llmserve_silu_mul_xfrag": (_I32, [_P, _P, _P, _I64, _I64, _P]),
     "llmserve_int8_linear_prefill_workspace_bytes": (_I64, [_I64, _I64, _I64]),

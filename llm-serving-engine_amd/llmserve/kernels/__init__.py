@@ -88,5 +88,6 @@ def load_fused_ops() -> SimpleNamespace | None:
     """Decoder-layer elementwise ops and decode-step glue (HIP, gfx950), or None."""
     return _namespace("fused ops", (
         "rmsnorm", "add_rmsnorm_", "embed_rmsnorm", "add_rmsnorm_xfrag_", "embed_rmsnorm_xfrag",
-        "silu_mul_xfrag", "int4_linear_gemm_xfrag", "lm_head_f32_xfrag", "lm_head_f32",
+        "silu_mul_xfrag", "int4_linear_gemm_xfrag", "int4_linear_gemm_xfrag_split",
+        "int4_xfrag_splits", "lm_head_f32_xfrag", "lm_head_f32",
         "silu_mul", "rope_qk_", "decode_qkv_kv", "argmax_advance"))

@@ -22,6 +22,7 @@ no checkpoints on this path. The AWQ per-input-channel scales are searched (the 
 
 from __future__ import annotations
 
+import functools
 from dataclasses import dataclass
 
 import torch
@@ -40,6 +41,12 @@ def _fused_ops():
         raise RuntimeError("QuantCausalLM runs the fused HIP kernels of this package: build the "
                            "native library (llm-serving-engine_amd/build.py)")
     return fo
+
+
+@functools.lru_cache(maxsize=None)
+def _xfrag_splits(M: int, N: int, K: int) -> int:
+    """K planes of the decode step's narrow linears (llmserve_int4_xfrag_splits)."""
+    return int(_fused_ops().int4_xfrag_splits(M, N, K))
 
 
 @dataclass
@@ -361,6 +368,15 @@ class QuantCausalLM(nn.Module):
             return fo.int4_linear_gemm_xfrag(xf, lin.gemm_packed, B, lin.out_features, K,
                                              lin.group_size)
 
+        def gemm_planes(xf, lin, K):
+            """The linear before a residual norm: as K-split output planes [P, B, N] when its
+            output alone would leave CUs idle (add_rmsnorm_xfrag_ adds them in order)."""
+            P = _xfrag_splits(B, lin.out_features, K)
+            if P == 1:
+                return gemm(xf, lin, K)
+            return fo.int4_linear_gemm_xfrag_split(xf, lin.gemm_packed, B, lin.out_features, K,
+                                                   lin.group_size, P)
+
         if frag:
             x, h = fo.embed_rmsnorm_xfrag(ids, self.embed, self.layers[0].input_layernorm,
                                           self.layers[0].qkv_proj.inv_act_scale, eps)
@@ -375,7 +391,7 @@ class QuantCausalLM(nn.Module):
                 _, xo = pa.paged_attention_decode_int8_xfrag(
                     q, kc.data, vc.data, kc.scale, vc.scale, block_tables, context_lens,
                     block_size, self.scale, 0, kc._q_mult, L.o_proj.inv_act_scale)
-                attn = gemm(xo, L.o_proj, nq * D)
+                attn = gemm_planes(xo, L.o_proj, nq * D)
             else:
                 o = pa.paged_attention_decode_int8(q, kc.data, vc.data, kc.scale, vc.scale,
                                                    block_tables, context_lens, block_size,
@@ -387,7 +403,8 @@ class QuantCausalLM(nn.Module):
                 h = fo.add_rmsnorm_xfrag_(x, attn, L.post_attention_layernorm,
                                           L.gate_up_proj.inv_act_scale, eps)
                 a = fo.silu_mul_xfrag(gemm(h, L.gate_up_proj, H), L.down_proj.inv_act_scale)
-                down = gemm(a, L.down_proj, I)
+                to_frag = nxt is not None or self._lm_frag(B)
+                down = gemm_planes(a, L.down_proj, I) if to_frag else gemm(a, L.down_proj, I)
                 if nxt is not None:
                     h = fo.add_rmsnorm_xfrag_(x, down, nxt_w, nxt.qkv_proj.inv_act_scale, eps)
                 elif self._lm_frag(B):

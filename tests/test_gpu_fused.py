@@ -214,6 +214,29 @@ def test_xfrag_producers_equal_split_path(gpu, T, awq):
     assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("T,P", [(17, 2), (64, 4), (70, 3)])
+def test_add_rmsnorm_xfrag_adds_planes_in_order(gpu, T, P):
+    """A residual given as P output planes [P, T, H] (a K-split linear's) is added plane by
+    plane, then to x: the same x and fragments, bit for bit, as add_rmsnorm_xfrag_ with the
+    planes summed in that order beforehand."""
+    f = fo()
+    H = 1024
+    rng = np.random.default_rng(100 * T + P)
+    x0 = rng.standard_normal((T, H)).astype(F32)
+    planes = cu.dev(rng.standard_normal((P, T, H)).astype(F32))
+    w = cu.dev((1 + 0.1 * rng.standard_normal(H)).astype(F32))
+    inv = cu.dev((rng.random(H) + 0.5).astype(F32))
+    r = planes[0].clone()
+    for p in range(1, P):
+        r = r + planes[p]
+    xa, xb = cu.dev(x0), cu.dev(x0)
+    ref = f.add_rmsnorm_xfrag_(xa, r, w, inv, 1e-6)
+    got = f.add_rmsnorm_xfrag_(xb, planes, w, inv, 1e-6)
+    assert torch.equal(xa, xb) and torch.equal(got, ref)
+    with pytest.raises(RuntimeError, match="P, T, H"):
+        f.add_rmsnorm_xfrag_(xb, planes[:, :-1].contiguous(), w, inv, 1e-6)
+
+
 def test_xfrag_rejects_bad_shapes(gpu):
     f = fo()
     with pytest.raises(RuntimeError, match="multiple of 128"):

@@ -154,6 +154,53 @@ def test_packed_gemm_tails(gpu, M, N, K, g):
     cu.assert_rel_close(y, mr.int4_linear_f64(x, nib, gs, gz, g, inv), TOL, f"M={M} {N}x{K} g{g}")
 
 
+def _gemm_xfrag_split(xf, packed, M, N, K, g, P):
+    L = cu.capi()
+    y = torch.full((P, M, N), float("nan"), dtype=torch.float32, device=xf.device)
+    cu.check(L.llmserve_int4_linear_gemm_xfrag_split(cu._p(xf), cu._p(packed), cu._p(y), M, N, K,
+                                                     g, P, cu._stream()))
+    return y
+
+
+@pytest.mark.parametrize("M", [17, 64])
+@pytest.mark.parametrize("N,K", [(1024, 2048), (1024, 3072), (4096, 1024)])
+def test_packed_gemm_split_planes(gpu, M, N, K):
+    """The decode step's K-split linear (o_proj, down_proj): plane p of P is the product over
+    the K blocks [p ceil(nb / P), ...) -- checked against the float64 mathematics of x with the
+    other channels zeroed (an empty plane is exactly 0) -- and the planes added in order give
+    the linear. P = 2, 3 (not dividing the blocks), 4 and the count the step uses."""
+    x, nib, gs, gz, inv = _case(M, N, K, 128, M * 41 + N + K)
+    packed = cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), 128)
+    xf = cu.split_fragments(cu.dev(x), cu.dev(inv))
+    nb = K // 128
+    step_p = cu.capi().llmserve_int4_xfrag_splits(M, N, K)
+    # the rule: double P while the slab tiles of all planes leave CUs (256) without a
+    # workgroup and each plane keeps >= 4 blocks
+    tiles, want = (N // 64) * -(-M // 16), 1
+    while want < 8 and tiles * want < 256 and nb >= 8 * want:
+        want *= 2
+    assert step_p == want
+    full = mr.int4_linear_f64(x, nib, gs, gz, 128, inv)
+    for P in sorted({2, 3, 4, step_p}):
+        y = _gemm_xfrag_split(xf, packed, M, N, K, 128, P)
+        bpp = -(-nb // P)
+        for p in range(P):
+            lo, hi = min(p * bpp, nb) * 128, min((p + 1) * bpp, nb) * 128
+            xp = np.zeros_like(x)
+            xp[:, lo:hi] = x[:, lo:hi]
+            ref = mr.int4_linear_f64(xp, nib, gs, gz, 128, inv)
+            if hi == lo:
+                assert not y[p].any(), f"P={P} plane {p} is empty and must be zero"
+            else:
+                cu.assert_rel_close(y[p], ref, TOL, f"M={M} {N}x{K} P={P} plane {p}")
+        s = y[0].clone()
+        for p in range(1, P):
+            s = s + y[p]
+        cu.assert_rel_close(s, full, TOL, f"M={M} {N}x{K} P={P} sum")
+    with pytest.raises(RuntimeError, match="splits"):
+        _gemm_xfrag_split(xf, packed, M, N, K, 128, 9)
+
+
 def test_packed_gemm_rejects_bad_shapes(gpu):
     x, nib, gs, gz, _ = _case(20, 48, 256, 64, 3, awq=False)
     with pytest.raises(RuntimeError, match="multiples of 128"):
