@@ -427,14 +427,15 @@ def extra_configs(torch, dev) -> dict:
     return out
 
 
-def c5_decode(torch, dev, steps: int, warmup: int) -> dict:
+def c5_decode(torch, dev, steps: int, warmup: int, profile: bool = False) -> dict:
     """Config 5: greedy decode of 64 sequences through a random-init int4-AWQ Qwen3-0.6B (28
     layers, g128, AWQ scales searched on synthetic activations) over an int8 KV cache with key
     smoothing; contexts ~ U[1024, 4096], block tables a random permutation of the physical
     blocks, cache contents random int8 with random scales (the state after a prefill). Each
     step is one graph replay of the whole step (embedding to greedy token, context lengths
     advanced on the device). tok/s = 64 x steps / wall time; also the same with the LM head
-    quantized (quantize_lm_head), and per-op times at the step's shapes."""
+    quantized (quantize_lm_head), and per-op times at the step's shapes. profile: the fp32-head
+    replays only (for a kernel trace of the step)."""
     import numpy as np
 
     from llmserve.kv_cache import KVCache
@@ -501,6 +502,8 @@ def c5_decode(torch, dev, steps: int, warmup: int) -> dict:
             "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"[bench] c5 lm_head {head}: {out[f'lm_head_{head}']}")
         runner.graph = None
+        if profile:
+            return out
     model.lm_head = None
     out["per_op"] = c5_per_op(torch, dev, model, lm4, cache, runner)
     del runner, cache
@@ -738,6 +741,8 @@ def profile_only(torch, dev, what: str) -> int:
         for i in range(64):
             pk, inv = packed[i]
             gemv.int4_linear_gemm_packed(x, pk, N, GROUP, inv)
+    elif what == "c5step":  # config 5's decode step: 2 + 10 graph replays, fp32 LM head
+        c5_decode(torch, dev, 10, 2, profile=True)
     elif what == "attention":
         copies, q, cl, qm, bs, D, _ = c4_inputs(torch, dev)
         pa = load_paged_attention()
@@ -773,7 +778,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
-    ap.add_argument("--only", choices=["gemv", "gemm4", "attention", "prefill", "lmhead", "copy"],
+    ap.add_argument("--only", choices=["gemv", "gemm4", "attention", "prefill", "lmhead", "copy",
+                                       "c5step"],
                     help="profiling run: only launch that kernel (64 times) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -794,6 +800,7 @@ def main() -> int:
 
     by_rows = {}
     headline = None
+    spread = None
     packed = None
     for M in (1, 4, 16):
         xs = make_inputs(torch, dev, calib, M)
@@ -811,6 +818,12 @@ def main() -> int:
                            "gpu_ms_per_step": round(gpu / steps * 1e3, 4), "bytes": step_bytes}
         if M == 1:
             headline = (gbs, wall / steps * 1e3, steps, step_bytes)
+            # spread: five more timed windows of at least 200 steps (outside the headline's)
+            n = max(steps, 200)
+            runs = sorted(step_bytes * n / time_graphs(torch, graphs, n, 0)[0] / 1e9
+                          for _ in range(5))
+            spread = {"windows": 5, "steps_per_window": n, "GBps_min": round(runs[0], 1),
+                      "GBps_median": round(runs[2], 1), "GBps_max": round(runs[-1], 1)}
         del graphs
         log(f"[bench] M={M}: {by_rows[str(M)]}")
     del packed
@@ -877,6 +890,7 @@ def main() -> int:
             "bytes_per_step": step_bytes,
             "parallelism": "single GPU",
         },
+        "spread": spread,
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "roofline": roofline,
         "cpu_baseline": cpu,
