@@ -337,9 +337,11 @@ int llmserve_lm_head_f32(const float* x, const float* w, float* y, int64_t M, in
  * q fp32 [B,Hq,D]; k/v_cache int8 [num_slots,Hk,D]; k/v_scale fp32 [num_slots,Hk];
  * block_tables int64 [B,max_blocks]; context_lens int64 [B] -> out fp32 [B,Hq,D].
  * The context is split, as the reference's partitions are, into work ranges whose partial
- * (max, sum, acc) are merged: partition_size = tokens per range; 0 splits the whole batch
- * evenly over the GPU's resident workgroups (the same number of cache rows for each, whatever
- * the context lengths). Block ids outside [0, num_slots/block_size) contribute nothing;
+ * (max, sum, acc) are merged: partition_size = tokens per range; 0 cuts each (sequence, kv
+ * head group) into equal ranges, sized so that the whole batch's ranges fill the GPU's
+ * resident workgroups once (ranges never straddle two sequences; a sequence more than a few
+ * times the batch's mean context gets wider ranges, so that its partials fit a workspace
+ * bounded by the grid rather than by max_blocks). Block ids outside [0, num_slots/block_size) contribute nothing;
  * context lengths are clamped to max_blocks*block_size. A zero context yields NaN, as the
  * reference's 0 * (1/0) does. `workspace` holds the partials: at least
  * llmserve_paged_attention_workspace_bytes(...) bytes (non-zero whenever B > 0; the size of
@@ -490,7 +492,7 @@ int llmserve_decode_chain_error(const void* workspace, int* error);
  * llmserve_paged_attention_decode_int8 without a workspace argument, for callers that cannot
  * allocate device memory (HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). No counterpart in the reference. The split-context partials go to a scratch
- * array of llmserve_paged_attention_noalloc_scratch_bytes() bytes (16 MiB) that the library
+ * array of llmserve_paged_attention_noalloc_scratch_bytes() bytes (32 MiB) that the library
  * holds on each device it runs on until the process ends; a call whose partials
  * (llmserve_paged_attention_workspace_bytes(...)) exceed it fails with LLMSERVE_ERR_INVALID
  * before anything runs. Calls on one device share the array: calls that overlap on a device

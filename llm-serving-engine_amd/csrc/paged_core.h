@@ -68,6 +68,8 @@ struct DecodeArgs {
   float* out;
   float* part_ml;   // [slots, G, 2]  (running max in log2 units, sum)
   float* part_acc;  // [slots, G, D]
+  int* unit_n;      // [B * NHG]: ranges of each (row, head group) unit, set by its first range
+  int kcap;         // partial slots per unit (bound on its ranges)
   int64_t num_slots;
   int64_t range;  // tokens per work range; 0: the balanced plan (paged_decode.hip)
   int B, Hq, Hk, max_blocks, bs, bs_shift;  // bs_shift = log2(bs), or -1

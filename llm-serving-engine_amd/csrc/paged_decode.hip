@@ -32,6 +32,7 @@
 // The scores are the reference's s = (scale * k_scale) * (q . k_int8) and the values
 // acc += (p * v_scale) * v_int8 (paged_attention.cpp:301-355), up to the order of the
 // float operations (scale folded into q; exp2 of log2-unit scores).
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -55,8 +56,9 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
 // n_b = ceil(ctx_b / Q) ranges, numbered unit by unit in (b, hg) order. With a caller's fixed
 // partition size P (the reference's partitions) Q = P and the ranges hold P tokens, the last
 // one the rest. The balanced default equalises the ranges of a unit (ceil(ctx_b / n_b) tokens
-// each) and takes Q between max(ceil(T / W), kMinRange), T = NHG * sum_b ctx_b, and
-// ceil(T / (W - units)) (which always fits: each unit rounds up by less than one range) so
+// each) and takes Q between max(ceil(T / W), kMinRange, ceil(max ctx / kcap)), T = NHG *
+// sum_b ctx_b, kcap the partial slots per unit, and ceil(T / (W - units)) (which always fits:
+// each unit rounds up by less than one range) so
 // that the R = NHG * sum_b n_b ranges fit the W resident workgroups: the lower end if it fits,
 // else the feasible end of kPlanSteps bisections. Every workgroup derives the same plan from
 // the contexts, with DPP / readlane reductions (no LDS crossbar round trips: the plan is on
@@ -152,6 +154,8 @@ __device__ Plan make_plan(const DecodeArgs& a) {
   const int64_t even = (T + a.W - 1) / a.W;
   uint32_t lo = even > kMinRange ? static_cast<uint32_t>(even < 0x7fffffff ? even : 0x7fffffff)
                                  : kMinRange;
+  const uint32_t fit = (mx + static_cast<uint32_t>(a.kcap) - 1) / static_cast<uint32_t>(a.kcap);
+  if (fit > lo) lo = fit;  // the longest unit's ranges fit its kcap partial slots
   if (lo >= mx) {
     p.Q = lo;  // every unit is one range
   } else if (units >= a.W) {
@@ -181,7 +185,7 @@ __device__ Plan make_plan(const DecodeArgs& a) {
 struct RangePos {
   int b, hg;
   int t0, t1;
-  uint32_t n;
+  uint32_t n, k;  // the unit's ranges, this range's index among them
 };
 
 __device__ RangePos find_range(const DecodeArgs& a, const Plan& p, int64_t j) {
@@ -218,35 +222,12 @@ __device__ RangePos find_range(const DecodeArgs& a, const Plan& p, int64_t j) {
       const uint32_t t0 = k * L, t1 = t0 + L < cb ? t0 + L : cb;
       r.t0 = static_cast<int>(t0);
       r.t1 = static_cast<int>(t1);
+      r.k = k;
       return r;
     }
     base += uniform64(__shfl(incl, kWave - 1, kWave));
   }
-  return RangePos{a.B, 0, 0, 0, 0};  // unreachable for j < R
-}
-
-// Row b's context, its number of ranges per head group and the first range of its unit
-// (b, 0) (its unit (b, hg) starts hg * n later).
-struct RowPlan {
-  uint32_t ctx, n;
-  int64_t pre;
-};
-
-__device__ RowPlan row_plan(const DecodeArgs& a, const Plan& p, int b) {
-  const int lane = threadIdx.x % kWave;
-  int64_t pre = 0;
-  uint32_t cb = 0;
-  for (int b0 = 0; b0 < a.B; b0 += kWave) {
-    const uint32_t c = a.B <= kWave ? p.c0 : lane_ctx(a, b0);
-    const int bb = b0 + lane;
-    pre += uniform64(wave_sum_i64(bb < b ? static_cast<int64_t>(ranges_of(c, p.Q)) : 0));
-    if (b >= b0 && b < b0 + kWave) cb = __builtin_amdgcn_readlane(c, b - b0);
-  }
-  RowPlan r;
-  r.pre = pre * a.NHG;
-  r.ctx = cb;
-  r.n = ranges_of(r.ctx, p.Q);
-  return r;
+  return RangePos{a.B, 0, 0, 0, 0, 0};  // unreachable for j < R
 }
 
 // Runs tokens [t0, t1) of (b, h) and writes the output rows (whole) or partial `slot`.
@@ -301,7 +282,9 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int h
 // Decode kernel: workgroup w runs work ranges w, w + W, ... (one range each with the
 // balanced default unless the units outnumber the workgroups); its wavefront i takes kv head
 // hg * HB + i. Waves proceed independently (no barriers). A range that is its unit's only one
-// writes the output rows, the others their partial at slot j * HB + i.
+// writes the output rows, the others their partial at slot (u * kcap + k) * HB + i (unit
+// u = b * NHG + hg, k its range in the unit), and the unit's first range records n, so that
+// the merge finds the partials without the plan.
 template <typename E, int D, int G, bool kScalarBlk, bool kOff32>
 __global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_kernel(DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -309,39 +292,61 @@ __global__ __launch_bounds__(kMaxHeadsPerBlock * kWave) void paged_decode_kernel
   for (int64_t j = blockIdx.x; j < p.R; j += a.W) {
     const RangePos rp = find_range(a, p, j);
     if (rp.b >= a.B) continue;  // unreachable for j < R
+    const int64_t u = static_cast<int64_t>(rp.b) * a.NHG + rp.hg;
+    if (rp.k == 0 && threadIdx.x == 0) a.unit_n[u] = static_cast<int>(rp.n);
     decode_segment<E, D, G, kScalarBlk, kOff32>(a, rp.b, rp.hg * a.HB + wave, rp.t0, rp.t1,
-                                                rp.n == 1, j * a.HB + wave);
+                                                rp.n == 1, (u * a.kcap + rp.k) * a.HB + wave);
   }
 }
 
-// Merge of the split sequences (paged_attention.cpp:432-455): one wavefront per (b, q head).
+// Merge of the split units (paged_attention.cpp:432-455): one wavefront per (b, q head).
 //   M = max_j m_j;  w_j = exp2(m_j - M);  out = sum_j w_j acc_j / sum_j w_j l_j  (l_j = 0 skipped)
-// A (b, hg) inside one range was written by the decode kernel; a zero context gives NaN (the
-// reference's 0 * (1 / 0)). Three dependent rounds of loads: the context lengths (one pass
-// gives the line length and the sequence's place on it), the (m, l) of up to 64 partials (one
-// per lane), then their acc rows, kMergeBatch partials at a time with all loads in flight.
+// A unit's partials sit at slots (u * kcap + k) * HB + head-in-group, k < n, and the decode
+// kernel records n in unit_n[u], so one round of loads brings everything the merge needs: the
+// row's context (a zero context gives NaN, the reference's 0 * (1 / 0)), n (1: the unit was
+// written whole), the (m, l) of the first 64 slots and the accumulator rows of the first
+// kMergeBatch, taken speculatively up to kcap and masked once n is known.
 constexpr int kMergeBatch = 16;
 
-// Combines np >= 1 partials of one (sequence, q head) into this lane's N output elements:
-//   M = max_j m_j;  w_j = exp2(m_j - M) (0 where l_j = 0);  o[e] = sum_j w_j acc_j[e] in j
-//   order;  returns L = sum_j w_j l_j (the same bits in every lane).
-// ml(p) points at (m, l) of partial p; row(p) at this lane's first accumulator element of
-// partial p, its N elements STEP floats apart. The (m, l) of the first 64 partials and the
-// accumulator rows of the first kMergeBatch go out together: they do not depend on each other.
+// What a merge wavefront loaded: the row's context, the unit's n, and (for n >= 2) the merged
+// accumulators of this lane's N elements in o with L = sum_j w_j l_j (the same bits in every
+// lane). ml(p) points at (m, l) of partial p; row(p) at this lane's first accumulator element
+// of partial p, its N elements STEP floats apart.
+struct UnitMerge {
+  int64_t ctx;
+  int n;
+  float L;
+};
+
 template <int N, int STEP, typename ML, typename ROW>
-__device__ __forceinline__ float merge_partials(int np, ML ml, ROW row, float (&o)[N]) {
+__device__ __forceinline__ UnitMerge merge_unit(const DecodeArgs& a, int b, int64_t u, ML ml,
+                                                ROW row, float (&o)[N]) {
   const int lane = threadIdx.x % kWave;
+  const int kcap = a.kcap;
+  // one round: context, n, the first (m, l) pairs and accumulator rows (slots below kcap)
+  const int64_t ctx = seq_ctx(a, b);
+  const int n_raw = a.unit_n[u];
   float v0[kMergeBatch][N];
 #pragma unroll
   for (int j = 0; j < kMergeBatch; ++j) {
-    const float* src = row(j < np ? j : np - 1);  // in-bounds row; its weight is zeroed below
+    const float* src = row(j < kcap ? j : kcap - 1);
 #pragma unroll
     for (int e = 0; e < N; ++e) v0[j][e] = src[e * STEP];
   }
   float m0 = kNegBig, l0 = 0.f;
-  if (lane < np) {
+  if (lane < kcap) {
     m0 = ml(lane)[0];
     l0 = ml(lane)[1];
+  }
+  UnitMerge r;
+  r.ctx = uniform64(ctx);
+  r.n = __builtin_amdgcn_readfirstlane(n_raw);
+  r.L = 0.f;
+  if (r.ctx == 0 || r.n <= 1) return r;
+  const int np = r.n < kcap ? r.n : kcap;
+  if (lane >= np) {  // slots past the unit's ranges hold older partials
+    m0 = kNegBig;
+    l0 = 0.f;
   }
   float M = m0;
   for (int p = lane + kWave; p < np; p += kWave) M = fmaxf(M, ml(p)[0]);
@@ -364,7 +369,7 @@ __device__ __forceinline__ float merge_partials(int np, ML ml, ROW row, float (&
 #pragma unroll
         for (int j = 0; j < kMergeBatch; ++j)
 #pragma unroll
-          for (int e = 0; e < N; ++e) v[j][e] = v0[j][e];
+          for (int e = 0; e < N; ++e) v[j][e] = j < n ? v0[j][e] : 0.f;
       } else {
 #pragma unroll
         for (int j = 0; j < kMergeBatch; ++j) {
@@ -381,7 +386,8 @@ __device__ __forceinline__ float merge_partials(int np, ML ml, ROW row, float (&
       }
     }
   }
-  return lsh::group_sum<kWave>(L);  // the same bits in every lane (xor / mirror steps)
+  r.L = lsh::group_sum<kWave>(L);  // the same bits in every lane (xor / mirror steps)
+  return r;
 }
 
 template <int D>
@@ -395,42 +401,29 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_kernel
   const int G = a.Hq / a.Hk;
   const int h = hq / G, g = hq % G;
   float* out = a.out + item * D;
-
-  const Plan p = make_plan(a);
-  const RowPlan rp = row_plan(a, p, b);
-  if (rp.ctx == 0) {
+  // partial k of unit u: slot (u * kcap + k) * HB + h % HB; lane holds dims lane + 64 i
+  const int64_t u = static_cast<int64_t>(b) * a.NHG + h / a.HB;
+  const int64_t base = u * a.kcap * a.HB + h % a.HB;
+  const int dl = lane < D ? lane : 0;  // D < 64: lanes past D read dim 0 and write nothing
+  float o[PER];
+  const UnitMerge r = merge_unit<PER, kWave>(
+      a, b, u, [&](int p) { return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2; },
+      [&](int p) { return a.part_acc + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * D + dl; },
+      o);
+  if (r.ctx == 0) {
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       if (lane + i * kWave < D) out[lane + i * kWave] = __builtin_nanf("");
     return;
   }
-  if (rp.n == 1) return;  // written whole by the decode kernel
-  // partial of range first + k: slot base + k * HB; lane holds dims lane + 64 i
-  const int hg = h / a.HB;
-  const int64_t base = (rp.pre + static_cast<int64_t>(hg) * rp.n) * a.HB + h % a.HB;
-  const int np = static_cast<int>(rp.n);
-  const int dl = lane < D ? lane : 0;  // D < 64: lanes past D read dim 0 and write nothing
-  float o[PER];
-  const float L = merge_partials<PER, kWave>(
-      np, [&](int p) { return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2; },
-      [&](int p) { return a.part_acc + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * D + dl; },
-      o);
-  const float inv = 1.f / L;
+  if (r.n <= 1) return;  // written whole by the decode kernel
+  const float inv = 1.f / r.L;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int d = lane + i * kWave;
     if (d < D) out[d] = o[i] * inv;
   }
 }
-
-// Merge writing the o_proj input fragments as well (decode step): one wavefront per (row m,
-// q head) over the mp = 16-row-padded rows, each lane holding CPL = D / 64 consecutive
-// channels of the output row. A split (b, head) is merged as paged_decode_merge_kernel does
-// (same operations in the same order, so the same bits); a whole one is read back from out;
-// a zero context is NaN; rows m >= B are zero. Every row then goes out as
-// x' = out * act_inv (act_inv nullable) in the activation-fragment layout of the batched int4
-// linear (xfrag.h), and each 128-channel block's sum of x' as the same pairwise tree in
-// channel order that the other fragment producers use.
 template <int D>
 __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_frag_kernel(
     DecodeArgs a, const float* __restrict__ act_inv, __bf16* __restrict__ xf,
@@ -453,29 +446,29 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void paged_decode_merge_frag_k
     const int G = a.Hq / a.Hk;
     const int h = hq / G, g = hq % G;
     float* out = a.out + item * D + lane * CPL;
-    const Plan p = make_plan(a);
-    const RowPlan rp = row_plan(a, p, b);
-    const int hg = h / a.HB;
-    if (rp.ctx == 0) {
+    const int64_t u = static_cast<int64_t>(b) * a.NHG + h / a.HB;
+    const int64_t base = u * a.kcap * a.HB + h % a.HB;
+    float whole[CPL];  // the row as the decode kernel wrote it when the unit had one range
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) whole[e] = out[e];
+    float o[CPL];
+    const UnitMerge r = merge_unit<CPL, 1>(
+        a, b, u, [&](int p) { return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2; },
+        [&](int p) {
+          return a.part_acc + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * D + lane * CPL;
+        },
+        o);
+    if (r.ctx == 0) {
 #pragma unroll
       for (int e = 0; e < CPL; ++e) {
         x[e] = __builtin_nanf("");
         out[e] = x[e];
       }
-    } else if (rp.n == 1) {  // written whole by the decode kernel
+    } else if (r.n <= 1) {  // written whole by the decode kernel
 #pragma unroll
-      for (int e = 0; e < CPL; ++e) x[e] = out[e];
+      for (int e = 0; e < CPL; ++e) x[e] = whole[e];
     } else {
-      const int64_t base = (rp.pre + static_cast<int64_t>(hg) * rp.n) * a.HB + h % a.HB;
-      const int np = static_cast<int>(rp.n);
-      float o[CPL];
-      const float L = merge_partials<CPL, 1>(
-          np, [&](int p) { return a.part_ml + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * 2; },
-          [&](int p) {
-            return a.part_acc + ((base + static_cast<int64_t>(p) * a.HB) * G + g) * D + lane * CPL;
-          },
-          o);
-      const float inv = 1.f / L;
+      const float inv = 1.f / r.L;
 #pragma unroll
       for (int e = 0; e < CPL; ++e) {
         x[e] = o[e] * inv;
@@ -609,20 +602,29 @@ int grid_blocks(int64_t D, int64_t G, int64_t Hk, int64_t block_size, int off32 
   return w8 > w32 ? w8 : w32;
 }
 
-// Partial slots the workspace holds: HB per work range. The balanced split has at most one
-// range per resident workgroup, or one per (b, head group) when those outnumber the
-// workgroups; a fixed range size P gives each (b, head group) at most ceil(max context / P).
+// Partial slots per (b, head group) unit: a bound on its ranges. A fixed range size P gives
+// at most ceil(max context / P). The balanced plan's ranges hold at least kMinRange tokens,
+// number at most the resident workgroups W, and the plan raises its range size until the
+// longest unit fits kBalanceSlack x (its fair share W / units) + 1 slots: a unit up to
+// kBalanceSlack x the mean context splits as the balance asks, and the workspace stays near
+// kBalanceSlack x W slots for any batch.
+constexpr int64_t kBalanceSlack = 4;
+
+int64_t unit_slots(int64_t B, int64_t D, int64_t G, int64_t Hk, int64_t max_blocks,
+                   int64_t block_size, int64_t partition_size) {
+  const int64_t cap = max_blocks * block_size;
+  if (partition_size > 0) return std::max<int64_t>(1, (cap + partition_size - 1) / partition_size);
+  const int64_t w = grid_blocks(D, G, Hk, block_size);
+  const int64_t units = B * (Hk / heads_per_block(Hk));
+  const int64_t fair = (kBalanceSlack * w + units - 1) / units + 1;
+  return std::max<int64_t>(1, std::min({w, (cap + kMinRange - 1) / kMinRange, fair}));
+}
+
+// Partial slots the workspace holds: HB per (unit, range in unit).
 int64_t partial_slots(int64_t B, int64_t Hk, int64_t D, int64_t G, int64_t max_blocks,
                       int64_t block_size, int64_t partition_size) {
   const int64_t hb = heads_per_block(Hk), nhg = Hk / hb;
-  int64_t ranges;
-  if (partition_size > 0) {
-    ranges = B * nhg * ((max_blocks * block_size + partition_size - 1) / partition_size);
-  } else {
-    ranges = grid_blocks(D, G, Hk, block_size);
-    if (B * nhg > ranges) ranges = B * nhg;
-  }
-  return ranges * hb;
+  return B * nhg * unit_slots(B, D, G, Hk, max_blocks, block_size, partition_size) * hb;
 }
 
 }  // namespace
@@ -635,7 +637,8 @@ extern "C" int64_t llmserve_paged_attention_workspace_bytes(int64_t B, int64_t H
   if (Hq % Hk != 0 || Hq / Hk > 8) return 0;
   const int64_t G = Hq / Hk;
   const int64_t slots = partial_slots(B, Hk, D, G, max_blocks, block_size, partition_size);
-  return slots * G * (D + 2) * static_cast<int64_t>(sizeof(float));
+  const int64_t units = B * (Hk / heads_per_block(Hk));
+  return slots * G * (D + 2) * static_cast<int64_t>(sizeof(float)) + units * 4;
 }
 
 namespace {
@@ -684,7 +687,8 @@ int decode_paged(const float* q, const CacheView& c, const int64_t* block_tables
                 lsh::aligned16(out) && (q_mult == nullptr || lsh::aligned16(q_mult)),
             "paged_attention: q, caches, out and q_mult must be 16-byte aligned");
   const int64_t slots = partial_slots(B, Hk, D, G, max_blocks, block_size, partition_size);
-  const int64_t need = slots * G * (D + 2) * static_cast<int64_t>(sizeof(float));
+  const int64_t units = B * (Hk / heads_per_block(Hk));
+  const int64_t need = slots * G * (D + 2) * static_cast<int64_t>(sizeof(float)) + units * 4;
   LSH_CHECK(workspace != nullptr && workspace_bytes >= need,
             "paged_attention: workspace of %lld bytes needed, %lld given", (long long)need,
             (long long)workspace_bytes);
@@ -706,6 +710,8 @@ int decode_paged(const float* q, const CacheView& c, const int64_t* block_tables
   float* ws = static_cast<float*>(workspace);
   a.part_ml = ws;
   a.part_acc = ws + slots * G * 2;
+  a.unit_n = reinterpret_cast<int*>(ws + slots * G * (D + 2));
+  a.kcap = static_cast<int>(unit_slots(B, D, G, Hk, max_blocks, block_size, partition_size));
   a.num_slots = num_slots;
   a.range = partition_size > 0 ? partition_size : 0;
   a.B = static_cast<int>(B);
@@ -820,7 +826,7 @@ extern "C" int llmserve_paged_attention_rows_f32(
 // each GPU the library runs on holds its own copy until the process ends. Calls that overlap
 // on one GPU share it and race; nothing in it needs clearing (the merge reads only partials
 // the same call's decode kernel wrote).
-constexpr int64_t kNoAllocScratchBytes = 16LL << 20;
+constexpr int64_t kNoAllocScratchBytes = 32LL << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {

@@ -81,7 +81,7 @@ def test_paged_attention_workspace_size(lib):
         # straddle two units)
         nhg, G = Hk // HB, Hq // Hk
         ranges = B * nhg * -(-max_blocks * bs // P)
-        return ranges * HB * G * (D + 2) * 4
+        return ranges * HB * G * (D + 2) * 4 + B * nhg * 4  # + each unit's range count
 
     # 8 kv heads share a workgroup; one range covers a whole unit
     assert ws(4, 16, 8, 128, 4, 16, 10_000) == expect(4, 16, 8, 128, 4, 16, 10_000, 8)
@@ -92,6 +92,12 @@ def test_paged_attention_workspace_size(lib):
     # 16 kv heads: two groups of 8
     assert ws(3, 32, 16, 64, 5, 16, 40) == expect(3, 32, 16, 64, 5, 16, 40, 8)
     assert ws(0, 16, 8, 128, 16, 16, 32) == 0
+    # the balanced plan (P = 0) bounds each unit's slots by a multiple of its share of the
+    # grid, so a large batch's workspace does not grow with the context bound, and stays
+    # within the fixed 64-token split's
+    assert ws(256, 32, 8, 128, 2048, 16, 0) == ws(256, 32, 8, 128, 4096, 16, 0)
+    assert ws(256, 32, 8, 128, 2048, 16, 0) < ws(256, 32, 8, 128, 2048, 16, 64)
+    assert ws(1, 32, 8, 128, 64, 16, 0) <= ws(1, 32, 8, 128, 64, 16, 64)
 
 
 def test_single_hip_runtime_with_torch():

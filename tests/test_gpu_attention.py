@@ -114,6 +114,29 @@ def test_baseline_config4_size(gpu):
     assert torch.equal(out3, out)
 
 
+def test_skewed_batch_within_unit_slots(gpu):
+    """One long sequence among 255 short ones: the workspace holds a few times each unit's
+    fair share of ranges, so the plan widens the ranges until the long unit fits; the result
+    still matches float64 and a fixed partition size."""
+    c = make_case(77, 256, 16, 8, 64, 16, 1, 24, outlier=False, slack_blocks=300)
+    bs = 16
+    long_blocks = 250  # 4000 tokens in blocks past the short rows' blocks
+    nb = c["kq"].shape[0] // bs
+    width = max(c["bt"].shape[1], long_blocks)
+    bt = np.zeros((256, width), np.int64)
+    bt[:, :c["bt"].shape[1]] = c["bt"]
+    bt[100, :long_blocks] = np.random.default_rng(3).permutation(nb)[:long_blocks]
+    cl = c["cl"].copy()
+    cl[100] = long_blocks * bs
+    ref = mr.paged_decode_f64(oq.q_smooth(c["q"], c["q_mult"]), mr.kv_dequantize(c["kq"], c["ks"]),
+                              mr.kv_dequantize(c["vq"], c["vs"]), bt, cl, bs, 0.125)
+    args = [cu.dev(a) for a in (c["q"], c["kq"], c["vq"], c["ks"], c["vs"], bt, cl)]
+    out = cu.paged_decode_int8(*args, bs, 0.125, 0, cu.dev(c["q_mult"]))
+    cu.assert_rel_close(out, ref, TOL, "skewed batch, balanced plan")
+    out64 = cu.paged_decode_int8(*args, bs, 0.125, 64, cu.dev(c["q_mult"]))
+    cu.assert_rel_close(out64, ref, TOL, "skewed batch, 64-token partitions")
+
+
 def test_cache_beyond_4gb(gpu):
     """A cache tensor of more than 4 GB (num_slots * Hk * D > 2^32) takes the kernel variant
     with 64-bit slot addressing; its sequences live in blocks past the 4 GB mark. The used
