@@ -8,8 +8,8 @@
 // the group, which run the same tokens: together they read whole HB * D-byte pieces of every
 // slot row (all of it when HB = Hk), so the cache streams in long contiguous runs. A range that
 // is its unit's only one writes the output rows; the others write a partial (running max, sum,
-// acc) per head to slot j * HB + head-in-group (j = range index), and the merge kernel combines
-// the partials of every split unit.
+// acc) per head to slot (u * kcap + k) * HB + head-in-group (unit u, range k of the unit, kcap
+// slots per unit), and the merge kernel combines the partials of every split unit.
 //
 // Lane layout inside a wavefront (D = head dim, LPR = D / 16 lanes per token row):
 //   lane = r * LPR + seg : row slot r of the RPW = 64 / LPR tokens of one step, dims
