@@ -15,8 +15,13 @@
 // layout). Per block of 128 channels:
 //   * x (8 KB per row tile) is staged in LDS for all wavefronts, double-buffered, one block
 //     ahead;
-//   * each lane loads its A operand directly: row l % 16, channels 32 (l / 16) .. + 32, one
-//     128-byte line kept in L1 over its 8 loads, two blocks ahead (8 KB per wavefront);
+//   * each lane loads its A operand directly, two blocks ahead (8 KB per wavefront): row
+//     l % 16, channels 16 i + 4 (l / 16) .. + 4 for i = 0 .. 7, so that one load instruction
+//     reads 64 contiguous bytes of each of 16 rows (16 cache lines; a lane-contiguous 128 bytes
+//     per lane would touch 64 lines per instruction and stall the address unit);
+//   * the products' k order is therefore permuted: step q's lane group g = l / 16 takes
+//     channels 32 q + 4 g .. + 4 and 32 q + 16 + 4 g .. + 4, and x's fragments are rearranged
+//     to match as they are staged (8-byte halves of the fragment pieces);
 //   * 4 steps x 4 row tiles x 4 products = 64 MFMAs.
 // The output lane holds vocab rows 4 (l / 16) .. + 4 of batch row l % 16: one 16-byte store.
 #include "common.h"
@@ -75,6 +80,7 @@ __global__ __launch_bounds__(kWaves * kWave) void lm_head_f32_kernel(LmArgs a) {
 
   // x staging: 16-byte piece p = tid + 512 i of the hi and mid parts of the T (row tile,
   // block) fragments; within one, piece (2 q + h) * 64 + lane comes from step q, part h
+  // (lane = fr + 16 fc: row fr, channels 32 fc + 8 q .. + 8)
   constexpr int kPer = T * kTilePieces / (kWaves * kWave);
   auto load_x = [&](int b, u32x4 (&r)[kPer]) {
 #pragma unroll
@@ -86,18 +92,33 @@ __global__ __launch_bounds__(kWaves * kWave) void lm_head_f32_kernel(LmArgs a) {
                     (lsh::kFragPieces * kWave) + (qh % 2) * kWave + l];
     }
   };
+  // Staged in the products' k order: source piece (step q', part h, lane fr + 16 fc) holds
+  // channels 32 fc + 8 q' + 4 hf .. + 4 in its half hf; they belong to step fc, lane group
+  // g = 2 (q' & 1) + hf, in the low half of that piece when q' < 2, else the high half.
   auto store_x = [&](int buf, const u32x4 (&r)[kPer]) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) xs[buf][tid + i * kWaves * kWave] = r[i];
+    for (int i = 0; i < kPer; ++i) {
+      const int p = tid + i * kWaves * kWave;
+      const int t = p / kTilePieces, within = p % kTilePieces;
+      const int qh = within / kWave, l = within % kWave;
+      const int qs = qh / 2, h = qh % 2, fr = l % 16, fc = l / 16;
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int g = 2 * (qs & 1) + hf;
+        u32x2* d = reinterpret_cast<u32x2*>(&xs[buf][t * kTilePieces + (2 * fc + h) * kWave + fr + 16 * g]);
+        d[qs >> 1] = u32x2{r[i][2 * hf], r[i][2 * hf + 1]};
+      }
+    }
   };
-  // a lane's 128 contiguous bytes of its W row in the block (kept in L1 over the 8 loads)
+  // a lane's W channels 16 i + 4 (lane / 16) .. + 4 (i = 0 .. 7) of its row in the block
   auto load_w = [&](int s, u32x4 (&r)[8]) {
     const int v = vtile(s) * kVRows + wave * 16 + lane % 16;
     const int vr = v < a.V ? v : a.V - 1;  // loads stay in bounds
     const u32x4* p = reinterpret_cast<const u32x4*>(a.w + static_cast<int64_t>(vr) * a.K +
-                                                    (s % a.nblk) * lsh::kFragBlk + 32 * (lane / 16));
+                                                    (s % a.nblk) * lsh::kFragBlk + 4 * (lane / 16));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = p[i];
+    for (int i = 0; i < 8; ++i) r[i] = p[4 * i];
   };
 
   f32x4 acc[T];
