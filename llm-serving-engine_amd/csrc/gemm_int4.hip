@@ -47,6 +47,7 @@ constexpr int kCols = 16 * kNT;        // output channels per wavefront
 constexpr int kWaves = 4;              // wavefronts of the x-split workgroups
 constexpr int kSplitWaves = 4;         // largest K split
 constexpr int kMaxPlanes = 8;          // largest K split across workgroups (output planes)
+constexpr int64_t kWideTiles = 4096;   // slab x row tiles from which int4_gemm_wide runs
 
 // x' = x * inv -> xh, xl (bf16, round to nearest even) and xsum[b, m] = sum of x' over block
 // b. One wavefront per (m, b): lane i holds channels 2i, 2i + 1 of the block. xsum rows are
@@ -410,8 +411,10 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
         }
         const float s1 = on * sc[kb][u];
         const float zz = on * zc[kb][u];
+        // one explicit form (s1 d + (zz xs rounded), then the sum), so that every kernel
+        // computing a block's term rounds it the same way
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[u][r] += s1 * d[r] + zz * xs[kb][r];
+        for (int r = 0; r < 4; ++r) acc[u][r] += __builtin_fmaf(s1, d[r], zz * xs[kb][r]);
       }
     }
   }
@@ -442,6 +445,99 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_lat(Int4GemmArgs a, int s
   }
 }
 
+// Very wide outputs (an LM head: thousands of slabs). int4_gemm_lat re-reads a row tile's x
+// fragments for every slab it computes (96 KB per 64 output channels at K = 1024: ten times
+// the nibble bytes). Here the S = K / 128 wavefronts of a workgroup each keep one K block's x
+// fragments and channel sums in registers, and the workgroup runs a range of slabs for one
+// row tile, loading each slab's nibbles and scales one slab ahead. The per-block arithmetic
+// and the fixed-order sum of the S partials in LDS are int4_gemm_lat<1, S>'s. Workgroups of
+// the mtiles row tiles of one slab range are numbered onto one XCD, so that a slab's nibbles
+// come from HBM into that XCD's L2 once.
+template <int S>
+__global__ __launch_bounds__(S * kWave) __attribute__((amdgpu_waves_per_eu(4)))
+void int4_gemm_wide(Int4GemmArgs a, int mtiles, int groups) {
+  __shared__ f32x4 red[S * kNT * kWave];
+  const int lane = threadIdx.x % kWave, ks = threadIdx.x / kWave;
+  const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+  const int t = j % mtiles;
+  const int grp = (j / mtiles) * 8 + xcd;  // slab range of this workgroup
+  const int slabs = (a.N + kCols - 1) / kCols;
+  const int s0 = static_cast<int>(static_cast<int64_t>(grp) * slabs / groups);
+  const int s1 = static_cast<int>(static_cast<int64_t>(grp + 1) * slabs / groups);
+  if (grp >= groups || s0 >= s1) return;  // whole workgroup: no barrier is reached
+  const int fr = lane % 16, fc = lane / 16;
+  const int b = ks, g = b / a.bpg;  // this wavefront's K block (S == K / 128)
+  const int m0 = t * kRows;
+
+  u32x4 xh[4], xm[4], xl[4];
+  constexpr int P = lsh::kFragPieces;
+  const __bf16* xt = a.xh + ((static_cast<int64_t>(t) * S + b) * 4 * P) * kPkFrag + 8 * lane;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    xh[q] = *reinterpret_cast<const u32x4*>(xt + (P * q) * kPkFrag);
+    xm[q] = *reinterpret_cast<const u32x4*>(xt + (P * q + 1) * kPkFrag);
+    xl[q] = *reinterpret_cast<const u32x4*>(xt + (P * q + 2) * kPkFrag);
+  }
+  const f32x4 xs = *reinterpret_cast<const f32x4*>(a.xsum + static_cast<int64_t>(b) * a.mp + m0 + 4 * fc);
+
+  auto load_w = [&](int slab, u32x4 (&w)[kNT], f32x4& s4, f32x4& z4) {
+    const uint8_t* wt = a.w + ((static_cast<int64_t>(slab) * S + b) * kNT) * kPkTile + 16 * lane;
+#pragma unroll
+    for (int u = 0; u < kNT; ++u)
+      w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wt + u * kPkTile));
+    const float* st = a.s + ((static_cast<int64_t>(g) * slabs + slab) * 16 + fr) * 8;
+    s4 = *reinterpret_cast<const f32x4*>(st);
+    z4 = *reinterpret_cast<const f32x4*>(st + 4);  // z - 8 s
+  };
+  auto run = [&](int slab, const u32x4 (&w)[kNT], const f32x4& s4, const f32x4& z4) {
+#pragma unroll
+    for (int u = 0; u < kNT; ++u) {
+      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bf16x8 bq = nibbles_bf16(w[u][q]);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xh[q]), bq, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xm[q]), bq, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xl[q]), bq, d, 0, 0, 0);
+      }
+      const float s1 = s4[u], zz = z4[u];
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += __builtin_fmaf(s1, d[r], zz * xs[r]);  // as int4_gemm_lat
+      red[(ks * kNT + u) * kWave + lane] = acc;
+    }
+    __syncthreads();
+    if (ks < kNT) {  // wavefront ks finishes channel tile u = ks
+      const int u = ks;
+      f32x4 v = red[u * kWave + lane];
+#pragma unroll
+      for (int k = 1; k < S; ++k) v += red[(k * kNT + u) * kWave + lane];
+      const int n = slab * kCols + 16 * u + fr;
+      if (n < a.N) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 4 * fc + r;
+          if (m < a.M) a.y[static_cast<int64_t>(m) * a.N + n] = v[r];
+        }
+      }
+    }
+    __syncthreads();  // red is rewritten by the next slab
+  };
+
+  // two register sets, each slab's loads issued before the previous slab's products; past the
+  // range the last slab is loaded again (unused), so the loads stay unconditional
+  u32x4 wa[kNT], wb[kNT];
+  f32x4 sa, za, sb, zb;
+  load_w(s0, wa, sa, za);
+  for (int sl = s0; sl < s1; sl += 2) {
+    load_w(sl + 1 < s1 ? sl + 1 : s1 - 1, wb, sb, zb);
+    run(sl, wa, sa, za);
+    if (sl + 1 >= s1) break;
+    load_w(sl + 2 < s1 ? sl + 2 : s1 - 1, wa, sa, za);
+    run(sl + 1, wb, sb, zb);
+  }
+}
+
 int64_t xsum_rows(int64_t M) { return (M + kRows - 1) / kRows * kRows; }
 
 template <int KB, int S>
@@ -462,6 +558,26 @@ void launch_lat_ks(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int pla
 // below.
 void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all, hipStream_t st,
                 int planes = 1) {
+  // very wide outputs with K = 512 or 1024: int4_gemm_wide, about two workgroups per CU
+  if (planes == 1 && (nb_all == 4 || nb_all == 8) && slabs * mtiles >= kWideTiles) {
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) {
+      int c = 0;
+      if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
+        cus = c;
+    }
+    int64_t groups = (2 * cus + mtiles - 1) / mtiles;
+    groups = std::min<int64_t>(groups, slabs / 2);
+    groups = std::max<int64_t>(8, (groups + 7) / 8 * 8);
+    const dim3 grid(static_cast<unsigned>(mtiles * groups));
+    if (nb_all == 8)
+      lsh::launch(int4_gemm_wide<8>, grid, dim3(8 * kWave), 0, st, true, a, static_cast<int>(mtiles),
+                  static_cast<int>(groups));
+    else
+      lsh::launch(int4_gemm_wide<4>, grid, dim3(4 * kWave), 0, st, true, a, static_cast<int>(mtiles),
+                  static_cast<int>(groups));
+    return;
+  }
   const int bpp = (nb_all + planes - 1) / planes;  // blocks per plane
   const int nb = bpp;
   int KB = std::min(2, (nb + 7) / 8);

@@ -154,6 +154,25 @@ def test_packed_gemm_tails(gpu, M, N, K, g):
     cu.assert_rel_close(y, mr.int4_linear_f64(x, nib, gs, gz, g, inv), TOL, f"M={M} {N}x{K} g{g}")
 
 
+@pytest.mark.parametrize("M,N,K", [(64, 151936, 1024), (20, 2049 * 64 - 24, 512)])
+def test_packed_gemm_wide_outputs(gpu, M, N, K):
+    """Outputs of thousands of slabs (an LM head) run the slab-looping kernel that keeps each
+    K block's x fragments in registers: against float64, and bit for bit against the same
+    columns computed in chunks narrow enough for the per-slab kernel (same per-block
+    arithmetic, same order of the partial sums)."""
+    x, nib, gs, gz, inv = _case(M, N, K, 128, M + N + K)
+    packed = cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), 128)
+    y = cu.int4_linear_gemm_packed(cu.dev(x), packed, N, 128, cu.dev(inv))
+    cu.assert_rel_close(y, mr.int4_linear_f64(x, nib, gs, gz, 128, inv), TOL, f"M={M} {N}x{K}")
+    chunk = 512 * 64 if M > 32 else 1024 * 64  # below the wide kernel's slab count
+    parts = []
+    for c0 in range(0, N, chunk):
+        c1 = min(N, c0 + chunk)
+        pk = cu.int4_gemm_pack(cu.dev(nib[c0:c1]), cu.dev(gs[c0:c1]), cu.dev(gz[c0:c1]), 128)
+        parts.append(cu.int4_linear_gemm_packed(cu.dev(x), pk, c1 - c0, 128, cu.dev(inv)))
+    assert torch.equal(y, torch.cat(parts, 1)), f"M={M} {N}x{K}: wide kernel != per-slab kernel"
+
+
 def _gemm_xfrag_split(xf, packed, M, N, K, g, P):
     L = cu.capi()
     y = torch.full((P, M, N), float("nan"), dtype=torch.float32, device=xf.device)
