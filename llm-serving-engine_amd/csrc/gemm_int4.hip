@@ -558,8 +558,9 @@ void launch_lat_ks(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int pla
 // below.
 void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all, hipStream_t st,
                 int planes = 1) {
-  // very wide outputs with K = 512 or 1024: int4_gemm_wide, about two workgroups per CU
-  if (planes == 1 && (nb_all == 4 || nb_all == 8) && slabs * mtiles >= kWideTiles) {
+  // very wide outputs (at least 256 slabs) with K = 512 or 1024: int4_gemm_wide, about two
+  // workgroups per CU
+  if (planes == 1 && (nb_all == 4 || nb_all == 8) && slabs >= 256 && slabs * mtiles >= kWideTiles) {
     int cus = 256, dev = 0;
     if (hipGetDevice(&dev) == hipSuccess) {
       int c = 0;
