@@ -527,7 +527,7 @@ __device__ void attention_range(const ChainArgs& a, const AttnPlan& pl, uint32_t
 // (max, sum) words of the row's np partials (the producers store them after the
 // accumulators), then every wavefront takes the (max, sum) words (lane p) and the
 // accumulators of partials v, v + 8, ... (wavefront v) in one polling round, and the merge is
-// the decode merge's (paged_decode.hip, merge_partials): M = max_p m_p, w_p = exp2(m_p - M) (0
+// the decode merge's (paged_decode.hip, merge_unit): M = max_p m_p, w_p = exp2(m_p - M) (0
 // where the sum is 0), out = (sum_p w_p acc_p) / (sum_p w_p l_p), the wavefronts' sums added
 // in wavefront order (a row without context gets NaN). The row goes to exb (all replicas) for
 // the o_proj stage. `red2` is 2 kThreads floats of LDS. Returns false when a wait ran out of
