@@ -137,6 +137,43 @@ def test_skewed_batch_within_unit_slots(gpu):
     cu.assert_rel_close(out64, ref, TOL, "skewed batch, 64-token partitions")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_batches_vs_f64(gpu, seed):
+    """Seeded random batches across the split's regimes: 1 to 300 rows (one or several
+    64-row windows of the plan), contexts uniform, skewed (one long row) or with empty rows,
+    several head geometries and block sizes, the balanced split or a random fixed partition
+    size. Rows with an empty context must be NaN, every other row within 1e-5 of float64."""
+    rng = np.random.default_rng(1000 + seed)
+    Hq, Hk, D = [(16, 8, 128), (8, 8, 64), (32, 4, 128), (12, 4, 64)][seed % 4]
+    bs = [16, 32, 8][seed % 3]
+    B = int(rng.choice([1, 3, 17, 64, 65, 130, 300]))
+    c = make_case(seed, B, Hq, Hk, D, bs, 1, 300, outlier=seed % 2 == 0, slack_blocks=40)
+    cl = c["cl"].copy()
+    kind = seed % 3
+    nb = c["kq"].shape[0] // bs
+    bt = c["bt"]
+    if kind == 1:  # one long row over blocks shared with the others
+        long_blocks = min(nb, 120)
+        bt = np.zeros((B, max(bt.shape[1], long_blocks)), np.int64)
+        bt[:, :c["bt"].shape[1]] = c["bt"]
+        r = int(rng.integers(B))
+        bt[r, :long_blocks] = rng.permutation(nb)[:long_blocks]
+        cl[r] = long_blocks * bs - int(rng.integers(bs))
+    elif kind == 2:  # some empty rows
+        cl[rng.random(B) < 0.2] = 0
+    scale = D ** -0.5
+    ref = mr.paged_decode_f64(oq.q_smooth(c["q"], c["q_mult"]), mr.kv_dequantize(c["kq"], c["ks"]),
+                              mr.kv_dequantize(c["vq"], c["vs"]), bt, np.maximum(cl, 1), bs, scale)
+    args = [cu.dev(a) for a in (c["q"], c["kq"], c["vq"], c["ks"], c["vs"], bt, cl)]
+    part = 0 if seed % 4 < 2 else int(rng.integers(1, 200))
+    out = cu.paged_decode_int8(*args, bs, scale, part, cu.dev(c["q_mult"])).cpu().numpy()
+    empty = cl == 0
+    assert np.isnan(out[empty]).all(), f"seed {seed}: empty rows must be NaN"
+    if (~empty).any():
+        cu.assert_rel_close(torch.from_numpy(out[~empty]), ref[~empty], TOL,
+                            f"seed {seed}: B={B} H{Hq}/{Hk} D{D} bs{bs} part {part} kind {kind}")
+
+
 def test_cache_beyond_4gb(gpu):
     """A cache tensor of more than 4 GB (num_slots * Hk * D > 2^32) takes the kernel variant
     with 64-bit slot addressing; its sequences live in blocks past the 4 GB mark. The used
