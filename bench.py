@@ -743,6 +743,10 @@ def profile_only(torch, dev, what: str) -> int:
             gemv.int4_linear_gemm_packed(x, pk, N, GROUP, inv)
     elif what == "c5step":  # config 5's decode step: 2 + 10 graph replays, fp32 LM head
         c5_decode(torch, dev, 10, 2, profile=True)
+    elif what == "c5step1":  # the config-5 model at batch 1: the per-layer chain, then per-op
+        from llmserve.transformer import QWEN3_0_6B, QuantCausalLM
+
+        small_batch_decode(torch, dev, QuantCausalLM(QWEN3_0_6B, GROUP, seed=5, device=dev), 1, 20)
     elif what == "attention":
         copies, q, cl, qm, bs, D, _ = c4_inputs(torch, dev)
         pa = load_paged_attention()
@@ -779,7 +783,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
     ap.add_argument("--only", choices=["gemv", "gemm4", "attention", "prefill", "lmhead", "copy",
-                                       "c5step"],
+                                       "c5step", "c5step1"],
                     help="profiling run: only launch that kernel (64 times) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
