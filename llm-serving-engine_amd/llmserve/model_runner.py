@@ -59,6 +59,25 @@ class ModelRunner:
                 else:
                     c.index_copy_(0, dst.to(c.device), c.index_select(0, src.to(c.device)))
 
+    def _check_tables(self, tables, ctx_lens) -> None:
+        """Every block a context uses must lie inside the cache. The reference's cache write
+        (``index_copy_``, attention.py:159-162) raises on a slot past the cache; the native
+        write kernels skip such slots instead, so the host checks the tables it already holds
+        (no device synchronization) and raises the same way."""
+        if not tables:
+            return
+        bs = self.block_size
+        slots = self.cache.num_blocks * bs
+        for t, c in zip(tables, ctx_lens):
+            used = np.asarray(t[: -(-c // bs)], dtype=np.int64)
+            if used.size == 0:
+                continue  # a table too short is reported by the metadata build
+            lo, hi = int(used.min()), int(used.max())
+            if lo < 0 or (hi + 1) * bs > slots:
+                bad = lo if lo < 0 else hi
+                raise IndexError(f"index_copy_(): block {bad} (slots {bad * bs}..{bad * bs + bs - 1})"
+                                 f" is out of bounds for a cache of {slots} slots")
+
     def _decode_step_ok(self, q_lens: list[int], logit_rows: list[int]) -> bool:
         m = self.model
         return (self.fused_decode and isinstance(m, QuantCausalLM)
@@ -94,15 +113,18 @@ class ModelRunner:
         for i in sample_rows:
             k = (num_logits or {}).get(i, 1)
             rows += range(last[i] - k + 1, last[i] + 1)
+        self._check_tables(tables, ctx_lens)
         m = self.model
-        if not rows:
-            return torch.empty(0, m.cfg.vocab_size)
+        # The forward always runs, also when no row is sampled: a step made only of non-final
+        # prompt chunks (chunked prefill) writes its K/V here and samples nothing.
         if self._decode_step_ok(q_lens, rows):
             return self._decode(ids, ctx_lens, tables, rows)
         meta = AttentionMetadata.build(q_lens, ctx_lens, tables, self.block_size, self.device,
                                        self.attention_backend)
         hidden = m(torch.tensor(ids, dtype=torch.long, device=self.device),
                    torch.tensor(pos, dtype=torch.long, device=self.device), self.cache.layers, meta)
+        if not rows:
+            return torch.empty(0, m.cfg.vocab_size)
         sel = torch.tensor(rows, dtype=torch.long, device=self.device)
         return m.compute_logits(hidden.index_select(0, sel)).float().cpu()
 
@@ -123,8 +145,13 @@ class ModelRunner:
         h = m.forward_decode(torch.tensor(ids, dtype=torch.long, device=dev),
                              torch.tensor(ctx_lens, dtype=torch.long, device=dev),
                              torch.from_numpy(bt).to(dev), self.cache.layers, bs)
-        logits = m.compute_logits(h, B if m._lm_frag(B) else None)
-        return logits.index_select(0, torch.tensor(rows, device=dev)).float().cpu()
+        if not rows:
+            out = torch.empty(0, m.cfg.vocab_size)
+        else:
+            logits = m.compute_logits(h, B if m._lm_frag(B) else None)
+            out = logits.index_select(0, torch.tensor(rows, device=dev)).float().cpu()
+        m.check_chain()  # after the copy's synchronization: a chain that gave up raises
+        return out
 
 
 class DecodeRunner:
@@ -234,3 +261,12 @@ class DecodeRunner:
         self._advance()
         self.graph.replay()
         return self.ids
+
+    def check(self) -> None:
+        """Raises when a decode-chain launch of the steps since the last check gave up on a
+        hand-off wait (the tokens those steps produced are invalid). ``step`` and ``replay``
+        never synchronize; a caller that reads the ids on the host calls this alongside.
+        Synchronizes."""
+        if getattr(self.model, "_chain_ws", None) is not None:
+            self.model._chain_pending = True  # graph replays launch the chain without the flag
+        self.model.check_chain()

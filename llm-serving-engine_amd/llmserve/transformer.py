@@ -231,6 +231,19 @@ class QuantCausalLM(nn.Module):
                                                  ctypes.byref(err)))
         return err.value
 
+    def check_chain(self) -> None:
+        """Raises when a chain launch since the last check gave up on a hand-off wait (its
+        workgroups then left rows of the step's outputs unwritten, so the step is invalid).
+        Clears the error word first, so the next step starts clean. Synchronizes; a no-op when
+        no chain step ran since the last check."""
+        if not getattr(self, "_chain_pending", False):
+            return
+        self._chain_pending = False
+        if self.chain_error():
+            self.chain_workspace()[8:12].zero_()  # ctl[2], the error word (a fill kernel)
+            raise RuntimeError("decode_chain: a hand-off wait ran out of polls (spin_limit "
+                               f"{self.chain_spin_limit}); the step's outputs are invalid")
+
     def _chain(self, *, rows, x_out, q_in=None, attn_caches=None, x_in=None, ids=None,
                layer=None, nxt=None, h_out=None, q_out=None, caches=None, context_lens=None,
                block_tables=None, block_size=16, spin_limit=None) -> None:
@@ -278,6 +291,7 @@ class QuantCausalLM(nn.Module):
                  self.chain_spin_limit if spin_limit is None else spin_limit,
                  ctypes.c_void_p(torch.cuda.current_stream(ws.device).cuda_stream)]
         check(capi().llmserve_decode_chain(*args))
+        self._chain_pending = True
 
     def _forward_decode_chain(self, ids, context_lens, block_tables, kv_layers, block_size):
         """forward_decode for 1..4 rows: an embedding + layer-0 qkv launch, then one launch

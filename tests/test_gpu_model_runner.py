@@ -172,3 +172,82 @@ def test_calibrate_k_smoothing(gpu):
         att.resolve_backend = orig
     assert torch.equal(f_torch[0], f_hip[0])
     torch.testing.assert_close(f_torch[1], f_hip[1], rtol=1e-4, atol=1e-6)
+
+
+def _prompt_runs(kv_dtype, layers, chunks, first_rows, seed=13, prompt=300):
+    """A ``prompt``-token prompt prefilled in ``chunks`` (new-token counts, one execute each;
+    every chunk but the last samples ``first_rows``), then one decode step through the fused
+    step. Returns (final prefill logits, decode logits, cache snapshots after each execute)."""
+    cfg, model, cache, runner, tables, rng = _setup(seed, "hip", [prompt + 1], kv_dtype, layers)
+    toks = rng.integers(0, cfg.vocab_size, prompt + 1).tolist()
+    snaps, done, out = [], 0, None
+    for i, n in enumerate(chunks):
+        seq = _Seq(toks[:prompt], done, tables[0])
+        rows = [0] if i == len(chunks) - 1 else first_rows
+        out = runner.execute(_sched([seq], [n]), rows)
+        assert out.shape == (len(rows), cfg.vocab_size)
+        done += n
+        snaps.append([[t.clone() for t in _cache_tensors(k) + _cache_tensors(v)]
+                      for k, v in cache.layers])
+    seq = _Seq(toks, prompt, tables[0])
+    dec = runner.execute(_sched([seq], [1]), [0])
+    return out, dec, snaps
+
+
+def _cache_tensors(c):
+    return [c.data, c.scale] if hasattr(c, "scale") else [c]
+
+
+@pytest.mark.parametrize("kv_dtype,layers", [("int8", 1), ("int8", 2), ("auto", 2)])
+def test_chunked_prefill_step_without_sampled_rows(gpu, kv_dtype, layers):
+    """A step made only of a non-final prompt chunk samples nothing (the reference engine's
+    execute(sched, []) during chunked prefill, engine.py:323-333) but must still run the
+    forward and write the chunk's K/V (model_runner.py:66-83)."""
+    quiet, _, snaps_q = _prompt_runs(kv_dtype, layers, [160, 140], [])
+    loud, _, snaps_l = _prompt_runs(kv_dtype, layers, [160, 140], [0])
+    # the step that samples nothing writes exactly what the same step sampling a row writes
+    for a, b in zip(snaps_q, snaps_l):
+        for la, lb in zip(a, b):
+            assert all(torch.equal(x, y) for x, y in zip(la, lb))
+    assert torch.equal(quiet, loud)
+    # and the result equals a one-chunk prefill. Its 300-row linears run another kernel than
+    # the 160- and 140-row chunks (rounding ~1e-6 apart), so even layer 0's int8 K/V rows can
+    # land one step apart (checked below): the two-layer int8 tolerance for every int8 case.
+    one, dec_one, snaps_one = _prompt_runs(kv_dtype, layers, [300], [])
+    _, dec_two, _ = _prompt_runs(kv_dtype, layers, [160, 140], [])
+    tol = logit_tol(2, kv_dtype)
+    for x, y in ((quiet, one), (dec_two, dec_one)):
+        err = float((x.double() - y.double()).abs().max() / y.double().abs().max())
+        assert err < tol, err
+    for layer, (la, lb) in enumerate(zip(snaps_q[-1], snaps_one[-1])):
+        if kv_dtype == "int8":
+            # layer 0 sees only the linears' rounding; deeper layers also the attention over
+            # layer 0's differing int8 steps
+            share = 0.01 if layer == 0 else 0.05
+            for x, y in ((la[0], lb[0]), (la[2], lb[2])):
+                d = (x.to(torch.int32) - y.to(torch.int32)).abs()
+                assert int(d.max()) <= 1 and float((d > 0).float().mean()) < share
+        else:
+            for x, y in zip(la, lb):
+                assert float((x - y).abs().max()) <= 1e-4 * float(y.abs().max())
+
+
+def test_execute_raises_when_the_decode_chain_gives_up(gpu):
+    """A decode chain whose hand-off waits get a single poll gives up (error word set, rows
+    unwritten): execute raises instead of returning logits from unwritten rows, clears the
+    word, and a step with the normal poll budget then runs."""
+    cfg, model, cache, runner, tables, rng = _setup(17, "hip", [90], "int8", 2)
+    assert model._chain_ok(1)
+    seq = _Seq(rng.integers(0, cfg.vocab_size, 90).tolist(), 89, tables[0])
+    model.chain_spin_limit = 0
+    raised = 0
+    for _ in range(20):  # a single poll is rarely enough for every wait of a step
+        try:
+            runner.execute(_sched([seq], [1]), [0])
+        except RuntimeError as e:
+            assert "ran out of polls" in str(e)
+            raised += 1
+    assert raised > 0
+    model.chain_spin_limit = 1 << 22
+    out = runner.execute(_sched([seq], [1]), [0])
+    assert torch.isfinite(out).all() and model.chain_error() == 0

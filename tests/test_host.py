@@ -321,3 +321,21 @@ def test_decode_runner_context_guard():
         DecodeRunner(model, cache, torch.tensor([1]), torch.tensor([65]), bt[:1])
     short_rope = SimpleNamespace(embed=torch.zeros(4, 8), rope_cos=torch.zeros(62, 16))
     assert DecodeRunner(short_rope, cache, torch.tensor([1]), torch.tensor([60]), bt[:1]).steps_left() == 3
+
+
+def test_model_runner_rejects_blocks_past_the_cache():
+    """A block table naming a block past the cache (or a negative one) raises on the host, as
+    the reference's index_copy_ write does; blocks past the context are not checked."""
+    from llmserve.model_runner import ModelRunner
+
+    cfg = SimpleNamespace(num_hidden_layers=1, num_key_value_heads=2, head_dim=16)
+    r = ModelRunner.__new__(ModelRunner)
+    r.cache = KVCache(cfg, 8, 16, kv_dtype="int8")  # blocks 0..7
+    r.block_size = 16
+    r._check_tables([[0, 7], [3]], [32, 5])
+    r._check_tables([[0, 99]], [16])  # block 99 lies past the context: unused
+    r._check_tables([[]], [0])
+    with pytest.raises(IndexError, match="out of bounds"):
+        r._check_tables([[0, 8]], [17])
+    with pytest.raises(IndexError, match="out of bounds"):
+        r._check_tables([[1], [-1]], [3, 3])
