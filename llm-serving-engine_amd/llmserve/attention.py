@@ -190,7 +190,7 @@ class _BatchPlan:
 
 @functools.cache
 def _ops_namespace():
-    from llmserve.kernels import load_paged_attention
+    from .kernels import load_paged_attention
 
     return load_paged_attention()
 
@@ -292,7 +292,7 @@ class QuantizedKV:
 def _quant_ops(x: torch.Tensor):
     if not x.is_cuda:
         return None
-    from llmserve.kernels import load_quant
+    from .kernels import load_quant
 
     return load_quant()
 
@@ -336,7 +336,7 @@ def calibrate_k_smoothing(model, ids: list[int], alpha: float = 1.0) -> list[tor
     ``model`` has the reference's calling convention ``model(ids, positions, kv_caches, meta)``
     and a ``cfg``; the prefill runs over a throw-away cache in the model's dtype on its device
     (``QuantCausalLM`` of this package qualifies)."""
-    from llmserve.kv_cache import KVCache
+    from .kv_cache import KVCache
 
     dev, dtype = _model_placement(model)
     bs = 16

@@ -28,8 +28,17 @@ Functions, with the reference's names and signatures where the reference has the
   (fused_ops.cpp:129-137) and the decode-step kernels of this package (embedding + norm, the
   fused post-qkv KV write, greedy selection, the activation-fragment producers and consumers).
 
-``paged_attention_decode_v1`` and ``set_simd`` select CPU code paths of the reference and have
-no counterpart.
+The reference's attention module also calls ``paged_attention_decode_v1``, ``set_simd`` and
+``simd_available`` on the attention namespace (paged_attention.cpp:386-399) and imports
+``decode_kernel`` and ``paged_attention_op`` from this module (attention.py:260-289); they are
+provided with the same meaning: v1 is the fp32 decode as one context partition per sequence
+(the reference's previous kernel, one work item per sequence and kv head), and there is no
+CPU SIMD branch to switch (``simd_available()`` is False, ``set_simd`` accepts and ignores its
+flag: the GPU kernel is the only code path).
+
+Intra-package imports are relative, so the package also loads under another name (the
+reference's process keeps its own ``llmserve``; its loaders import this one by path as
+``llmserve_mi355x``).
 """
 
 from __future__ import annotations
@@ -38,21 +47,46 @@ import functools
 import logging
 from types import SimpleNamespace
 
-from llmserve._native import NativeLibraryMissing, ops
+import os
 
-__all__ = ["NativeLibraryMissing", "load_fused_ops", "load_int8_gemv", "load_paged_attention",
-           "load_quant", "native_available"]
+import torch
+
+from .._native import NativeLibraryMissing, ops
+
+__all__ = ["NativeLibraryMissing", "decode_kernel", "load_fused_ops", "load_int8_gemv",
+           "load_paged_attention", "load_quant", "native_available", "paged_attention_op"]
 
 log = logging.getLogger(__name__)
 
 
-def _namespace(what: str, names: tuple[str, ...]) -> SimpleNamespace | None:
+def _namespace(what: str, names: tuple[str, ...], **extra) -> SimpleNamespace | None:
     try:
         o = ops()
     except (NativeLibraryMissing, OSError, RuntimeError) as e:
         log.warning("%s unavailable, using the PyTorch fallback: %s", what, e)
         return None
-    return SimpleNamespace(**{n: getattr(o, n) for n in names})
+    return SimpleNamespace(**{n: getattr(o, n) for n in names}, **extra)
+
+
+def _decode_v1(o):
+    def paged_attention_decode_v1(q, k_cache, v_cache, block_tables, context_lens, block_size,
+                                  scale):
+        """The fp32 decode with one context partition per sequence (paged_attention.cpp's v1
+        entry: no split-context merge)."""
+        width = max(1, int(block_tables.shape[1]) * int(block_size))
+        return o.paged_attention_decode(q, k_cache, v_cache, block_tables, context_lens,
+                                        block_size, scale, width)
+
+    return paged_attention_decode_v1
+
+
+def _set_simd(on: bool) -> None:
+    """The reference's switch of its AVX-512 branch; the GPU kernel has one code path."""
+    bool(on)
+
+
+def _simd_available() -> bool:
+    return False
 
 
 def native_available() -> bool:
@@ -71,9 +105,47 @@ def load_int8_gemv() -> SimpleNamespace | None:
 @functools.cache
 def load_paged_attention() -> SimpleNamespace | None:
     """Paged attention over int8 and fp32 KV caches (HIP, gfx950), or None."""
+    try:
+        v1 = _decode_v1(ops())
+    except (NativeLibraryMissing, OSError, RuntimeError):
+        v1 = None
     return _namespace("paged attention kernels", (
         "paged_attention_decode_int8", "paged_attention_decode_int8_xfrag",
-        "paged_attention_decode", "paged_attention_rows", "attention_metadata"))
+        "paged_attention_decode", "paged_attention_rows", "attention_metadata"),
+        paged_attention_decode_v1=v1, set_simd=_set_simd, simd_available=_simd_available)
+
+
+def decode_kernel():
+    """The fp32 decode entry (reference kernels/__init__.py:75-81): ``paged_attention_decode``,
+    or ``paged_attention_decode_v1`` when ``LLMSERVE_ATTN_KERNEL=v1``."""
+    m = load_paged_attention()
+    if os.environ.get("LLMSERVE_ATTN_KERNEL") == "v1":
+        return m.paged_attention_decode_v1
+    return m.paged_attention_decode
+
+
+@functools.cache
+def paged_attention_op():
+    """``torch.ops.llmserve.paged_attention_decode`` (reference kernels/__init__.py:84-111): the
+    fp32 decode as a custom op with a fake (shape-only) kernel, so ``torch.compile`` traces
+    around it. When the reference's own module registered the op already in this process,
+    that registration is returned."""
+    try:
+        @torch.library.custom_op("llmserve::paged_attention_decode", mutates_args=())
+        def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor,
+                                   v_cache: torch.Tensor, block_tables: torch.Tensor,
+                                   context_lens: torch.Tensor, block_size: int,
+                                   scale: float) -> torch.Tensor:
+            return decode_kernel()(q.contiguous(), k_cache, v_cache, block_tables, context_lens,
+                                   block_size, scale)
+    except RuntimeError:  # already defined by the reference's kernels module
+        return torch.ops.llmserve.paged_attention_decode
+
+    @paged_attention_decode.register_fake
+    def _(q, k_cache, v_cache, block_tables, context_lens, block_size, scale):
+        return torch.empty_like(q)
+
+    return paged_attention_decode
 
 
 @functools.cache

@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from llmserve.attention import QuantizedKV
+from .attention import QuantizedKV
 
 KV_DTYPES = ("auto", "int8")
 

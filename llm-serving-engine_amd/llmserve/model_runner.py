@@ -22,10 +22,10 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from llmserve.attention import AttentionMetadata, QuantizedKV, _model_placement, resolve_backend
-from llmserve.kernels import load_fused_ops
-from llmserve.kv_cache import KVCache
-from llmserve.transformer import QuantCausalLM
+from .attention import AttentionMetadata, QuantizedKV, _model_placement, resolve_backend
+from .kernels import load_fused_ops
+from .kv_cache import KVCache
+from .transformer import QuantCausalLM
 
 
 class ModelRunner:

@@ -22,7 +22,7 @@ from collections import defaultdict
 import torch
 from torch import nn
 
-from llmserve.kernels import load_int8_gemv, load_quant
+from .kernels import load_int8_gemv, load_quant
 
 QUANT_METHODS = ("int8", "int4", "int4-awq")
 

@@ -207,7 +207,7 @@ def _csr(lists: list[list[int]], dev) -> tuple[torch.Tensor, torch.Tensor]:
 
 def _sample_device(logits: torch.Tensor, rows: list[SampleRow], capi) -> torch.Tensor:
     """One llmserve_sample launch over the batch (penalties and masks written in place)."""
-    from llmserve._native import check
+    from ._native import check
 
     B, V = logits.shape
     dev = logits.device
@@ -265,11 +265,11 @@ def _device_capi(logits: torch.Tensor):
     """The C ABI when the batch can run on the GPU kernel (None: the torch path)."""
     if not logits.is_cuda or logits.dtype != torch.float32 or logits.dim() != 2:
         return None
-    from llmserve.kernels import native_available
+    from .kernels import native_available
 
     if not native_available():
         return None
-    from llmserve._native import capi
+    from ._native import capi
 
     return capi()
 

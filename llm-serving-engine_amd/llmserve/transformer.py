@@ -30,9 +30,9 @@ from torch import nn
 
 import ctypes
 
-from llmserve.attention import paged_attention
-from llmserve.kernels import load_fused_ops, load_paged_attention
-from llmserve.quant import Int4Linear, _search_awq_scale
+from .attention import paged_attention
+from .kernels import load_fused_ops, load_paged_attention
+from .quant import Int4Linear, _search_awq_scale
 
 
 def _fused_ops():
@@ -214,7 +214,7 @@ class QuantCausalLM(nn.Module):
         this model: steps on one model must not overlap)."""
         ws = getattr(self, "_chain_ws", None)
         if ws is None:
-            from llmserve._native import capi
+            from ._native import capi
 
             n = capi().llmserve_decode_chain_workspace_bytes(self.cfg.hidden_size,
                                                              self.cfg.intermediate_size)
@@ -224,7 +224,7 @@ class QuantCausalLM(nn.Module):
 
     def chain_error(self) -> int:
         """Nonzero when a chain hand-off wait ran out of polls (synchronizes)."""
-        from llmserve._native import capi, check
+        from ._native import capi, check
 
         err = ctypes.c_int(0)
         check(capi().llmserve_decode_chain_error(ctypes.c_void_p(self.chain_workspace().data_ptr()),
@@ -250,7 +250,7 @@ class QuantCausalLM(nn.Module):
         """One llmserve_decode_chain launch: layer ``layer``'s attention (of ``q_in`` over
         ``attn_caches``) and MLP half (None: embedding mode) and ``nxt``'s qkv part (None: the
         last layer, writing ``h_out``). ``q_out`` must not be ``q_in``."""
-        from llmserve._native import capi, check
+        from ._native import capi, check
 
         cfg = self.cfg
 

@@ -191,3 +191,29 @@ def test_paged_attention_module_native_vs_torch(gpu, kv_dtype):
         assert torch.equal(v0.data, v1.data) and torch.equal(v0.scale, v1.scale)
     else:
         assert torch.equal(k0, k1) and torch.equal(v0, v1)
+
+
+@pytest.mark.parametrize("simd", [True, False])
+@pytest.mark.parametrize("partition", [0, 4, 8, 10_000])
+def test_loader_v1_entry_and_simd_switch(gpu, simd, partition):
+    """The reference's own v1-vs-v2 check (tests/test_attention.py:84-101) through this
+    build's loader: paged_attention_decode at every partition size, with set_simd either way,
+    equals paged_attention_decode_v1 (one partition per sequence) at 1e-5, and both equal the
+    float64 attention."""
+    from llmserve.kernels import load_paged_attention
+
+    m = load_paged_attention()
+    g = dict(np.load(GOLDEN / "attention_f32_golden.npz"))
+    bs, sc = (float(x) for x in g["f32_small_meta"])
+    bs = int(bs)
+    arrays = [g[f"f32_small_{k}"] for k in ("q", "k", "v", "bt", "cl")]
+    q, k, v, bt, cl = (torch.from_numpy(a).to(gpu) for a in arrays)
+    ref = m.paged_attention_decode_v1(q, k, v, bt, cl, bs, sc)
+    m.set_simd(simd)
+    try:
+        out = m.paged_attention_decode(q, k, v, bt, cl, bs, sc, partition)
+    finally:
+        m.set_simd(True)
+    torch.testing.assert_close(out, ref, atol=1e-5, rtol=1e-5)
+    ref64 = mr.paged_decode_f64(*arrays, bs, sc)
+    cu.assert_rel_close(ref, ref64, TOL, "v1 vs f64")

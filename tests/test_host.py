@@ -339,3 +339,94 @@ def test_model_runner_rejects_blocks_past_the_cache():
         r._check_tables([[0, 8]], [17])
     with pytest.raises(IndexError, match="out of bounds"):
         r._check_tables([[1], [-1]], [3, 3])
+
+
+_STUB_KERNELS = '''"""Stub laid out as the reference's src/llmserve/kernels/__init__.py (its imports, logger,
+csrc path and functools-cached JIT loaders that return a module or None)."""
+
+from __future__ import annotations
+
+import functools
+import logging
+import os
+from pathlib import Path
+
+import torch
+
+log = logging.getLogger(__name__)
+_CSRC = Path(__file__).parent / "csrc"
+
+
+@functools.cache
+def load_paged_attention():
+    """Return the compiled extension module, or None if it cannot be built."""
+    return "reference-cpu:paged_attention"
+
+
+@functools.cache
+def load_fused_ops():
+    """Fused ops, or None."""
+    return "reference-cpu:fused_ops"
+
+
+@functools.cache
+def load_int8_gemv():
+    """Weight-only int8 small-batch matmul, or None."""
+    return "reference-cpu:int8_gemv"
+'''
+
+_BINDING_CHECK = r'''
+import os, sys
+import torch
+torch.cuda.is_available = lambda: {cuda}  # a ROCm host, as the binding expects (or not)
+sys.path.insert(0, {stub!r})
+import llmserve.kernels as k
+assert os.path.dirname(k.__file__).startswith({stub!r}), k.__file__  # the reference's package
+gemv, attn, fused = k.load_int8_gemv(), k.load_paged_attention(), k.load_fused_ops()
+if {expect_build}:
+    assert sys.modules["llmserve_mi355x.kernels"].__file__.startswith({pkg!r})
+    assert "llmserve_hip.int8_linear" in repr(gemv.int8_linear), gemv
+    assert "llmserve_hip.int4_linear" in repr(gemv.int4_linear), gemv
+    assert "llmserve_hip.paged_attention_decode_int8" in repr(attn.paged_attention_decode_int8)
+    assert attn.simd_available() is False and attn.set_simd(True) is None
+    assert callable(attn.paged_attention_decode_v1)
+    assert "llmserve_hip.rope_qk_" in repr(fused.rope_qk_)
+else:
+    assert (gemv, attn, fused) == ("reference-cpu:int8_gemv", "reference-cpu:paged_attention",
+                                   "reference-cpu:fused_ops"), (gemv, attn, fused)
+assert k.load_int8_gemv() is gemv  # cached, as the reference's loaders are
+print("binding ok")
+'''
+
+
+@pytest.mark.parametrize("case", ["rocm", "no-device", "no-package"])
+def test_reference_binding_from_integration_doc(tmp_path, case):
+    """INTEGRATION.md's binding block, appended verbatim to a stub package named ``llmserve``
+    (laid out as the reference's kernels/__init__.py, kernels/__init__.py:19-72), loads this
+    build under its alias and returns its namespaces on a ROCm host with no recursion; with no
+    device, or no package at the configured path, the reference's own loaders answer."""
+    import re
+    import subprocess
+    import sys
+
+    from conftest import REPO
+    from llmserve.kernels import native_available
+
+    doc = (REPO / "INTEGRATION.md").read_text()
+    blocks = [b for b in re.findall(r"```python\n(.*?)```", doc, re.S) if "def _mi355x" in b]
+    assert len(blocks) == 1
+    pkg = tmp_path / "llmserve"
+    (pkg / "kernels").mkdir(parents=True)
+    (pkg / "__init__.py").write_text('"""Stub of the reference package."""\n')
+    (pkg / "kernels" / "__init__.py").write_text(_STUB_KERNELS + "\n\n" + blocks[0])
+    ours = REPO / "llm-serving-engine_amd" / "llmserve"
+    env = dict(__import__("os").environ)
+    env["LLMSERVE_MI355X"] = str(ours if case != "no-package" else tmp_path / "absent")
+    env["PYTHONPATH"] = ""
+    expect = case == "rocm" and native_available()
+    code = _BINDING_CHECK.format(cuda=case != "no-device", stub=str(tmp_path), pkg=str(ours),
+                                 expect_build=expect)
+    r = subprocess.run([sys.executable, "-c", code], env=env, cwd=tmp_path,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "binding ok" in r.stdout, r.stderr[-3000:]
+    assert "RecursionError" not in r.stderr
