@@ -12,20 +12,25 @@ input channels x20; each layer shape's AWQ scale comes from the reference's grid
 (quant.py:154-170) on 512 such rows and that shape's first weight.
 
 `value` = algorithmic bytes per step (packed weights + group scales/zeros + inv_act_scale +
-x + y) x steps / wall time of the K timed steps. `roofline` is for the dominant kernel (the
-gate_up GEMV): its algorithmic bytes per launch over its average launch duration, measured
-here with HIP events around graph replays of back-to-back launches (distinct weights) on the
-stream the kernel runs on — the per-dispatch interval a kernel-trace profiler reports.
-The same interval for a one-element fill kernel (`empty_kernel_us`) is the floor of such a
-measurement; `roofline.rocprof` holds what rocprofv3's kernel trace reports for both
-(profiles/launch_calibration.md), so the two clocks can be compared.
+x + y) x steps / wall time of the K timed steps. `roofline` is for the dominant kernel: of the
+four GEMVs of a step (each launched 28 times) the one with the longest duration on the
+profiler's clock, i.e. the median End - Start of its dispatches in the committed rocprofv3
+kernel trace of `bench.py --only gemv` (profiles/gemv_kernel_trace.md); `frac` is its
+algorithmic bytes over that median, and every other fraction that names a profile
+(`extra.c1_int8_gemv`, `extra.c4_int8kv_paged_decode`: decode + merge) is computed the same
+way from the file's rows. Measured live in this run and carried beside each of them:
+`pipelined_*`, the per-dispatch interval of back-to-back launches over distinct inputs in a
+HIP graph replay (HIP events on the kernels' stream), where one dispatch's ramp overlaps the
+previous one's drain, and the same interval for a one-element fill kernel
+(`empty_kernel_pipelined_us`, the floor of that measurement).
 `cpu_baseline` times the reference's own CPU kernels (oracle/_ref, built from the reference
 sources) — or the oracle's C restatement where that build is absent — on the host cores, on
 the same quantized weights: config 2 on one thread per physical core of the GPU's NUMA node;
 `extra.cpu` adds configs 1 and 4 and a 4-thread run of all three, with the CPU model and its
 AVX-512 flag (about 25 s in all).
 Extra fields report M = 4 / 16 steps (the kernel Int4Linear runs at that batch: the GEMV up
-to 4 rows, the matrix-core kernel on the packed weight above) and configs 1 (int8 GEMV), 3
+to 4 rows, the matrix-core kernel on the packed weight above, one launch per linear up to 16
+rows), rows at the reference's own published benchmark shapes (`extra.reference_shapes`) and configs 1 (int8 GEMV), 3
 (prefill int8 GEMM on the bf16 matrix cores, x conversion included), 4 (int8-KV decode) and
 5 (the full greedy decode step of a random-init int4-AWQ Qwen3-0.6B at batch 64 over the int8
 KV cache, one HIP graph replay per step: tokens/s, with the fp32 and the int4 LM head, and
@@ -192,6 +197,41 @@ def kernel_avg_us(torch, launch, n: int, reps: int = 20) -> float:
     return e0.elapsed_time(e1) * 1e3 / (n * reps)
 
 
+# rocprofv3 rows (kernel, workgroups) of the kernels the BENCH line's fractions name, in the
+# committed kernel-trace summaries: the GEMVs Int4Linear runs at M = 1 for the four shapes and
+# config 1's int8 GEMV (profiles/gemv_kernel_trace.md, `bench.py --only gemv`), config 4's
+# decode and merge (profiles/attention_kernel_trace.md, `bench.py --only attention`).
+PROFILE_ROWS = {
+    "qkv": ("gemv_kernel_trace.md", "gemv_lat<1, 32, 1, 4, true>", "512 x 1"),
+    "o": ("gemv_kernel_trace.md", "gemv_lat<1, 64, 1, 4, true>", "256 x 1"),
+    "gate_up": ("gemv_kernel_trace.md", "gemv_lat<1, 32, 1, 4, true>", "768 x 1"),
+    "down": ("gemv_kernel_trace.md", "gemv_lat<1, 32, 1, 6, true, 3>", "256 x 1"),
+    "c1": ("gemv_kernel_trace.md", "gemv_lat<1, 64, 1, 4, false>", "1536 x 1"),
+    "c4_decode": ("attention_kernel_trace.md", "paged_decode_kernel<signed char, 128, 2, true, true>",
+                  "256 x 1"),
+    "c4_merge": ("attention_kernel_trace.md", "paged_decode_merge_kernel<128>", "128 x 1"),
+}
+
+
+def read_profile(key: str) -> dict | None:
+    """avg / median us of a kernel from a committed kernel-trace summary: the markdown row
+    `| `kernel` | workgroups (x, y) x threads | dispatches | avg us | median us | min us |`."""
+    fname, kernel, wgs = PROFILE_ROWS[key]
+    p = REPO / "profiles" / fname
+    if not p.is_file():
+        return None
+    for line in p.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == f"`{kernel}`" and cells[1].startswith(wgs + ","):
+            try:
+                return {"file": f"profiles/{fname}", "kernel": kernel, "workgroups": wgs,
+                        "dispatches": int(cells[2]), "avg_us": float(cells[3]),
+                        "median_us": float(cells[4])}
+            except ValueError:
+                return None
+    return None
+
+
 def read_traffic(kernel: str) -> dict | None:
     """HBM bytes per launch from the committed PMC summary (profiles/roofline_traffic.md):
     a markdown table row `| kernel | fetch_bytes | write_bytes | ... |`."""
@@ -248,24 +288,6 @@ def host_info(torch) -> dict:
         gpu_node = None
     info["gpu_numa_node"] = gpu_node
     return info
-
-
-def read_launch_calibration() -> dict | None:
-    """The rocprofv3 kernel-trace figures of the same two measurements (the gate_up GEMV and
-    the fill kernel, each 224 launches per graph replay) from profiles/launch_calibration.md:
-    table rows `| name | dispatches | avg us | median us |`."""
-    p = REPO / "profiles" / "launch_calibration.md"
-    if not p.is_file():
-        return None
-    out = {}
-    for line in p.read_text().splitlines():
-        cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) >= 4 and cells[0] in ("gate_up GEMV", "fill kernel"):
-            try:
-                out[cells[0]] = {"avg_us": float(cells[2]), "median_us": float(cells[3])}
-            except ValueError:
-                pass
-    return out or None
 
 
 def cpu_baseline(torch, model, calib, dev, budget_s: float = 4.0) -> tuple[dict, dict]:
@@ -397,8 +419,9 @@ def extra_configs(torch, dev) -> dict:
     gemv = load_int8_gemv()
     us = kernel_avg_us(torch, lambda i: gemv.int8_linear(x, *qs[i % len(qs)]), 200)
     b = int8_bytes(N, K, 1)
-    out["c1_int8_gemv"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
-                           "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}
+    out["c1_int8_gemv"] = with_profile(
+        {"pipelined_us": round(us, 2), "pipelined_GBps": round(b / us / 1e3, 1),
+         "pipelined_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}, b, ["c1"])
     del qs
     # config 3: prefill-sized int8 GEMMs (M = 2048) on the bf16 matrix cores
     c3 = {}
@@ -421,9 +444,90 @@ def extra_configs(torch, dev) -> dict:
         pa.paged_attention_decode_int8(q, kq, vq, ks, vs, bt, cl, bs, D ** -0.5, 0, qm)
 
     us = kernel_avg_us(torch, launch, 40)
-    out["c4_int8kv_paged_decode"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
-                                     "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}
+    out["c4_int8kv_paged_decode"] = with_profile(
+        {"pipelined_us": round(us, 2), "pipelined_GBps": round(b / us / 1e3, 1),
+         "pipelined_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": b}, b,
+        ["c4_decode", "c4_merge"])
     del copies
+    out["reference_shapes"] = reference_shapes(torch, dev)
+    return out
+
+
+def with_profile(row: dict, nbytes: int, keys: list[str]) -> dict:
+    """Adds the committed kernel-trace medians of `keys` (the kernels of one call, summed:
+    decode + merge) and `frac` = bytes / that sum; without the profile rows `frac` is the
+    in-process per-dispatch interval's."""
+    profs = [read_profile(k) for k in keys]
+    if all(p is not None for p in profs):
+        us = sum(p["median_us"] for p in profs)
+        row.update({"profile_us": round(us, 3), "profile": profs,
+                    "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                    "GBps": round(nbytes / us / 1e3, 1)})
+    else:
+        row.update({"frac": row["pipelined_frac"], "GBps": row["pipelined_GBps"],
+                    "profile": None})
+    return row
+
+
+def reference_shapes(torch, dev) -> dict:
+    """The reference's own published CPU benchmark shapes (4-vCPU Xeon, its results files),
+    run here on the same kernels, beside its figures: the int8-KV decode at Qwen3-0.6B
+    attention geometry, block 16, batch 16 x ctx 1024 / 4096 and batch 1 x ctx 256 / 1024 /
+    4096 (results/microbench/attention.json, docs/report.md:277-278: 2941 / 14555 and 40 / 264
+    / 1082 us), and the int4 group-64 gate_up GEMV 1024 -> 6144 at M = 1 / 4 / 16
+    (results/m8/kernels.md:8-10: 0.51 / 2.96 / 8.12 ms). GPU times are per-dispatch intervals
+    of back-to-back launches over rotating copies (HIP events around graph replays)."""
+    from llmserve.kernels import load_int8_gemv, load_paged_attention, load_quant
+
+    out = {"attention_int8kv": {}, "int4_g64_gate_up": {}}
+    pa = load_paged_attention()
+    Hq, Hk, D, bs = 16, 8, 128, 16
+    g = torch.Generator(device=dev).manual_seed(77)
+    ref_attn = {(16, 1024): 2941.0, (16, 4096): 14555.0, (1, 256): 40.0, (1, 1024): 264.0,
+                (1, 4096): 1082.0}
+    for (B, ctx), ref_us in ref_attn.items():
+        nblk = -(-ctx // bs)
+        slots = B * nblk * bs
+        copies = []
+        for _ in range(max(2, min(16, (1 << 30) // (2 * slots * Hk * (D + 4))))):
+            perm = torch.randperm(B * nblk, generator=g, device=dev)
+            kq = torch.randint(-127, 128, (slots, Hk, D), dtype=torch.int8, device=dev, generator=g)
+            vq = torch.randint(-127, 128, (slots, Hk, D), dtype=torch.int8, device=dev, generator=g)
+            ks = torch.rand(slots, Hk, device=dev, generator=g) * 0.05
+            vs = torch.rand(slots, Hk, device=dev, generator=g) * 0.05
+            copies.append((kq, vq, ks, vs, perm.view(B, nblk).contiguous()))
+        q = torch.randn(B, Hq, D, device=dev, generator=g)
+        cl = torch.full((B,), ctx, dtype=torch.long, device=dev)
+
+        def launch(i, copies=copies, q=q, cl=cl):
+            kq, vq, ks, vs, bt = copies[i % len(copies)]
+            pa.paged_attention_decode_int8(q, kq, vq, ks, vs, bt, cl, bs, D ** -0.5, 0, None)
+
+        us = kernel_avg_us(torch, launch, 4 * len(copies))
+        nbytes = B * ctx * Hk * (2 * D + 8)
+        out["attention_int8kv"][f"B={B} ctx={ctx}"] = {
+            "us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "reference_cpu_us": ref_us,
+            "speedup": round(ref_us / us, 1)}
+        del copies
+    gemv = load_int8_gemv()
+    N, K, G = 6144, 1024, 64
+    lins = [load_quant().int4_quantize(torch.randn(N, K, device=dev, generator=g) * 0.02, G,
+                                       torch.rand(K, device=dev, generator=g) + 0.5)
+            for _ in range(64)]  # 64 x 3.5 MB
+    for M, ref_ms in ((1, 0.51), (4, 2.96), (16, 8.12)):
+        x = torch.randn(M, K, device=dev, generator=g)
+
+        def launch(i, x=x):
+            nib, gs, gz, inv = lins[i % len(lins)]
+            gemv.int4_linear(x, nib, gs, gz, G, inv)
+
+        us = kernel_avg_us(torch, launch, 128)
+        nbytes = N * K // 2 + 8 * N * (K // G) + 4 * K + 4 * M * K + 4 * M * N
+        out["int4_g64_gate_up"][f"M={M}"] = {
+            "us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "reference_cpu_us": ref_ms * 1e3,
+            "speedup": round(ref_ms * 1e3 / us, 1)}
     return out
 
 
@@ -708,17 +812,24 @@ def profile_only(torch, dev, what: str) -> int:
     """64 launches of one kernel, for rocprofv3 counter runs (no timing output)."""
     from llmserve.kernels import load_int8_gemv, load_paged_attention, load_quant
 
-    if what == "gemv":  # the dominant kernel: int4 g128 GEMV at the gate_up shape, M = 1
-        N, K = SHAPES["gate_up"]
+    if what == "gemv":  # the four int4 g128 GEMV shapes at M = 1, then config 1's int8 GEMV
         g = torch.Generator(device=dev).manual_seed(3)
-        lins = [load_quant().int4_quantize(torch.randn(N, K, device=dev, generator=g) * 0.02, GROUP,
-                                           torch.rand(K, device=dev, generator=g) + 0.5)
-                for _ in range(64)]
-        x = torch.randn(1, K, device=dev, generator=g)
         gemv = load_int8_gemv()
+        for name, (N, K) in SHAPES.items():  # 64 distinct weights each (~0.6 GB in all)
+            lins = [load_quant().int4_quantize(torch.randn(N, K, device=dev, generator=g) * 0.02,
+                                               GROUP, torch.rand(K, device=dev, generator=g) + 0.5)
+                    for _ in range(64)]
+            x = torch.randn(1, K, device=dev, generator=g)
+            for i in range(64):
+                nib, gs, gz, inv = lins[i]
+                gemv.int4_linear(x, nib, gs, gz, GROUP, inv)
+            del lins
+        N, K = 6144, 1024
+        qs = [load_quant().int8_quantize(torch.randn(N, K, device=dev, generator=g) * 0.02)
+              for _ in range(64)]
+        x = torch.randn(1, K, device=dev, generator=g)
         for i in range(64):
-            nib, gs, gz, inv = lins[i]
-            gemv.int4_linear(x, nib, gs, gz, GROUP, inv)
+            gemv.int8_linear(x, *qs[i])
     elif what == "prefill":  # config 3 gate_up: M = 2048, 2048 -> 16384
         g = torch.Generator(device=dev).manual_seed(4)
         x = torch.randn(2048, 2048, device=dev, generator=g)
@@ -816,7 +927,7 @@ def main() -> int:
         step_bytes = LAYERS * sum(int4_bytes(N, K, M) for N, K in SHAPES.values())
         gbs = step_bytes * steps / wall / 1e9
         by_rows[str(M)] = {"kernel": ("gemv" if M <= GEMV_ROWS else
-                                      "matrix-core on packed weight (split pass included)"),
+                                      "matrix-core on packed weight, fragments built in the kernel (one launch)"),
                            "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                            "ms_per_step": round(wall / steps * 1e3, 4),
                            "gpu_ms_per_step": round(gpu / steps * 1e3, 4), "bytes": step_bytes}
@@ -832,31 +943,56 @@ def main() -> int:
         log(f"[bench] M={M}: {by_rows[str(M)]}")
     del packed
 
-    # dominant kernel: the gate_up GEMV at M = 1
-    N, K = SHAPES["gate_up"]
+    # dominant kernel: of the four GEMV shapes at M = 1 (each launched 28 times per step), the
+    # one with the most time per step on the profiler's clock (the committed kernel trace of
+    # `bench.py --only gemv`: each dispatch's own start-to-end interval); `frac` is its
+    # algorithmic bytes over that median. Measured live here, beside it: the per-dispatch
+    # interval of 224 back-to-back launches in a graph replay (HIP events on the kernels'
+    # stream), where each dispatch's ramp overlaps the previous one's drain.
     xs = make_inputs(torch, dev, calib, 1)
     order = [(c, l) for l in range(LAYERS) for c in range(COPIES)]
 
-    def gate_up(i):
-        c, l = order[i % len(order)]
-        nib, gs, gz, inv = model[c][l]["gate_up"]
-        gemv.int4_linear(xs["gate_up"], nib, gs, gz, GROUP, inv)
+    def shape_launch(name):
+        def launch(i):
+            c, l = order[i % len(order)]
+            nib, gs, gz, inv = model[c][l][name]
+            gemv.int4_linear(xs[name], nib, gs, gz, GROUP, inv)
+        return launch
 
-    avg_us = kernel_avg_us(torch, gate_up, 224)
-    # the per-dispatch floor of this measurement: a one-element fill kernel timed the same way
+    per_shape = {}
+    for name, (N, K) in SHAPES.items():
+        kb = int4_bytes(N, K, 1)
+        live = kernel_avg_us(torch, shape_launch(name), 224)
+        prof = read_profile(name)
+        per_shape[name] = {"N": N, "K": K, "bytes": kb, "pipelined_us": round(live, 3),
+                           "pipelined_frac": round(kb / live / 1e3 / HBM_PEAK_GBS, 4)}
+        if prof is not None:
+            per_shape[name].update({"profile_median_us": prof["median_us"],
+                                    "profile_frac": round(kb / prof["median_us"] / 1e3 / HBM_PEAK_GBS, 4)})
+    have_prof = all("profile_median_us" in v for v in per_shape.values())
+    clock = "profile_median_us" if have_prof else "pipelined_us"
+    dom = max(per_shape, key=lambda n: per_shape[n][clock])
+    N, K = SHAPES[dom]
+    kb = per_shape[dom]["bytes"]
+    dur = per_shape[dom][clock]
+    # the per-dispatch floor of the pipelined measurement: a one-element fill kernel
     tiny = [torch.zeros(1, device=dev) for _ in range(8)]
     empty_us = kernel_avg_us(torch, lambda i: tiny[i % 8].fill_(float(i)), 224)
-    kb = int4_bytes(N, K, 1)
-    achieved = kb / avg_us / 1e3
-    traffic = read_traffic("gemv_lat int4 gate_up M=1")
-    prof = read_launch_calibration()
+    achieved = kb / dur / 1e3
+    traffic = read_traffic(f"gemv_lat int4 {dom} M=1")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None if traffic is None else int(traffic["fetch"] + traffic["write"]),
-                "kernel": "gemv_lat int4 (gate_up 1024->6144, M=1)",
-                "bytes_per_launch": kb, "avg_launch_us": round(avg_us, 3),
-                "empty_kernel_us": round(empty_us, 3),
-                "rocprof": prof}
+                "kernel": f"gemv_lat int4 ({dom} {K}->{N}, M=1)",
+                "duration_us": dur,
+                "clock": ("rocprofv3 kernel trace median (profiles/gemv_kernel_trace.md, "
+                          "`bench.py --only gemv`)" if have_prof else
+                          "in-process per-dispatch interval (no committed profile found)"),
+                "bytes_per_launch": kb,
+                "pipelined_interval_us": per_shape[dom]["pipelined_us"],
+                "pipelined_GBps": round(kb / per_shape[dom]["pipelined_us"] / 1e3, 1),
+                "empty_kernel_pipelined_us": round(empty_us, 3),
+                "per_shape": per_shape}
     log(f"[bench] roofline: {roofline}")
 
     extra = {} if args.no_extra else extra_configs(torch, dev)

@@ -538,6 +538,163 @@ void int4_gemm_wide(Int4GemmArgs a, int mtiles, int groups) {
   }
 }
 
+// One 16-row tile of activations (M <= 16: a decode batch through Int4Linear.forward) in ONE
+// launch: each wavefront builds its K block's three-piece fragments and block sums from the
+// fp32 x rows itself, in registers, instead of reading those of a separate split pass. The
+// values are the split pass's bit for bit: x' = x * inv (rounded multiply), hi / mid / lo as
+// split3_bf16, and each row's block sum as the same pairwise tree (lane (fr, fc) holds the
+// channels 32 fc .. + 32 of row fr, i.e. the split pass's segments 4 fc .. 4 fc + 3: its
+// 8-channel trees and their first two butterfly levels are in-lane, the last two are lane
+// swaps 16 and 32 apart; the MFMA layout then wants the sums of rows 4 fc + r, fetched with
+// four lane shuffles). The products and their accumulation are int4_gemm_lat's.
+// Work: S wavefronts split the K blocks of NT 16-column tiles (one block per wavefront and
+// round); NT = 1 gives each workgroup one tile of a slab, so a narrow output (N = 1024:
+// 16 slabs) spreads over 64 workgroups instead of 16.
+struct Int4GemmXArgs {
+  const float* x;    // [M, K] fp32
+  const float* inv;  // [K] AWQ pre-scale (INV only)
+  const uint8_t* w;  // packed nibbles
+  const float* s;    // packed scales
+  float* y;          // [M, N]
+  int M, N, K, bpg;
+};
+
+template <int S, int NT, bool INV>
+__global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
+  extern __shared__ f32x4 red[];  // S > 1: [S][NT][64]
+  constexpr int kUnits = kNT / NT;  // workgroups per slab
+  const int lane = threadIdx.x % kWave, ks = threadIdx.x / kWave;
+  const int slab = blockIdx.x / kUnits, u0 = (blockIdx.x % kUnits) * NT;
+  const int n0 = slab * kCols + 16 * u0;
+  if (n0 >= a.N) return;  // whole workgroup: no barrier is reached
+  const int fr = lane % 16, fc = lane / 16;
+  const int nblk = a.K / kBlk;
+  const int slabs = (a.N + kCols - 1) / kCols;
+  const bool live = fr < a.M;
+  const float* xrow = a.x + static_cast<int64_t>(live ? fr : a.M - 1) * a.K + 32 * fc;
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int u = 0; u < NT; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int base = 0; base < nblk; base += S) {
+    const int b = min(base + ks, nblk - 1);  // clamped: loads stay unconditional
+    const int g = b / a.bpg;
+    u32x4 w[NT];
+    const uint8_t* wt = a.w + ((static_cast<int64_t>(slab) * nblk + b) * kNT + u0) * kPkTile + 16 * lane;
+#pragma unroll
+    for (int u = 0; u < NT; ++u)
+      w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wt + u * kPkTile));
+    const float* st = a.s + ((static_cast<int64_t>(g) * slabs + slab) * 16 + fr) * 8;
+    const f32x4 s4 = *reinterpret_cast<const f32x4*>(st);
+    const f32x4 z4 = *reinterpret_cast<const f32x4*>(st + 4);  // z - 8 s
+    f32x4 xv[8], iv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = *reinterpret_cast<const f32x4*>(xrow + b * kBlk + 4 * i);
+    if constexpr (INV) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        iv[i] = *reinterpret_cast<const f32x4*>(a.inv + b * kBlk + 32 * fc + 4 * i);
+    }
+    // every load above goes out before the arithmetic below
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 xh[4], xm[4], xl[4];
+    float tq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xe = xv[2 * q + e / 4][e % 4];
+        const float ve = INV ? __fmul_rn(xe, iv[2 * q + e / 4][e % 4]) : xe;
+        v[e] = live ? ve : 0.f;
+      }
+      tq[q] = lsh::tree_sum<8>(v);
+      bf16x8 hi, mid, lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        __bf16 h, md, l;
+        lsh::split3_bf16(v[e], h, md, l);
+        hi[e] = h;
+        mid[e] = md;
+        lo[e] = l;
+      }
+      xh[q] = __builtin_bit_cast(u32x4, hi);
+      xm[q] = __builtin_bit_cast(u32x4, mid);
+      xl[q] = __builtin_bit_cast(u32x4, lo);
+    }
+    float rs = (tq[0] + tq[1]) + (tq[2] + tq[3]);  // row fr: this lane's 32 channels
+    rs += __shfl_xor(rs, 16, kWave);               // + the neighbouring 32
+    rs += __shfl_xor(rs, 32, kWave);               // + the other 64: the block sum of row fr
+    f32x4 xs;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xs[r] = __shfl(rs, 4 * fc + r, kWave);  // rows 4 fc + r
+    const float on = base + ks < nblk ? 1.f : 0.f;
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bf16x8 bq = nibbles_bf16(w[u][q]);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xh[q]), bq, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xm[q]), bq, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xl[q]), bq, d, 0, 0, 0);
+      }
+      const float s1 = on * s4[u0 + u];
+      const float zz = on * z4[u0 + u];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[u][r] += __builtin_fmaf(s1, d[r], zz * xs[r]);  // as int4_gemm_lat
+    }
+  }
+
+  if constexpr (S > 1) {
+#pragma unroll
+    for (int u = 0; u < NT; ++u) red[(ks * NT + u) * kWave + lane] = acc[u];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < NT; ++u) {
+    const bool mine = S == 1 || (S <= NT ? u % S == ks : u == ks);
+    if (!mine) continue;
+    f32x4 v = acc[u];
+    if constexpr (S > 1) {
+      v = red[u * kWave + lane];
+#pragma unroll
+      for (int k = 1; k < S; ++k) v += red[(k * NT + u) * kWave + lane];
+    }
+    const int n = n0 + 16 * u + fr;
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * fc + r;
+      if (m < a.M) a.y[static_cast<int64_t>(m) * a.N + n] = v[r];
+    }
+  }
+}
+
+template <int S, int NT>
+void launch_x(const Int4GemmXArgs& a, int64_t slabs, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(slabs * (kNT / NT))), block(S * kWave);
+  const size_t lds = S > 1 ? static_cast<size_t>(S) * NT * kWave * sizeof(f32x4) : 0;
+  if (a.inv)
+    lsh::launch(int4_gemm_x<S, NT, true>, grid, block, lds, st, true, a);
+  else
+    lsh::launch(int4_gemm_x<S, NT, false>, grid, block, lds, st, true, a);
+}
+
+// S: wavefronts to cover the K blocks in one round (up to 16: K = 2048; K = 3072 takes two
+// rounds); NT: tiles per workgroup. More workgroups beat less redundant conversion: config 2
+// at 16 rows (the four Qwen3-0.6B shapes, 112 launches) 273 GB/s with one tile per
+// workgroup, 276 with two, 219 with a whole slab (four); 5 rows 324 / 307 / 221.
+void launch_x_tile(const Int4GemmXArgs& a, int64_t slabs, int nb, hipStream_t st) {
+  const int S = nb <= 4 ? 4 : (nb <= 8 ? 8 : 16);
+  const int NT = slabs * kNT <= 512 ? 1 : 2;
+#define LSH_X(s, nt) \
+  if (S == s && NT == nt) return launch_x<s, nt>(a, slabs, st);
+  LSH_X(4, 1) LSH_X(4, 2) LSH_X(4, 4) LSH_X(8, 1) LSH_X(8, 2) LSH_X(8, 4)
+  LSH_X(16, 1) LSH_X(16, 2) LSH_X(16, 4)
+#undef LSH_X
+}
+
 int64_t xsum_rows(int64_t M) { return (M + kRows - 1) / kRows * kRows; }
 
 template <int KB, int S>
@@ -730,6 +887,15 @@ extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv
   const int nb = static_cast<int>(K / kBlk);
   const int64_t mtiles = (M + kRows - 1) / kRows;
   const int mp = static_cast<int>(xsum_rows(M));
+  const uint8_t* wpk0 = static_cast<const uint8_t*>(packed);
+  if (mtiles == 1) {  // one row tile: fragments built inside the GEMM, one launch
+    Int4GemmXArgs xa{x, inv_act_scale, wpk0,
+                     reinterpret_cast<const float*>(wpk0 + (pk_weight_bytes(N, K) + 255) / 256 * 256),
+                     y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
+                     static_cast<int>(group_size / kBlk)};
+    launch_x_tile(xa, pk_slabs(N), nb, st);
+    return lsh::launch_status("int4_linear_gemm_packed");
+  }
   __bf16* xf = static_cast<__bf16*>(workspace);
   float* xsum = lsh::frag_sums(xf, mp, K);
   lsh::launch(x_split_frag_kernel, dim3(static_cast<unsigned>(mtiles * nb)), dim3(256), 0, st, false,

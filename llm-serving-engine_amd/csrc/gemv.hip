@@ -382,7 +382,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fast(GemvArgs a) {
 // Requires K <= kLatMaxK, K == nseg * LPR * CPL with nseg <= NSEG, blockDim.x == 64 * WPB.
 constexpr int kLatMaxK = 4096;
 
-template <int MT, int LPR, int NSEG, int WPB, bool INT4>
+// KS > 1: the row's K segments are split over KS wavefronts of the workgroup (wavefront
+// w takes segments (w % KS) * NSEG .. + NSEG of the rows of group w / KS), and their row sums
+// meet in LDS, added in wavefront order (deterministic): KS times the wavefronts, each with a
+// KS-th of the dependent chain (down_proj, K = 3072: three segments per lane otherwise).
+template <int MT, int LPR, int NSEG, int WPB, bool INT4, int KS = 1>
 __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
   constexpr int RPL = 1;
   extern __shared__ float4 xs4[];          // [MT][K] floats, slices rotated by chunk_pos
@@ -392,12 +396,15 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
   constexpr int SEGK = LPR * CPL;
   constexpr int CPC = CPL / 4;
   constexpr int BD = WPB * kWave;
-  constexpr int UMAX = kLatMaxK / 4 / BD;  // x chunks per thread per row, at most
+  constexpr int UMAX = (kLatMaxK / 4 + BD - 1) / BD;  // x chunks per thread per row, at most
+  static_assert(WPB % KS == 0, "gemv_lat: whole row groups per workgroup");
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int rg = wave / KS, kw = wave % KS;  // row group, K part
   const int rs = lane / LPR, li = lane % LPR;
-  const int row0 = (blockIdx.x * WPB + wave) * RPL * RPW + rs;
+  const int row0 = (blockIdx.x * (WPB / KS) + rg) * RPL * RPW + rs;
   const int RB = INT4 ? a.K / 2 : a.K;
   const int nseg = a.K / SEGK;
+  const int seg0 = kw * NSEG;  // this wavefront's first segment
   const int wchunks = a.K / 4, rounds = (wchunks + BD - 1) / BD;
   const bool has_inv = INT4 && a.inv != nullptr;
 
@@ -426,12 +433,12 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < RPL; ++r) {
       const int64_t row = min(row0 + r * RPW, a.N - 1);
-      w[j][r] = load16(a.w + row * RB + min(j, nseg - 1) * LPR * 16 + li * 16);
+      w[j][r] = load16(a.w + row * RB + min(seg0 + j, nseg - 1) * LPR * 16 + li * 16);
     }
   if constexpr (INT4) {
 #pragma unroll
     for (int j = 0; j < NSEG; ++j) {
-      const int slice = j * LPR + li;
+      const int slice = (seg0 + j) * LPR + li;
       const int g = a.spg_log2 >= 0 ? slice >> a.spg_log2 : slice / (a.K / CPL / a.G);
 #pragma unroll
       for (int r = 0; r < RPL; ++r) {
@@ -442,23 +449,31 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
       }
     }
   }
-  // 3. x * inv into LDS (rotated slices), one barrier
+  // 3. x * inv into LDS (rotated slices) and, for int4, each slice's channel sum of x * inv
+  //    per row (xsl [slice][MT]: the (z - 8 s) factor, the same for every weight row, summed
+  //    once per workgroup: the 8 chunk sums of a slice sit in 8 consecutive lanes and meet
+  //    with DPP), one barrier
+  [[maybe_unused]] float* xsl = xs + MT * a.K;
 #pragma unroll
   for (int u = 0; u < UMAX; ++u) {
+    if (u >= rounds) continue;  // uniform
     const int q = threadIdx.x + u * BD;
-    if (u < rounds && q < wchunks) {
-      const int sl = q / CPC;
-      float* dst = xs + (sl * CPC + chunk_pos<CPC>(sl, q % CPC)) * 4;
+    const bool on = q < wchunks;  // whole slices (K % 32 == 0): a slice's 8 lanes agree
+    const int sl = q / CPC;
+    float* dst = xs + (sl * CPC + chunk_pos<CPC>(sl, q % CPC)) * 4;
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        float4 v = xv4[m][u];
-        if (has_inv) {
-          v.x = __fmul_rn(v.x, iv4[u].x);
-          v.y = __fmul_rn(v.y, iv4[u].y);
-          v.z = __fmul_rn(v.z, iv4[u].z);
-          v.w = __fmul_rn(v.w, iv4[u].w);
-        }
-        lds_st4(dst + m * a.K, v);
+    for (int m = 0; m < MT; ++m) {
+      float4 v = xv4[m][u];
+      if (has_inv) {
+        v.x = __fmul_rn(v.x, iv4[u].x);
+        v.y = __fmul_rn(v.y, iv4[u].y);
+        v.z = __fmul_rn(v.z, iv4[u].z);
+        v.w = __fmul_rn(v.w, iv4[u].w);
+      }
+      if (on) lds_st4(dst + m * a.K, v);
+      if constexpr (INT4) {
+        const float cs = lsh::group_sum<CPC>(on ? (v.x + v.y) + (v.z + v.w) : 0.f);
+        if (on && q % CPC == 0) xsl[sl * MT + m] = cs;
       }
     }
   }
@@ -471,8 +486,8 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
     for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
 #pragma unroll
   for (int j = 0; j < NSEG; ++j) {
-    if (j >= nseg) break;
-    const int sl = j * LPR + li;
+    if (seg0 + j >= nseg) break;
+    const int sl = (seg0 + j) * LPR + li;
     float wf[RPL][CPL];
 #pragma unroll
     for (int r = 0; r < RPL; ++r)
@@ -495,9 +510,7 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
         xv[4 * i + 3] = v.w;
       }
       if constexpr (INT4) {
-        float xsum = 0.f;
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) xsum += xv[i];
+        const float xsum = xsl[sl * MT + m];
 #pragma unroll
         for (int r = 0; r < RPL; ++r) {
           float d = 0.f;
@@ -516,15 +529,37 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
       }
     }
   }
+  float tot[RPL][MT];
+#pragma unroll
+  for (int r = 0; r < RPL; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) tot[r][m] = lsh::group_total<LPR>(acc[r][m]);
+  if constexpr (KS > 1) {
+    // [row group][row slot][m][K part] after the staged x and slice sums
+    float* red = xs + MT * (a.K + (INT4 ? a.K / 32 : 0));
+    const int base = ((rg * RPW + rs) * MT) * KS;
+    if (li == LPR - 1) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) red[base + m * KS + kw] = tot[0][m];
+    }
+    __syncthreads();
+    if (kw != 0) return;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      float v = red[base + m * KS];
+#pragma unroll
+      for (int k = 1; k < KS; ++k) v += red[base + m * KS + k];
+      tot[0][m] = v;
+    }
+  }
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
     const int row = row0 + r * RPW;
     const float sr = (!INT4 && row < a.N) ? a.s[row] : 1.f;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      const float v = lsh::group_total<LPR>(acc[r][m]);
       if (li == LPR - 1 && row < a.N && m < a.M)
-        a.y[static_cast<int64_t>(m) * a.N + row] = INT4 ? v : v * sr;
+        a.y[static_cast<int64_t>(m) * a.N + row] = INT4 ? tot[r][m] : tot[r][m] * sr;
     }
   }
 }
@@ -690,7 +725,8 @@ void run_generic(const GemvArgs& a, hipStream_t st) {
 template <int MT, int LPR, int NSEG, bool INT4>
 void launch_lat(const GemvArgs& a, int wpb, hipStream_t st) {
   constexpr int rpw = kWave / LPR;
-  const size_t lds = static_cast<size_t>(MT) * a.K * sizeof(float);
+  // staged x, and for int4 the channel sum of each 32-channel slice per row
+  const size_t lds = static_cast<size_t>(MT) * (a.K + (INT4 ? a.K / 32 : 0)) * sizeof(float);
   const int rows_per_block = wpb * rpw;
   const dim3 grid((a.N + rows_per_block - 1) / rows_per_block);
   constexpr int kSmallWpb = MT > 2 ? 4 : 2;  // MT > 2 always runs 4 wavefronts
@@ -701,8 +737,27 @@ void launch_lat(const GemvArgs& a, int wpb, hipStream_t st) {
                 true, a);
 }
 
+// K split over KS wavefronts (one segment each), two row groups per workgroup.
+template <int MT, int LPR, int KS, bool INT4>
+void launch_lat_split(const GemvArgs& a, hipStream_t st) {
+  constexpr int rpw = kWave / LPR, WPB = 2 * KS;
+  const size_t lds = (static_cast<size_t>(MT) * (a.K + (INT4 ? a.K / 32 : 0)) +
+                      static_cast<size_t>(WPB / KS) * rpw * MT * KS) * sizeof(float);
+  const int rows_per_block = (WPB / KS) * rpw;
+  const dim3 grid((a.N + rows_per_block - 1) / rows_per_block);
+  lsh::launch(gemv_lat<MT, LPR, 1, WPB, INT4, KS>, grid, dim3(WPB * kWave), lds, st, true, a);
+}
+
 template <int MT, int LPR, bool INT4>
 void launch_lat_lpr(const GemvArgs& a, int nseg, int wpb, hipStream_t st) {
+  if constexpr (MT <= 2) {
+    switch (nseg) {  // several segments per lane: split them over wavefronts instead
+      case 2: return launch_lat_split<MT, LPR, 2, INT4>(a, st);
+      case 3: return launch_lat_split<MT, LPR, 3, INT4>(a, st);
+      case 4: return launch_lat_split<MT, LPR, 4, INT4>(a, st);
+      default: break;
+    }
+  }
   switch (nseg) {
     case 1: launch_lat<MT, LPR, 1, INT4>(a, wpb, st); break;
     case 2: launch_lat<MT, LPR, 2, INT4>(a, wpb, st); break;

@@ -246,3 +246,32 @@ def test_xfrag_rejects_bad_shapes(gpu):
                               torch.ones(256, device="cuda"), None, 1e-6)
     with pytest.raises(RuntimeError, match="fragments"):
         f.int4_linear_gemm_xfrag(xf, pk, 17, 64, 256, 128)  # buffer of one 16-row tile
+
+
+@pytest.mark.parametrize("T", [1, 5, 16])
+@pytest.mark.parametrize("awq", [True, False])
+def test_one_tile_packed_gemm_equals_fragment_path(gpu, T, awq):
+    """Up to 16 rows int4_linear_gemm_packed builds the fragments inside its one launch; they
+    and the products are the split pass's, so the result equals the fragment consumer on the
+    fragments a norm or silu * up kernel writes, bit for bit (same per-wavefront blocks and
+    the same fixed-order sum of the wavefronts at these shapes)."""
+    from llmserve.kernels import load_int8_gemv
+
+    f, lin = fo(), load_int8_gemv()
+    H, I, N = 1024, 3072, 4096
+    rng = np.random.default_rng(7 * T + awq)
+    x0 = rng.standard_normal((T, H)).astype(F32)
+    r = rng.standard_normal((T, H)).astype(F32)
+    w = (1 + 0.1 * rng.standard_normal(H)).astype(F32)
+    pk, inv = _int4_packed(N, H, 3, awq)
+    xa, xb = cu.dev(x0), cu.dev(x0)
+    h = f.add_rmsnorm_(xa, cu.dev(r), cu.dev(w), 1e-6)
+    ref = lin.int4_linear_gemm_packed(h, pk, N, 128, inv)
+    got = f.int4_linear_gemm_xfrag(f.add_rmsnorm_xfrag_(xb, cu.dev(r), cu.dev(w), inv, 1e-6),
+                                   pk, T, N, H, 128)
+    assert torch.equal(got, ref)
+    pkd, invd = _int4_packed(1024, I, 4, awq)
+    gu = cu.dev(rng.standard_normal((T, 2 * I)).astype(F32))
+    ref = lin.int4_linear_gemm_packed(f.silu_mul(gu), pkd, 1024, 128, invd)
+    got = f.int4_linear_gemm_xfrag(f.silu_mul_xfrag(gu, invd), pkd, T, 1024, I, 128)
+    assert torch.equal(got, ref)

@@ -49,7 +49,8 @@ def test_int4_reference_goldens(gpu, kg, M, K, N, g):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 16, 17, 33, 64])
-@pytest.mark.parametrize("N,K", [(6144, 1024), (1024, 3072), (96, 8192), (130, 448)])
+@pytest.mark.parametrize("N,K", [(6144, 1024), (1024, 3072), (96, 8192), (130, 448), (200, 4096),
+                                 (300, 2048)])
 def test_int8_shapes(gpu, M, N, K):
     rng = np.random.default_rng(M * 1000 + N + K)
     x = rng.standard_normal((M, K)).astype(F32)
@@ -63,7 +64,7 @@ def test_int8_shapes(gpu, M, N, K):
 QWEN = [(4096, 1024), (1024, 2048), (6144, 1024), (1024, 3072)]  # qkv, o, gate_up, down
 
 
-@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("M", [1, 2, 4, 16])
 @pytest.mark.parametrize("N,K", QWEN)
 def test_int4_awq_qwen_shapes(gpu, M, N, K):
     """g128 AWQ linears, activations with 1% outlier channels x20."""
@@ -82,7 +83,8 @@ def test_int4_awq_qwen_shapes(gpu, M, N, K):
 
 @pytest.mark.parametrize("M,N,K,g", [(1, 64, 256, 64), (3, 96, 512, 32), (7, 40, 1536, 64),
                                      (16, 128, 2048, 64), (2, 33, 96, 32), (64, 64, 1024, 128),
-                                     (20, 256, 4096, 128), (1, 8, 64, 2)])
+                                     (20, 256, 4096, 128), (1, 8, 64, 2), (1, 100, 4096, 128),
+                                     (2, 70, 2048, 32), (1, 50, 3072, 64)])
 def test_int4_group_sizes_and_tails(gpu, M, N, K, g):
     rng = np.random.default_rng(M + N + K + g)
     w = (rng.standard_normal((N, K)) * 0.02).astype(F32)

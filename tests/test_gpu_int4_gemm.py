@@ -259,3 +259,16 @@ def test_int4linear_packed_paths(gpu, rows):
     q.kernel = "gemm_ref"
     with pytest.raises(RuntimeError, match="multiple of 16"):
         q(x)
+
+
+@pytest.mark.parametrize("M,N,K,g,awq", [(1, 40, 128, 128, True), (2, 1024, 4096, 128, False),
+                                          (9, 200, 1536, 256, True), (15, 6144, 1024, 128, False),
+                                          (16, 64, 3200, 640, True), (3, 1024, 2048, 1024, True)])
+def test_one_tile_packed_gemm_odd_shapes(gpu, M, N, K, g, awq):
+    """The one-launch kernel for up to 16 rows: one K block (four wavefronts, three idle
+    blocks masked), two rounds of 16 blocks, groups spanning several blocks, a single
+    partial slab, no AWQ scale."""
+    x, nib, gs, gz, inv = _case(M, N, K, g, 11 * M + N + K, awq=awq)
+    packed = cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), g)
+    y = cu.int4_linear_gemm_packed(cu.dev(x), packed, N, g, None if inv is None else cu.dev(inv))
+    cu.assert_rel_close(y, mr.int4_linear_f64(x, nib, gs, gz, g, inv), TOL, f"M={M} {N}x{K} g{g}")

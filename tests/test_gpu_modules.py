@@ -70,7 +70,7 @@ def test_int4linear_decode_rows(gpu, N, K):
     m = Int4Linear(lin, 128, torch.from_numpy(act), device="cuda")
     nib, gs, gz, inv = oq.int4_quantize_pack(lin.weight.detach().numpy(), 128, act)
     assert np.array_equal(m.nibbles.cpu().numpy(), nib)
-    for rows in (1, 3, 4, 5, 16):
+    for rows in (1, 2, 3, 4, 5, 9, 16):
         assert m.packed_path(rows) == (rows > 4)
         x = rng.standard_normal((rows, K)).astype(F32)
         x[:, rng.permutation(K)[: K // 100]] *= 20
