@@ -164,12 +164,19 @@ int llmserve_int4_linear_gemm_packed(const float* x, const float* inv_act_scale 
  * Activation fragments: x' = x * inv_act_scale as the packed kernel reads it (bf16 hi / mid /
  * lo pieces in wavefront order, then fp32 sums of x' over every 128-channel block; rows up to M
  * rounded to 16, the extra rows zero). llmserve_int4_xfrag_bytes(M, K) bytes, 16-byte aligned.
- * Written by llmserve_int4_linear_gemm_packed's own split pass or by the fused producers
- * below (bit-identical for the same x'); read by llmserve_int4_linear_gemm_xfrag, which is
- * llmserve_int4_linear_gemm_packed without its split pass. No counterpart in the reference:
- * they fuse Int4Linear's `x * inv_act_scale` (quant.py:141) into the producing kernel.
+ * Written by llmserve_int4_xfrag_split (the split pass of llmserve_int4_linear_gemm_packed
+ * above 16 rows; up to 16 rows that entry point builds the same values inside its one launch
+ * and leaves its workspace unused) or by the fused producers below (bit-identical for the same
+ * x'); read by llmserve_int4_linear_gemm_xfrag, which is llmserve_int4_linear_gemm_packed on
+ * given fragments. No counterpart in the reference: they fuse Int4Linear's
+ * `x * inv_act_scale` (quant.py:141) into the producing kernel.
  */
 int64_t llmserve_int4_xfrag_bytes(int64_t M, int64_t K);
+/* x [M, K] fp32 (times inv_act_scale [K] when given) -> fragments in xfrag
+ * (xfrag_bytes >= llmserve_int4_xfrag_bytes(M, K); K a multiple of 128). */
+int llmserve_int4_xfrag_split(const float* x, const float* inv_act_scale /* nullable */,
+                              void* xfrag, int64_t M, int64_t K, int64_t xfrag_bytes,
+                              void* stream);
 int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* packed, float* y, int64_t M,
                                     int64_t N, int64_t K, int64_t group_size, void* stream);
 
@@ -308,9 +315,10 @@ int llmserve_argmax_advance(const float* logits, int64_t T, int64_t V, int64_t* 
  * fp32 LM head on activation fragments (replaces the tied-embedding lm_head,
  * models/transformer.py:192-193): y[M, V] = x[M, K] . w[V, K]^T with w fp32 row-major and x
  * given as llmserve_int4_xfrag_bytes(M, K) bytes of fragments (written, e.g., by
- * llmserve_add_rmsnorm_xfrag with act_inv = NULL). Split-bf16 matrix-core products (the hi and
- * mid pieces of x, w as bf16 hi + lo, four products, fp32 accumulation): within a few 1e-6
- * relative of fp32. K a multiple of 128; xfrag, w and y 16-byte aligned.
+ * llmserve_add_rmsnorm_xfrag with act_inv = NULL). Split-bf16 matrix-core products (the hi,
+ * mid and lo pieces of x and of w, the six products down to 2^-16 of the leading one, fp32
+ * accumulation): each product is the fp32 product up to fp32's rounding. K a multiple of 128;
+ * xfrag, w and y 16-byte aligned.
  */
 int llmserve_lm_head_f32_xfrag(const void* xfrag, const float* w, float* y, int64_t M, int64_t V,
                                int64_t K, void* stream);

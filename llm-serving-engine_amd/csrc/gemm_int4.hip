@@ -909,6 +909,27 @@ extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv
   return lsh::launch_status("int4_linear_gemm_packed");
 }
 
+extern "C" int llmserve_int4_xfrag_split(const float* x, const float* inv_act_scale, void* xfrag,
+                                         int64_t M, int64_t K, int64_t xfrag_bytes, void* stream) {
+  LSH_CHECK(M >= 0 && K >= kBlk && K % kBlk == 0, "int4_xfrag_split: K must be a multiple of 128");
+  LSH_CHECK(M < (1LL << 31) && K < (1LL << 31) && M * K < (1LL << 40), "int4_xfrag_split: shape too large");
+  if (M == 0) return LLMSERVE_OK;
+  LSH_CHECK(x && xfrag, "int4_xfrag_split: null pointer");
+  LSH_CHECK(lsh::aligned16(x) && lsh::aligned16(xfrag) &&
+                (inv_act_scale == nullptr || lsh::aligned16(inv_act_scale)),
+            "int4_xfrag_split: x, inv_act_scale and xfrag must be 16-byte aligned");
+  LSH_CHECK(xfrag_bytes >= lsh::frag_bytes(M, K), "int4_xfrag_split: %lld bytes of fragments needed",
+            (long long)lsh::frag_bytes(M, K));
+  const int nb = static_cast<int>(K / kBlk);
+  const int64_t mtiles = (M + kRows - 1) / kRows;
+  const int mp = static_cast<int>(xsum_rows(M));
+  __bf16* xf = static_cast<__bf16*>(xfrag);
+  lsh::launch(x_split_frag_kernel, dim3(static_cast<unsigned>(mtiles * nb)), dim3(256), 0,
+              lsh::as_stream(stream), true, x, inv_act_scale, xf, lsh::frag_sums(xf, mp, K),
+              static_cast<int>(M), static_cast<int>(K), mp);
+  return lsh::launch_status("int4_xfrag_split");
+}
+
 extern "C" int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* packed, float* y,
                                                int64_t M, int64_t N, int64_t K,
                                                int64_t group_size, void* stream) {

@@ -1,13 +1,13 @@
 // fp32 LM head of the decode step on activation fragments (replaces the tied-embedding
 // lm_head of models/transformer.py:192-193, F.linear(h, embed.weight)):
 //   y[m, v] = sum_k x[m, k] * W[v, k]      W fp32 [V, K] row-major (the embedding matrix)
-// x arrives as the bf16 fragments of xfrag.h, of which this kernel reads the hi and mid pieces
-// (x = xh + xm to 2^-17 relative: the head is the last operation of the step, where that
-// error is not amplified by later layers); each W value is split the same way in registers
-// (W = wh + wl), and the four products
-// wh*xh + wh*xm + wl*xh + wl*xm go through v_mfma_f32_16x16x32_bf16 (each product of two bf16
-// values is exact in fp32) with fp32 accumulation. Only the two split residuals are lost:
-// each product is within ~2^-15 of fp32, the sums within a few 1e-6 relative.
+// x arrives as the bf16 fragments of xfrag.h (x = xh + xm + xl to ~2^-26 relative); each W
+// value is split the same way in registers (W = wh + wm + wl), and the six products whose
+// weight is at least 2^-16 of wh*xh -- wh*xh, wh*xm, wm*xh, wh*xl, wl*xh, wm*xm -- go through
+// v_mfma_f32_16x16x32_bf16 (each product of two bf16 values is exact in fp32) with fp32
+// accumulation. What is left out (wm*xl, wl*xm, wl*xl and the ~2^-26 split residuals) is
+// below 2^-23 of each product: every product is the fp32 product up to fp32's own rounding,
+// as in the reference's fp32 F.linear.
 //
 // The kernel streams W once (622 MB at Qwen3-0.6B: HBM-bound). A workgroup of 8 wavefronts
 // (about one per CU, looping over vocab tiles) owns 128 vocab rows at a time, 16 per
@@ -22,7 +22,7 @@
 //   * the products' k order is therefore permuted: step q's lane group g = l / 16 takes
 //     channels 32 q + 4 g .. + 4 and 32 q + 16 + 4 g .. + 4, and x's fragments are rearranged
 //     to match as they are staged (8-byte halves of the fragment pieces);
-//   * 4 steps x 4 row tiles x 4 products = 64 MFMAs.
+//   * 4 steps x 4 row tiles x 6 products = 96 MFMAs.
 // The output lane holds vocab rows 4 (l / 16) .. + 4 of batch row l % 16: one 16-byte store.
 #include "common.h"
 #include "xfrag.h"
@@ -37,7 +37,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 8;                 // wavefronts per workgroup
 constexpr int kVRows = 16 * kWaves;       // vocab rows per workgroup
 constexpr int kMaxTiles = 4;              // 16-row tiles of x per pass (64 rows)
-constexpr int kTilePieces = 512;  // 16-byte pieces of the hi and mid parts of one (row tile, block)
+constexpr int kXParts = lsh::kFragPieces;           // hi, mid, lo of x
+constexpr int kTilePieces = 4 * kXParts * 64;  // 16-byte pieces of one (row tile, block)
 constexpr int kBlkElems = 4 * lsh::kFragPieces * kWave * 8;  // bf16 of one (row tile, block)
 
 struct LmArgs {
@@ -47,14 +48,17 @@ struct LmArgs {
   int M, V, K, nblk;
 };
 
-// W row chunk -> bf16 hi / lo A operands of step q (8 channels; W = hi + lo to 2^-17).
-__device__ __forceinline__ void split_w(const u32x4& p0, const u32x4& p1, bf16x8& hi, bf16x8& lo) {
+// W row chunk -> bf16 hi / mid / lo A operands of step q (8 channels; W = hi + mid + lo to
+// ~2^-26).
+__device__ __forceinline__ void split_w(const u32x4& p0, const u32x4& p1, bf16x8& hi, bf16x8& mid,
+                                        bf16x8& lo) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float v = __builtin_bit_cast(float, e < 4 ? p0[e] : p1[e - 4]);
-    __bf16 h, l;
-    lsh::split_bf16(v, h, l);
+    __bf16 h, m, l;
+    lsh::split3_bf16(v, h, m, l);
     hi[e] = h;
+    mid[e] = m;
     lo[e] = l;
   }
 }
@@ -78,18 +82,20 @@ __global__ __launch_bounds__(kWaves * kWave) void lm_head_f32_kernel(LmArgs a) {
   // W rows of step s: vocab tile blockIdx.x + (s / nblk) gridDim.x, block s % nblk
   auto vtile = [&](int s) { return static_cast<int>(blockIdx.x) + (s / a.nblk) * static_cast<int>(gridDim.x); };
 
-  // x staging: 16-byte piece p = tid + 512 i of the hi and mid parts of the T (row tile,
-  // block) fragments; within one, piece (2 q + h) * 64 + lane comes from step q, part h
+  // x staging: 16-byte piece p = tid + 512 i of the hi, mid and lo parts of the T (row tile,
+  // block) fragments; within one, piece (3 q + h) * 64 + lane comes from step q, part h
   // (lane = fr + 16 fc: row fr, channels 32 fc + 8 q .. + 8)
-  constexpr int kPer = T * kTilePieces / (kWaves * kWave);
+  constexpr int kPieces = T * kTilePieces;
+  constexpr int kPer = (kPieces + kWaves * kWave - 1) / (kWaves * kWave);
   auto load_x = [&](int b, u32x4 (&r)[kPer]) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int p = tid + i * kWaves * kWave;
+      if (kPieces % (kWaves * kWave) != 0 && p >= kPieces) continue;  // last round's tail
       const int t = p / kTilePieces, within = p % kTilePieces;
-      const int qh = within / kWave, l = within % kWave;  // qh = 2 q + h
-      r[i] = xg[((static_cast<int64_t>(tile0 + t) * a.nblk + b) * 4 + qh / 2) *
-                    (lsh::kFragPieces * kWave) + (qh % 2) * kWave + l];
+      const int qh = within / kWave, l = within % kWave;  // qh = 3 q + h
+      r[i] = xg[((static_cast<int64_t>(tile0 + t) * a.nblk + b) * 4 + qh / kXParts) *
+                    (lsh::kFragPieces * kWave) + (qh % kXParts) * kWave + l];
     }
   };
   // Staged in the products' k order: source piece (step q', part h, lane fr + 16 fc) holds
@@ -99,14 +105,15 @@ __global__ __launch_bounds__(kWaves * kWave) void lm_head_f32_kernel(LmArgs a) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int p = tid + i * kWaves * kWave;
+      if (kPieces % (kWaves * kWave) != 0 && p >= kPieces) continue;
       const int t = p / kTilePieces, within = p % kTilePieces;
       const int qh = within / kWave, l = within % kWave;
-      const int qs = qh / 2, h = qh % 2, fr = l % 16, fc = l / 16;
+      const int qs = qh / kXParts, h = qh % kXParts, fr = l % 16, fc = l / 16;
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         const int g = 2 * (qs & 1) + hf;
-        u32x2* d = reinterpret_cast<u32x2*>(&xs[buf][t * kTilePieces + (2 * fc + h) * kWave + fr + 16 * g]);
+        u32x2* d = reinterpret_cast<u32x2*>(&xs[buf][t * kTilePieces + (kXParts * fc + h) * kWave + fr + 16 * g]);
         d[qs >> 1] = u32x2{r[i][2 * hf], r[i][2 * hf + 1]};
       }
     }
@@ -167,16 +174,21 @@ __global__ __launch_bounds__(kWaves * kWave) void lm_head_f32_kernel(LmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      bf16x8 wh, wl;
-      split_w(wc[2 * q], wc[2 * q + 1], wh, wl);
+      bf16x8 wh, wm, wl;
+      split_w(wc[2 * q], wc[2 * q + 1], wh, wm, wl);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const bf16x8 xh = __builtin_bit_cast(bf16x8, xs[cur][t * kTilePieces + (q * 2) * kWave + lane]);
-        const bf16x8 xl = __builtin_bit_cast(bf16x8, xs[cur][t * kTilePieces + (q * 2 + 1) * kWave + lane]);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, xh, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, xl, acc[t], 0, 0, 0);
+        const u32x4* xq = &xs[cur][t * kTilePieces + (q * kXParts) * kWave + lane];
+        const bf16x8 xh = __builtin_bit_cast(bf16x8, xq[0]);
+        const bf16x8 xm = __builtin_bit_cast(bf16x8, xq[kWave]);
+        const bf16x8 xl = __builtin_bit_cast(bf16x8, xq[2 * kWave]);
+        // smallest terms first: each is added to an accumulator of its own magnitude
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wm, xm, acc[t], 0, 0, 0);
         acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wl, xh, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wl, xl, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, xl, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wm, xh, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, xm, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, xh, acc[t], 0, 0, 0);
       }
     }
     if (s % a.nblk == a.nblk - 1) store_tile(s);

@@ -48,12 +48,6 @@ __device__ __forceinline__ int64_t frag_offset(int m, int c, int nblk) {
   return ((((static_cast<int64_t>(t) * nblk + b) * 4 + q) * kFragPieces) * 64 + fr + 16 * fc) * 8 + e;
 }
 
-// hi / lo bf16 split of an fp32 value (round to nearest even; hi + lo equals v to 2^-17).
-__device__ __forceinline__ void split_bf16(float v, __bf16& hi, __bf16& lo) {
-  hi = static_cast<__bf16>(v);
-  lo = static_cast<__bf16>(v - static_cast<float>(hi));
-}
-
 // hi / mid / lo bf16 split (each difference exact in fp32; the sum equals v to ~2^-26).
 __device__ __forceinline__ void split3_bf16(float v, __bf16& hi, __bf16& mid, __bf16& lo) {
   hi = static_cast<__bf16>(v);

@@ -169,8 +169,9 @@ class QuantCausalLM(nn.Module):
     # matrix-core kernel on them: one launch less per linear, same result bits.
     fuse_xfrag = True
     # With fragments, the fp32 LM head runs the split-bf16 matrix-core kernel
-    # (lm_head_f32_xfrag, within a few 1e-6 of fp32) instead of torch.mm (hipBLASLt); at 1-4
-    # rows the fp32 GEMV lm_head_f32 (exact fp32, reads the matrix once at HBM speed).
+    # (lm_head_f32_xfrag: three bf16 pieces of each operand, every product fp32-faithful)
+    # instead of torch.mm (hipBLASLt); at 1-4 rows the fp32 GEMV lm_head_f32 (exact fp32,
+    # reads the matrix once at HBM speed).
     fp32_head_kernel = True
 
     # Up to chain_max_rows rows the step runs one persistent launch per layer for the whole

@@ -199,20 +199,14 @@ def attention_metadata(seq_info, tables, block_size, T):
 
 
 def split_fragments(x, inv=None):
-    """The activation fragments of x * inv that llmserve_int4_linear_gemm_packed's split pass
-    leaves at the start of its workspace (run against a small packed weight)."""
+    """The activation fragments of x * inv (llmserve_int4_xfrag_split: the split pass of
+    llmserve_int4_linear_gemm_packed above 16 rows) as a uint8 tensor."""
     M, K = x.shape
-    dev = x.device
-    nib = torch.zeros(64, K // 2, dtype=torch.uint8, device=dev)
-    gs = torch.ones(64, K // 128, dtype=torch.float32, device=dev)
-    packed = int4_gemm_pack(nib, gs, torch.zeros_like(gs), 128)
     L = capi()
-    nbytes = L.llmserve_int4_linear_gemm_packed_workspace_bytes(M, K)
-    ws = torch.zeros(max(nbytes, 16) // 16 * 16 + 16, dtype=torch.uint8, device=dev)
-    y = torch.empty(M, 64, dtype=torch.float32, device=dev)
-    check(L.llmserve_int4_linear_gemm_packed(_p(x), _p(inv), _p(packed), _p(y), M, 64, K, 128,
-                                             _p(ws), nbytes, _stream()))
-    return ws[:L.llmserve_int4_xfrag_bytes(M, K)]
+    nbytes = L.llmserve_int4_xfrag_bytes(M, K)
+    ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=x.device)
+    check(L.llmserve_int4_xfrag_split(_p(x), _p(inv), _p(ws), M, K, nbytes, _stream()))
+    return ws[:nbytes]
 
 
 def assert_rel_close(got, ref, tol: float, what: str = ""):

@@ -1,7 +1,8 @@
 """fp32 LM head on activation fragments (llmserve_lm_head_f32_xfrag) against float64.
 
-x and W are each split into bf16 hi + lo (exact to ~2^-16 relative) and the four products
-accumulate in fp32, so the logits are within a few 1e-6 of fp32; the bound here is
+x and W are each split into bf16 hi + mid + lo (~2^-26 relative) and the six products whose
+weight reaches 2^-16 of the leading one accumulate in fp32, so each product is the fp32
+product up to fp32's own rounding (the reference's fp32 F.linear); the bound here is
 max-abs <= 2e-5 * max|ref| and rel-L2 <= 2e-5 against x . W^T in float64. Shapes cover a
 partial row tile (rows past M are zero fragments and are not stored), several 64-row passes
 plus a remainder, vocab sizes that are not multiples of 64 or 4 (clamped loads, scalar
