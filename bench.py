@@ -202,11 +202,11 @@ def kernel_avg_us(torch, launch, n: int, reps: int = 20) -> float:
 # config 1's int8 GEMV (profiles/gemv_kernel_trace.md, `bench.py --only gemv`), config 4's
 # decode and merge (profiles/attention_kernel_trace.md, `bench.py --only attention`).
 PROFILE_ROWS = {
-    "qkv": ("gemv_kernel_trace.md", "gemv_lat<1, 32, 1, 4, true>", "512 x 1"),
-    "o": ("gemv_kernel_trace.md", "gemv_lat<1, 64, 1, 4, true>", "256 x 1"),
-    "gate_up": ("gemv_kernel_trace.md", "gemv_lat<1, 32, 1, 4, true>", "768 x 1"),
+    "qkv": ("gemv_kernel_trace.md", "gemv_lat<1, 32, 1, 4, true, 1>", "512 x 1"),
+    "o": ("gemv_kernel_trace.md", "gemv_lat<1, 64, 1, 4, true, 1>", "256 x 1"),
+    "gate_up": ("gemv_kernel_trace.md", "gemv_lat<1, 32, 1, 4, true, 1>", "768 x 1"),
     "down": ("gemv_kernel_trace.md", "gemv_lat<1, 32, 1, 6, true, 3>", "256 x 1"),
-    "c1": ("gemv_kernel_trace.md", "gemv_lat<1, 64, 1, 4, false>", "1536 x 1"),
+    "c1": ("gemv_kernel_trace.md", "gemv_lat<1, 64, 1, 4, false, 1>", "1536 x 1"),
     "c4_decode": ("attention_kernel_trace.md", "paged_decode_kernel<signed char, 128, 2, true, true>",
                   "256 x 1"),
     "c4_merge": ("attention_kernel_trace.md", "paged_decode_merge_kernel<128>", "128 x 1"),
