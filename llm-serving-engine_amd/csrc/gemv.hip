@@ -401,6 +401,7 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int rg = wave / KS, kw = wave % KS;  // row group, K part
   const int rs = lane / LPR, li = lane % LPR;
+  const bool lead = li == LPR - 1;  // the lane that holds the row total
   const int row0 = (blockIdx.x * (WPB / KS) + rg) * RPL * RPW + rs;
   const int RB = INT4 ? a.K / 2 : a.K;
   const int nseg = a.K / SEGK;
@@ -538,7 +539,7 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
     // [row group][row slot][m][K part] after the staged x and slice sums
     float* red = xs + MT * (a.K + (INT4 ? a.K / 32 : 0));
     const int base = ((rg * RPW + rs) * MT) * KS;
-    if (li == LPR - 1) {
+    if (lead) {
 #pragma unroll
       for (int m = 0; m < MT; ++m) red[base + m * KS + kw] = tot[0][m];
     }
@@ -558,7 +559,7 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_lat(GemvArgs a) {
     const float sr = (!INT4 && row < a.N) ? a.s[row] : 1.f;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      if (li == LPR - 1 && row < a.N && m < a.M)
+      if (lead && row < a.N && m < a.M)
         a.y[static_cast<int64_t>(m) * a.N + row] = INT4 ? tot[r][m] : tot[r][m] * sr;
     }
   }
@@ -750,7 +751,7 @@ void launch_lat_split(const GemvArgs& a, hipStream_t st) {
 
 template <int MT, int LPR, bool INT4>
 void launch_lat_lpr(const GemvArgs& a, int nseg, int wpb, hipStream_t st) {
-  if constexpr (MT <= 2) {
+  if constexpr (MT <= 4) {
     switch (nseg) {  // several segments per lane: split them over wavefronts instead
       case 2: return launch_lat_split<MT, LPR, 2, INT4>(a, st);
       case 3: return launch_lat_split<MT, LPR, 3, INT4>(a, st);
@@ -766,10 +767,11 @@ void launch_lat_lpr(const GemvArgs& a, int nseg, int wpb, hipStream_t st) {
   }
 }
 
-// The straight-line decode kernel for M <= 2, K <= kLatMaxK: the widest LPR (32 or 64)
-// whose segment divides the row into at most 4 segments; workgroups of 2 wavefronts when
-// there are fewer than 1024 wavefronts, so that the launch covers every CU. Returns false
-// when it does not apply.
+// The straight-line decode kernel for M <= 4, K <= kLatMaxK: the widest LPR (32 or 64)
+// whose segment divides the row into at most 4 segments. One segment per lane: workgroups of
+// 2 wavefronts when there are fewer than 1024 wavefronts, so that the launch covers every CU;
+// several: the segments go to as many wavefronts (launch_lat_split). Returns false when it
+// does not apply.
 template <bool INT4>
 bool try_lat(GemvArgs a, bool aligned, hipStream_t st) {
   if (a.M > 4 || a.K > kLatMaxK || !aligned || (INT4 && a.group % 32 != 0)) return false;
