@@ -852,6 +852,21 @@ def profile_only(torch, dev, what: str) -> int:
         for i in range(64):
             pk, inv = packed[i]
             gemv.int4_linear_gemm_packed(x, pk, N, GROUP, inv)
+    elif what == "gemm16":  # config 2 at 16 rows: the four shapes, packed weights, one launch
+        g = torch.Generator(device=dev).manual_seed(6)
+        gemv = load_int8_gemv()
+        for name, (N, K) in SHAPES.items():  # 32 distinct weights each
+            lins = []
+            for _ in range(32):
+                nib, gs, gz, inv = load_quant().int4_quantize(
+                    torch.randn(N, K, device=dev, generator=g) * 0.02, GROUP,
+                    torch.rand(K, device=dev, generator=g) + 0.5)
+                lins.append((gemv.int4_gemm_pack(nib, gs, gz, GROUP), inv))
+            x = torch.randn(16, K, device=dev, generator=g)
+            for i in range(64):
+                pk, inv = lins[i % 32]
+                gemv.int4_linear_gemm_packed(x, pk, N, GROUP, inv)
+            del lins
     elif what == "c5step":  # config 5's decode step: 2 + 10 graph replays, fp32 LM head
         c5_decode(torch, dev, 10, 2, profile=True)
     elif what == "c5step1":  # the config-5 model at batch 1: the per-layer chain, then per-op
@@ -893,7 +908,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
-    ap.add_argument("--only", choices=["gemv", "gemm4", "attention", "prefill", "lmhead", "copy",
+    ap.add_argument("--only", choices=["gemv", "gemm4", "gemm16", "attention", "prefill",
+                                       "lmhead", "copy",
                                        "c5step", "c5step1"],
                     help="profiling run: only launch that kernel (64 times) and exit")
     args = ap.parse_args()

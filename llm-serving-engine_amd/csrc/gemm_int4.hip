@@ -542,7 +542,7 @@ void int4_gemm_wide(Int4GemmArgs a, int mtiles, int groups) {
 // launch: each wavefront builds its K block's three-piece fragments and block sums from the
 // fp32 x rows itself, in registers, instead of reading those of a separate split pass. The
 // values are the split pass's bit for bit: x' = x * inv (rounded multiply), hi / mid / lo as
-// split3_bf16, and each row's block sum as the same pairwise tree (lane (fr, fc) holds the
+// split3_bf16 (two channels per packed conversion), and each row's block sum as the same pairwise tree (lane (fr, fc) holds the
 // channels 32 fc .. + 32 of row fr, i.e. the split pass's segments 4 fc .. 4 fc + 3: its
 // 8-channel trees and their first two butterfly levels are in-lane, the last two are lane
 // swaps 16 and 32 apart; the MFMA layout then wants the sums of rows 4 fc + r, fetched with
@@ -550,6 +550,22 @@ void int4_gemm_wide(Int4GemmArgs a, int mtiles, int groups) {
 // Work: S wavefronts split the K blocks of NT 16-column tiles (one block per wavefront and
 // round); NT = 1 gives each workgroup one tile of a slab, so a narrow output (N = 1024:
 // 16 slabs) spreads over 64 workgroups instead of 16.
+// v_permlane32_swap: the upper 32 lanes of a trade places with the lower 32 of b.
+__device__ __forceinline__ void swap_halves32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a),
+                                                  __builtin_bit_cast(uint32_t, b), false, false);
+  a = __builtin_bit_cast(float, static_cast<uint32_t>(r[0]));
+  b = __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+
+// v_permlane16_swap: the odd 16-lane rows of a trade places with the even rows of b.
+__device__ __forceinline__ void swap_rows16(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a),
+                                                  __builtin_bit_cast(uint32_t, b), false, false);
+  a = __builtin_bit_cast(float, static_cast<uint32_t>(r[0]));
+  b = __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+
 struct Int4GemmXArgs {
   const float* x;    // [M, K] fp32
   const float* inv;  // [K] AWQ pre-scale (INV only)
@@ -559,7 +575,7 @@ struct Int4GemmXArgs {
   int M, N, K, bpg;
 };
 
-template <int S, int NT, bool INV>
+template <int S, int NT, bool INV, bool CO>
 __global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
   extern __shared__ f32x4 red[];  // S > 1: [S][NT][64]
   constexpr int kUnits = kNT / NT;  // workgroups per slab
@@ -570,8 +586,10 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
   const int fr = lane % 16, fc = lane / 16;
   const int nblk = a.K / kBlk;
   const int slabs = (a.N + kCols - 1) / kCols;
-  const bool live = fr < a.M;
-  const float* xrow = a.x + static_cast<int64_t>(live ? fr : a.M - 1) * a.K + 32 * fc;
+  // rows past M repeat row M - 1 (in bounds): each output row depends on its own x row
+  // only, and theirs are not stored
+  const float* xrow =
+      a.x + static_cast<int64_t>(fr < a.M ? fr : a.M - 1) * a.K + (CO ? 4 * fc : 32 * fc);
 
   f32x4 acc[NT];
 #pragma unroll
@@ -587,16 +605,43 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
     const float* st = a.s + ((static_cast<int64_t>(g) * slabs + slab) * 16 + fr) * 8;
     const f32x4 s4 = *reinterpret_cast<const f32x4*>(st);
     const f32x4 z4 = *reinterpret_cast<const f32x4*>(st + 4);  // z - 8 s
+    // CO: load i gives lane (fr, fc) the channels 16 i + 4 fc .. + 4 of row fr: the four
+    // lanes of a row read 64 contiguous bytes, so each instruction touches 16 cache lines.
+    // Otherwise the MFMA layout is read directly (lane (fr, fc): channels 32 fc + 4 i .. + 4):
+    // 4 lines per distinct row, 64 at 16 rows, but no transpose (fewer instructions when few
+    // rows are distinct).
     f32x4 xv[8], iv[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = *reinterpret_cast<const f32x4*>(xrow + b * kBlk + 4 * i);
+    for (int i = 0; i < 8; ++i)
+      xv[i] = *reinterpret_cast<const f32x4*>(xrow + b * kBlk + (CO ? 16 : 4) * i);
     if constexpr (INV) {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        iv[i] = *reinterpret_cast<const f32x4*>(a.inv + b * kBlk + 32 * fc + 4 * i);
+        iv[i] = *reinterpret_cast<const f32x4*>(a.inv + b * kBlk +
+                                                (CO ? 16 * i + 4 * fc : 32 * fc + 4 * i));
     }
     // every load above goes out before the arithmetic below
     __builtin_amdgcn_sched_barrier(0);
+    float t[8][4];  // x' in the load layout
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) t[i][c] = INV ? __fmul_rn(xv[i][c], iv[i][c]) : xv[i][c];
+    // CO, to the MFMA layout (lane (fr, fc): channels 32 fc .. + 32 of row fr, in order): the
+    // loads 2 p, 2 p + 1 of lane group fc' belong to lane group p, as its channel quads fc'
+    // and 4 + fc'. A 4 x 4 transpose of (lane group, load pair) over the four 16-lane rows:
+    // swap the 32-lane halves of pairs (0, 2) and (1, 3), then the odd / even rows of pairs
+    // (0, 1) and (2, 3). Afterwards quad j of the lane's channels is t[2 (j % 4) + j / 4].
+    if constexpr (CO) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) swap_halves32(t[i][c], t[i + 4][c]);
+#pragma unroll
+      for (int i : {0, 1, 4, 5})
+#pragma unroll
+        for (int c = 0; c < 4; ++c) swap_rows16(t[i][c], t[i + 2][c]);
+    }
     u32x4 xh[4], xm[4], xl[4];
     float tq[4];
 #pragma unroll
@@ -604,23 +649,15 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
       float v[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float xe = xv[2 * q + e / 4][e % 4];
-        const float ve = INV ? __fmul_rn(xe, iv[2 * q + e / 4][e % 4]) : xe;
-        v[e] = live ? ve : 0.f;
+        const int j = 2 * q + e / 4;  // channel quad of the lane's 32
+        v[e] = t[CO ? 2 * (j % 4) + j / 4 : j][e % 4];
       }
       tq[q] = lsh::tree_sum<8>(v);
-      bf16x8 hi, mid, lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        __bf16 h, md, l;
-        lsh::split3_bf16(v[e], h, md, l);
-        hi[e] = h;
-        mid[e] = md;
-        lo[e] = l;
-      }
-      xh[q] = __builtin_bit_cast(u32x4, hi);
-      xm[q] = __builtin_bit_cast(u32x4, mid);
-      xl[q] = __builtin_bit_cast(u32x4, lo);
+      uint32_t h[4], md[4], l[4];
+      lsh::split3_words<8>(v, h, md, l);
+      xh[q] = u32x4{h[0], h[1], h[2], h[3]};
+      xm[q] = u32x4{md[0], md[1], md[2], md[3]};
+      xl[q] = u32x4{l[0], l[1], l[2], l[3]};
     }
     float rs = (tq[0] + tq[1]) + (tq[2] + tq[3]);  // row fr: this lane's 32 channels
     rs += __shfl_xor(rs, 16, kWave);               // + the neighbouring 32
@@ -671,27 +708,45 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
   }
 }
 
-template <int S, int NT>
+// Wavefronts of a workgroup whose wavefronts take one K block per round: the fewest rounds of
+// up to 16 wavefronts, then the smallest of 4, 8, 12, 16 that covers the nb blocks in that
+// many rounds.
+int one_block_waves(int nb) {
+  const int rounds = (nb + 15) / 16;
+  int S = 16;
+  for (int s : {12, 8, 4})
+    if (s * rounds >= nb) S = s;
+  return S;
+}
+
+template <int S, int NT, bool CO>
 void launch_x(const Int4GemmXArgs& a, int64_t slabs, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(slabs * (kNT / NT))), block(S * kWave);
   const size_t lds = S > 1 ? static_cast<size_t>(S) * NT * kWave * sizeof(f32x4) : 0;
   if (a.inv)
-    lsh::launch(int4_gemm_x<S, NT, true>, grid, block, lds, st, true, a);
+    lsh::launch(int4_gemm_x<S, NT, true, CO>, grid, block, lds, st, true, a);
   else
-    lsh::launch(int4_gemm_x<S, NT, false>, grid, block, lds, st, true, a);
+    lsh::launch(int4_gemm_x<S, NT, false, CO>, grid, block, lds, st, true, a);
 }
 
 // S: wavefronts to cover the K blocks in one round (up to 16: K = 2048; K = 3072 takes two
 // rounds); NT: tiles per workgroup. More workgroups beat less redundant conversion: config 2
 // at 16 rows (the four Qwen3-0.6B shapes, 112 launches) 273 GB/s with one tile per
 // workgroup, 276 with two, 219 with a whole slab (four); 5 rows 324 / 307 / 221.
+// CO (coalesced x loads and the lane transpose) above 8 rows: 16 rows 279 -> 292 GB/s;
+// at 1-8 rows the direct loads touch no more lines and skip the transpose (8 rows 330
+// against 319).
+// S = one_block_waves(nb) (idle wavefronts of a last round would still convert x): K = 3072
+// (24 blocks) takes two rounds of 12, 16 rows 292 -> 302 GB/s.
 void launch_x_tile(const Int4GemmXArgs& a, int64_t slabs, int nb, hipStream_t st) {
-  const int S = nb <= 4 ? 4 : (nb <= 8 ? 8 : 16);
+  const int S = one_block_waves(nb);
   const int NT = slabs * kNT <= 512 ? 1 : 2;
-#define LSH_X(s, nt) \
-  if (S == s && NT == nt) return launch_x<s, nt>(a, slabs, st);
-  LSH_X(4, 1) LSH_X(4, 2) LSH_X(4, 4) LSH_X(8, 1) LSH_X(8, 2) LSH_X(8, 4)
-  LSH_X(16, 1) LSH_X(16, 2) LSH_X(16, 4)
+  const bool co = a.M > 8;
+#define LSH_X(s, nt)                                            \
+  if (S == s && NT == nt)                                       \
+    return co ? launch_x<s, nt, true>(a, slabs, st) : launch_x<s, nt, false>(a, slabs, st);
+  LSH_X(4, 1) LSH_X(4, 2) LSH_X(8, 1) LSH_X(8, 2) LSH_X(12, 1) LSH_X(12, 2) LSH_X(16, 1)
+  LSH_X(16, 2)
 #undef LSH_X
 }
 
@@ -741,12 +796,13 @@ void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all
   int KB = std::min(2, (nb + 7) / 8);
   int S = 1;
   while (S < 8 && S * KB < nb) S *= 2;
-  // more than 8 blocks on a narrow output: 16 wavefronts of one block each (4 per SIMD) keep
-  // more loads in flight per CU than 8 of two blocks (o_proj at M = 64: 6.3 against 6.7 us;
-  // down, 24 blocks, takes two such rounds)
+  // more than 8 blocks on a narrow output: up to 16 wavefronts of one block each (4 per SIMD)
+  // keep more loads in flight per CU than 8 of two blocks (o_proj at M = 64: 6.3 against
+  // 6.7 us); the fewest rounds, then the smallest of 8, 12, 16 wavefronts covering the blocks
+  // in them (down, 24 blocks: two rounds of 12), as int4_gemm_x chooses
   if (KB == 2 && S == 8 && slabs * mtiles * planes < 256) {
     KB = 1;
-    S = 16;
+    S = one_block_waves(nb);
   }
   // very large outputs (an LM head) fill the GPU anyway: fewer, longer wavefronts
   if (KB == 1 && S == 8 && slabs * mtiles * planes * S > 16384) {
@@ -756,7 +812,7 @@ void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all
 #define LSH_LAT(kb, s) \
   if (KB == kb && S == s) return launch_lat_ks<kb, s>(a, slabs, mtiles, planes, bpp, st);
   LSH_LAT(1, 1) LSH_LAT(1, 2) LSH_LAT(1, 4) LSH_LAT(1, 8)
-  LSH_LAT(2, 4) LSH_LAT(2, 8) LSH_LAT(1, 16)
+  LSH_LAT(2, 4) LSH_LAT(2, 8) LSH_LAT(1, 12) LSH_LAT(1, 16)
 #undef LSH_LAT
 }
 

@@ -34,12 +34,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t b
                                            0x00020000);
 }
 
-__device__ __forceinline__ void unpack16(const u32x4& w, float (&f)[16]) {  // 16 int8 values
+// 16 int8 values, one sign-extending byte-select conversion each (left to itself the compiler
+// takes the odd bytes of the V words through a 16-bit shift first: 8 more instructions per
+// step).
+__device__ __forceinline__ void unpack16(const u32x4& w, float (&f)[16]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      f[4 * i + b] = static_cast<float>(static_cast<int8_t>((w[i] >> (8 * b)) & 0xffu));
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u = w[i];
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0"
+        : "=v"(f[4 * i]) : "v"(u));
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1"
+        : "=v"(f[4 * i + 1]) : "v"(u));
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2"
+        : "=v"(f[4 * i + 2]) : "v"(u));
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3"
+        : "=v"(f[4 * i + 3]) : "v"(u));
+  }
 }
 
 // 16 floats. The element goes through a named temporary: this compiler's __builtin_bit_cast of

@@ -49,36 +49,75 @@ __device__ __forceinline__ int64_t frag_offset(int m, int c, int nblk) {
 }
 
 // hi / mid / lo bf16 split (each difference exact in fp32; the sum equals v to ~2^-26).
+// The differences and sums below must stay separately rounded: fused with the multiply that
+// made v (x * inv), a difference would round differently in each producer. Every helper here
+// turns floating-point contraction off.
 __device__ __forceinline__ void split3_bf16(float v, __bf16& hi, __bf16& mid, __bf16& lo) {
+#pragma clang fp contract(off)
   hi = static_cast<__bf16>(v);
   const float r = v - static_cast<float>(hi);
   mid = static_cast<__bf16>(r);
   lo = static_cast<__bf16>(r - static_cast<float>(mid));
 }
 
+// split3_bf16 of two values at once, each piece of the pair as one 32-bit word (a in the low
+// half): one packed conversion per piece, whose halves are widened back to fp32 by shifting
+// and masking the packed word (converting each value alone as well would double the
+// conversions). Bit-identical to split3_bf16 of a and of b.
+__device__ __forceinline__ void split3_bf16x2(float a, float b, uint32_t& hi, uint32_t& mid,
+                                              uint32_t& lo) {
+#pragma clang fp contract(off)
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  auto pk = [](float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x, y}, bf16x2));
+  };
+  auto lo_f = [](uint32_t w) { return __builtin_bit_cast(float, w << 16); };
+  auto hi_f = [](uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); };
+  hi = pk(a, b);
+  const float ra = a - lo_f(hi), rb = b - hi_f(hi);
+  mid = pk(ra, rb);
+  lo = pk(ra - lo_f(mid), rb - hi_f(mid));
+}
+
+// The three pieces of N consecutive values as packed words (N / 2 words each).
+template <int N>
+__device__ __forceinline__ void split3_words(const float (&v)[N], uint32_t (&hi)[N / 2],
+                                             uint32_t (&mid)[N / 2], uint32_t (&lo)[N / 2]) {
+#pragma unroll
+  for (int e = 0; e < N / 2; ++e) split3_bf16x2(v[2 * e], v[2 * e + 1], hi[e], mid[e], lo[e]);
+}
+
 // Writes N consecutive channels c .. c + N - 1 (within one 8-channel group) of row m.
 template <int N>
 __device__ __forceinline__ void frag_store(__bf16* xf, int m, int c, int nblk, const float (&v)[N]) {
   static_assert(N == 2 || N == 4 || N == 8, "frag_store: 2, 4 or 8 channels");
-  typedef __bf16 bfN __attribute__((ext_vector_type(N)));
-  bfN hi, mid, lo;
-#pragma unroll
-  for (int e = 0; e < N; ++e) {
-    __bf16 h, md, l;
-    split3_bf16(v[e], h, md, l);
-    hi[e] = h;
-    mid[e] = md;
-    lo[e] = l;
-  }
+  uint32_t h[N / 2], md[N / 2], l[N / 2];
+  split3_words<N>(v, h, md, l);
   __bf16* p = xf + frag_offset(m, c, nblk);
-  *reinterpret_cast<bfN*>(p) = hi;
-  *reinterpret_cast<bfN*>(p + kFragElems) = mid;
-  *reinterpret_cast<bfN*>(p + 2 * kFragElems) = lo;
+  if constexpr (N == 2) {
+    *reinterpret_cast<uint32_t*>(p) = h[0];
+    *reinterpret_cast<uint32_t*>(p + kFragElems) = md[0];
+    *reinterpret_cast<uint32_t*>(p + 2 * kFragElems) = l[0];
+  } else {
+    typedef uint32_t uN __attribute__((ext_vector_type(N / 2)));
+    uN hv, mv, lv;
+#pragma unroll
+    for (int e = 0; e < N / 2; ++e) {
+      hv[e] = h[e];
+      mv[e] = md[e];
+      lv[e] = l[e];
+    }
+    *reinterpret_cast<uN*>(p) = hv;
+    *reinterpret_cast<uN*>(p + kFragElems) = mv;
+    *reinterpret_cast<uN*>(p + 2 * kFragElems) = lv;
+  }
 }
 
 // Pairwise tree of N consecutive values in index order (the first levels of a block sum).
 template <int N>
 __device__ __forceinline__ float tree_sum(const float (&v)[N]) {
+#pragma clang fp contract(off)
   if constexpr (N == 2) {
     return v[0] + v[1];
   } else if constexpr (N == 4) {
