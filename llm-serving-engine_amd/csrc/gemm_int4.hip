@@ -1014,14 +1014,15 @@ extern "C" int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* pa
 }
 
 // K planes for a decode-batch linear on fragments: enough that the slab tiles of all planes
-// give every CU a workgroup, with at least 4 blocks of K per plane; 1 when the slabs alone fill
-// the GPU (qkv, gate_up at Qwen3-0.6B shapes). o_proj and down_proj at 64 rows (N = 1024: 64
-// slab tiles) take 4.
+// give half the CUs a workgroup, with at least 4 blocks of K per plane; 1 when the slabs alone
+// do (qkv, gate_up at Qwen3-0.6B shapes). o_proj and down_proj at 64 rows (N = 1024: 64 slab
+// tiles) take 2: the residual norm that adds the planes reads each of them, and the config-5
+// step is faster with 2 than with 4 (17.99 k against 17.6 k tok/s) or 1 (17.4 k).
 extern "C" int64_t llmserve_int4_xfrag_splits(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K < kBlk) return 1;
   const int64_t tiles = pk_slabs(N) * ((M + kRows - 1) / kRows), nb = K / kBlk;
   int64_t P = 1;
-  while (P < kMaxPlanes && tiles * P < 256 && nb >= 4 * 2 * P) P *= 2;
+  while (P < kMaxPlanes && tiles * P < 128 && nb >= 4 * 2 * P) P *= 2;
   return P;
 }
 
