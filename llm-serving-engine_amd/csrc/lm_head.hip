@@ -52,15 +52,17 @@ struct LmArgs {
 // ~2^-26).
 __device__ __forceinline__ void split_w(const u32x4& p0, const u32x4& p1, bf16x8& hi, bf16x8& mid,
                                         bf16x8& lo) {
+  float v[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float v = __builtin_bit_cast(float, e < 4 ? p0[e] : p1[e - 4]);
-    __bf16 h, m, l;
-    lsh::split3_bf16(v, h, m, l);
-    hi[e] = h;
-    mid[e] = m;
-    lo[e] = l;
+    const uint32_t u = e < 4 ? p0[e] : p1[e - 4];
+    v[e] = __builtin_bit_cast(float, u);
   }
+  uint32_t h[4], m[4], l[4];
+  lsh::split3_words<8>(v, h, m, l);  // two channels per packed conversion
+  hi = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
+  mid = __builtin_bit_cast(bf16x8, u32x4{m[0], m[1], m[2], m[3]});
+  lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
 }
 
 // T: row tiles of this pass (blockIdx.y selects which). Workgroup g runs the vocab tiles
