@@ -738,16 +738,20 @@ void launch_x(const Int4GemmXArgs& a, int64_t slabs, hipStream_t st) {
 // against 319).
 // S = one_block_waves(nb) (idle wavefronts of a last round would still convert x): K = 3072
 // (24 blocks) takes two rounds of 12, 16 rows 292 -> 302 GB/s.
-void launch_x_tile(const Int4GemmXArgs& a, int64_t slabs, int nb, hipStream_t st) {
+// Returns false (nothing launched) for a configuration without an instance.
+bool launch_x_tile(const Int4GemmXArgs& a, int64_t slabs, int nb, hipStream_t st) {
   const int S = one_block_waves(nb);
   const int NT = slabs * kNT <= 512 ? 1 : 2;
   const bool co = a.M > 8;
-#define LSH_X(s, nt)                                            \
-  if (S == s && NT == nt)                                       \
-    return co ? launch_x<s, nt, true>(a, slabs, st) : launch_x<s, nt, false>(a, slabs, st);
+#define LSH_X(s, nt)                                                                        \
+  if (S == s && NT == nt) {                                                                 \
+    co ? launch_x<s, nt, true>(a, slabs, st) : launch_x<s, nt, false>(a, slabs, st);        \
+    return true;                                                                            \
+  }
   LSH_X(4, 1) LSH_X(4, 2) LSH_X(8, 1) LSH_X(8, 2) LSH_X(12, 1) LSH_X(12, 2) LSH_X(16, 1)
   LSH_X(16, 2)
 #undef LSH_X
+  return false;
 }
 
 int64_t xsum_rows(int64_t M) { return (M + kRows - 1) / kRows * kRows; }
@@ -768,7 +772,8 @@ void launch_lat_ks(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int pla
 // then the fewest of 1, 2, 4, 8
 // wavefronts that cover the nb blocks (8 when more than one round is needed); the exceptions
 // below.
-void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all, hipStream_t st,
+// Returns false (nothing launched) for a configuration without an instance.
+bool launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all, hipStream_t st,
                 int planes = 1) {
   // very wide outputs (at least 256 slabs) with K = 512 or 1024: int4_gemm_wide, about two
   // workgroups per CU
@@ -789,7 +794,7 @@ void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all
     else
       lsh::launch(int4_gemm_wide<4>, grid, dim3(4 * kWave), 0, st, true, a, static_cast<int>(mtiles),
                   static_cast<int>(groups));
-    return;
+    return true;
   }
   const int bpp = (nb_all + planes - 1) / planes;  // blocks per plane
   const int nb = bpp;
@@ -809,11 +814,15 @@ void launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all
     KB = 2;
     S = 4;
   }
-#define LSH_LAT(kb, s) \
-  if (KB == kb && S == s) return launch_lat_ks<kb, s>(a, slabs, mtiles, planes, bpp, st);
+#define LSH_LAT(kb, s)                                              \
+  if (KB == kb && S == s) {                                         \
+    launch_lat_ks<kb, s>(a, slabs, mtiles, planes, bpp, st);        \
+    return true;                                                    \
+  }
   LSH_LAT(1, 1) LSH_LAT(1, 2) LSH_LAT(1, 4) LSH_LAT(1, 8)
   LSH_LAT(2, 4) LSH_LAT(2, 8) LSH_LAT(1, 12) LSH_LAT(1, 16)
 #undef LSH_LAT
+  return false;
 }
 
 }  // namespace
@@ -949,7 +958,8 @@ extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv
                      reinterpret_cast<const float*>(wpk0 + (pk_weight_bytes(N, K) + 255) / 256 * 256),
                      y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
                      static_cast<int>(group_size / kBlk)};
-    launch_x_tile(xa, pk_slabs(N), nb, st);
+    LSH_CHECK(launch_x_tile(xa, pk_slabs(N), nb, st),
+              "int4_linear_gemm_packed: no kernel instance for K=%lld", (long long)K);
     return lsh::launch_status("int4_linear_gemm_packed");
   }
   __bf16* xf = static_cast<__bf16*>(workspace);
@@ -961,7 +971,9 @@ extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv
   Int4GemmArgs a{xf, nullptr, xsum, wpk, spk, nullptr, y, static_cast<int>(M),
                  static_cast<int>(N), static_cast<int>(K), static_cast<int>(K / group_size),
                  static_cast<int>(group_size / kBlk), mp};
-  launch_lat(a, pk_slabs(N), mtiles, nb, st);
+  LSH_CHECK(launch_lat(a, pk_slabs(N), mtiles, nb, st),
+            "int4_linear_gemm_packed: no kernel instance for M=%lld K=%lld", (long long)M,
+            (long long)K);
   return lsh::launch_status("int4_linear_gemm_packed");
 }
 
@@ -1009,7 +1021,9 @@ extern "C" int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* pa
   Int4GemmArgs a{xf, nullptr, xsum, wpk, spk, nullptr, y, static_cast<int>(M),
                  static_cast<int>(N), static_cast<int>(K), static_cast<int>(K / group_size),
                  static_cast<int>(group_size / kBlk), mp};
-  launch_lat(a, pk_slabs(N), mtiles, nb, lsh::as_stream(stream));
+  LSH_CHECK(launch_lat(a, pk_slabs(N), mtiles, nb, lsh::as_stream(stream)),
+            "int4_linear_gemm_xfrag: no kernel instance for M=%lld K=%lld", (long long)M,
+            (long long)K);
   return lsh::launch_status("int4_linear_gemm_xfrag");
 }
 
@@ -1054,6 +1068,8 @@ extern "C" int llmserve_int4_linear_gemm_xfrag_split(const void* xfrag, const vo
   Int4GemmArgs a{xf, nullptr, xsum, wpk, spk, nullptr, y, static_cast<int>(M),
                  static_cast<int>(N), static_cast<int>(K), static_cast<int>(K / group_size),
                  static_cast<int>(group_size / kBlk), mp};
-  launch_lat(a, pk_slabs(N), mtiles, nb, lsh::as_stream(stream), static_cast<int>(splits));
+  LSH_CHECK(launch_lat(a, pk_slabs(N), mtiles, nb, lsh::as_stream(stream), static_cast<int>(splits)),
+            "int4_linear_gemm_xfrag_split: no kernel instance for M=%lld K=%lld", (long long)M,
+            (long long)K);
   return lsh::launch_status("int4_linear_gemm_xfrag_split");
 }
