@@ -812,14 +812,16 @@ def profile_only(torch, dev, what: str) -> int:
     """64 launches of one kernel, for rocprofv3 counter runs (no timing output)."""
     from llmserve.kernels import load_int8_gemv, load_paged_attention, load_quant
 
-    if what == "gemv":  # the four int4 g128 GEMV shapes at M = 1, then config 1's int8 GEMV
+    if what in ("gemv", "gemv4"):  # the four int4 g128 GEMV shapes at M = 1 (4), then config
+        # 1's int8 GEMV
         g = torch.Generator(device=dev).manual_seed(3)
         gemv = load_int8_gemv()
+        rows = 4 if what == "gemv4" else 1
         for name, (N, K) in SHAPES.items():  # 64 distinct weights each (~0.6 GB in all)
             lins = [load_quant().int4_quantize(torch.randn(N, K, device=dev, generator=g) * 0.02,
                                                GROUP, torch.rand(K, device=dev, generator=g) + 0.5)
                     for _ in range(64)]
-            x = torch.randn(1, K, device=dev, generator=g)
+            x = torch.randn(rows, K, device=dev, generator=g)
             for i in range(64):
                 nib, gs, gz, inv = lins[i]
                 gemv.int4_linear(x, nib, gs, gz, GROUP, inv)
@@ -827,7 +829,7 @@ def profile_only(torch, dev, what: str) -> int:
         N, K = 6144, 1024
         qs = [load_quant().int8_quantize(torch.randn(N, K, device=dev, generator=g) * 0.02)
               for _ in range(64)]
-        x = torch.randn(1, K, device=dev, generator=g)
+        x = torch.randn(rows, K, device=dev, generator=g)
         for i in range(64):
             gemv.int8_linear(x, *qs[i])
     elif what == "prefill":  # config 3 gate_up: M = 2048, 2048 -> 16384
@@ -908,7 +910,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
-    ap.add_argument("--only", choices=["gemv", "gemm4", "gemm16", "attention", "prefill",
+    ap.add_argument("--only", choices=["gemv", "gemv4", "gemm4", "gemm16", "attention", "prefill",
                                        "lmhead", "copy",
                                        "c5step", "c5step1"],
                     help="profiling run: only launch that kernel (64 times) and exit")

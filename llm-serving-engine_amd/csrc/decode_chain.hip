@@ -34,7 +34,7 @@
 //
 // Layouts: int4 weights are the reference buffers (nibbles [N, K/2], even channel low;
 // group scale / zero [N, K/128]); x' = x * inv_act_scale is staged in LDS with each
-// 32-channel slice's eight 16-byte chunks rotated by the slice index (conflict-free
+// 32-channel slice's eight 16-byte chunks rotated by half the slice index (conflict-free
 // ds_read_b128); a lane holds 16-byte weight chunks (32 channels of one group) and computes
 // s * sum x'q + (z - 8 s) * sum x' (int8_gemv.cpp:48-52), partial sums reduced with DPP.
 #include <cmath>
@@ -215,11 +215,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t replica(const uint64_t* base, 
 // ---- staging and dot products ------------------------------------------------------------------
 
 // LDS offset of channel k of a staged row: 32-channel slice sl = k / 32 keeps its eight
-// 16-byte chunks rotated by sl, so the 16 lanes of a ds_read_b128 phase, reading chunk j of
-// consecutive slices, hit 16 distinct bank groups. Channels 2p and 2p + 1 stay adjacent.
+// 16-byte chunks rotated by sl / 2 (the two slices of a 256-byte LDS row share a rotation),
+// which SQ_LDS_BANK_CONFLICT shows conflict-free for a wavefront reading chunk j of
+// consecutive slices on gfx950 (a rotation by sl costs 4 conflict cycles per ds_read_b128).
+// Channels 2p and 2p + 1 stay adjacent.
+__device__ __forceinline__ int chunk_rot(int sl) { return sl >> 1; }
 __device__ __forceinline__ int xoff(int k) {
   const int sl = k >> 5, j = (k >> 2) & 7;
-  return (sl << 5) + (((j + sl) & 7) << 2) + (k & 3);
+  return (sl << 5) + (((j + chunk_rot(sl)) & 7) << 2) + (k & 3);
 }
 
 __device__ __forceinline__ float4 lds4(const float* p) {
@@ -276,7 +279,7 @@ __device__ __forceinline__ void chunk_terms(const Chunk& f, int c, const float* 
     float d = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float4 x = lds4(row + (((j + c) & 7) << 2));
+      const float4 x = lds4(row + (((j + chunk_rot(c)) & 7) << 2));
       d += x.x * q[4 * j] + x.y * q[4 * j + 1] + x.z * q[4 * j + 2] + x.w * q[4 * j + 3];
     }
     v[m] = f.on ? f.s * d + f.zc * cs[m * (K >> 5) + c] : 0.f;

@@ -13,8 +13,9 @@
 // way into LDS. Two LDS buffers: the global loads of stage s + 1 are in flight (in registers)
 // while the 128 MFMAs per wavefront of stage s run from LDS, then go to the other buffer.
 // LDS rows are 128 bytes (eight 16-byte chunks); chunk c of row r sits at position
-// c ^ (r & 7) ^ ((r >> 3) & 1): the 16 rows of one ds_read_b128 fragment load then fall on
-// distinct banks whether the LDS serves 8 lanes from 32 banks or 16 lanes from 64 banks.
+// c ^ (r & 7). Measured with SQ_LDS_BANK_CONFLICT on gfx950, the fragment loads (16 rows x
+// 4 chunks per ds_read_b128) and both stage stores are then conflict-free; with a further
+// ^ ((r >> 3) & 1) each fragment load costs 4 conflict cycles.
 // MFMA operands (16x16x32 bf16): lane l supplies row l % 16 of the A tile and column l % 16
 // of the B tile, k = 8 (l / 16) .. + 8; the result lane l holds rows 4 (l / 16) + r, column
 // l % 16.
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(256) void x_to_bf16(const float* __restrict__ x, __
 }
 
 __device__ __forceinline__ int swz(int row, int chunk) {
-  return chunk ^ (row & 7) ^ ((row >> 3) & 1);
+  return chunk ^ (row & 7);
 }
 
 // 16 int8 -> 16 bf16 (two 16-byte chunks), exact.

@@ -14,8 +14,8 @@
 //    global->LDS loads (global_load_lds_dwordx4: every load of the stage is in flight at once,
 //    none passes through VGPRs); the int4 AWQ pre-scale x * inv_act_scale is applied in LDS
 //    after they land. The 16-byte chunks of each slice are stored rotated by a function of
-//    the slice index, so the lanes of one ds_read_b128 phase (8 or 16 of them, reading the
-//    same chunk of consecutive slices) hit distinct banks on a 32- or a 64-bank LDS;
+//    the slice index (chunk_pos), so that a wavefront reading the same chunk of consecutive
+//    slices has no LDS bank conflict;
 //  * a lane unpacks its RPL weight slices once and reuses each x value it reads from LDS
 //    for RPL rows (register blocking for M > 2);
 //  * the LPR partial sums of a row are reduced with DPP only (butterflies within 16-lane
@@ -85,12 +85,16 @@ __device__ __forceinline__ void lds_st4(float* p, float4 v) {
   *static_cast<float4*>(__builtin_assume_aligned(p, 16)) = v;
 }
 
-// Position of chunk c (16 bytes = 4 channels) of slice `sl` within the slice: the chunks of
-// slice sl are rotated by sl + sl/8 (int4, 8 chunks) or sl/2 + sl/8 (int8, 4 chunks), so that
-// any 8 or 16 consecutive slices read at the same c land on distinct 16-byte bank groups.
+// Position of chunk c (16 bytes = 4 channels) of slice `sl` within the slice: the slices of
+// one 256-byte LDS row (2 int4 slices of 8 chunks, 4 int8 slices of 4 chunks) share a
+// rotation and consecutive rows rotate by one chunk, rot = sl / 2 (int4) or sl / 4 (int8).
+// Measured with SQ_LDS_BANK_CONFLICT on gfx950: a wavefront reading chunk c of 32 or 64
+// consecutive slices this way has no bank conflict; rotating every slice by one more chunk
+// (sl + sl / 8, sl / 2 + sl / 8) costs 4 conflict cycles per ds_read_b128. The staging
+// stores are conflict-free either way.
 template <int CPC>
 __device__ __forceinline__ int chunk_pos(int sl, int c) {
-  const int rot = CPC == 8 ? sl + (sl >> 3) : (sl >> 1) + (sl >> 3);
+  const int rot = CPC == 8 ? sl >> 1 : sl >> 2;
   return (c + rot) & (CPC - 1);
 }
 
