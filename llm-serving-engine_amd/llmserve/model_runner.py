@@ -78,6 +78,14 @@ class ModelRunner:
                 raise IndexError(f"index_copy_(): block {bad} (slots {bad * bs}..{bad * bs + bs - 1})"
                                  f" is out of bounds for a cache of {slots} slots")
 
+    @staticmethod
+    def _check_ids(ids, vocab: int) -> None:
+        """Token ids must index the embedding. The reference's ``nn.Embedding`` raises on one
+        outside [0, vocab); the native gather writes a NaN row instead, so the host checks the
+        ids it already holds and raises as torch does."""
+        if ids and (min(ids) < 0 or max(ids) >= vocab):
+            raise IndexError("index out of range in self")
+
     def _decode_step_ok(self, q_lens: list[int], logit_rows: list[int]) -> bool:
         m = self.model
         return (self.fused_decode and isinstance(m, QuantCausalLM)
@@ -115,6 +123,7 @@ class ModelRunner:
             rows += range(last[i] - k + 1, last[i] + 1)
         self._check_tables(tables, ctx_lens)
         m = self.model
+        self._check_ids(ids, m.cfg.vocab_size)
         # The forward always runs, also when no row is sampled: a step made only of non-final
         # prompt chunks (chunked prefill) writes its K/V here and samples nothing.
         if self._decode_step_ok(q_lens, rows):

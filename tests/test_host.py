@@ -341,6 +341,19 @@ def test_model_runner_rejects_blocks_past_the_cache():
         r._check_tables([[1], [-1]], [3, 3])
 
 
+def test_model_runner_rejects_token_ids_outside_the_vocabulary():
+    """A token id outside [0, vocab) raises on the host, as the reference's embedding does
+    (the native gather would write a NaN row)."""
+    from llmserve.model_runner import ModelRunner
+
+    ModelRunner._check_ids([0, 5, 99], 100)
+    ModelRunner._check_ids([], 100)
+    with pytest.raises(IndexError, match="index out of range"):
+        ModelRunner._check_ids([3, 100], 100)
+    with pytest.raises(IndexError, match="index out of range"):
+        ModelRunner._check_ids([-1], 100)
+
+
 _STUB_KERNELS = '''"""Stub laid out as the reference's src/llmserve/kernels/__init__.py (its imports, logger,
 csrc path and functools-cached JIT loaders that return a module or None)."""
 
