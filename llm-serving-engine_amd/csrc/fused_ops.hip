@@ -279,11 +279,23 @@ __global__ __launch_bounds__(kRowThreads) void argmax_parts_kernel(const float* 
   const float* row = logits + t * V;
   float best = -__builtin_inff();
   int64_t idx = V;  // none
-  for (int64_t i = lo + threadIdx.x; i < hi; i += kRowThreads) {
-    const float x = row[i];
-    if (arg_above(x, best)) {  // strictly above: the first index of equal values stays
-      best = x;
-      idx = i;
+  // kArgUnroll loads (clamped into the range, so that all of them go out before the first
+  // compare) per round: one memory round trip per round rather than one per element
+  constexpr int kArgUnroll = 16;
+  for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += kArgUnroll * kRowThreads) {
+    float x[kArgUnroll];
+#pragma unroll
+    for (int u = 0; u < kArgUnroll; ++u) {
+      const int64_t i = i0 + static_cast<int64_t>(u) * kRowThreads;
+      x[u] = row[i < hi ? i : hi - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < kArgUnroll; ++u) {
+      const int64_t i = i0 + static_cast<int64_t>(u) * kRowThreads;
+      if (i < hi && arg_above(x[u], best)) {  // strictly above: the first index of equal values stays
+        best = x[u];
+        idx = i;
+      }
     }
   }
 #pragma unroll

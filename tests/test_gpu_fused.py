@@ -145,16 +145,17 @@ def test_argmax_advance(gpu):
     logits[3, 0] = 60.0
     logits[4, 12345] = logits[4, 99999] = np.nan
     logits[5] = -np.inf
+    logits[6, 5000] = logits[6, 5256] = 70.0  # a tie inside one thread's unrolled loads
     ctx = np.arange(5, 5 + T, dtype=np.int64)
     c = cu.dev(ctx)
     ids = fo().argmax_advance(cu.dev(logits), c).cpu().numpy()
     want = torch.from_numpy(logits).argmax(-1).numpy()
     assert np.array_equal(ids, want)
-    assert ids[1] == 77 and ids[4] == 12345 and ids[5] == 0
+    assert ids[1] == 77 and ids[4] == 12345 and ids[5] == 0 and ids[6] == 5000
     assert np.array_equal(c.cpu().numpy(), ctx + 1)
 
 
-@pytest.mark.parametrize("V", [1, 31, 1000])
+@pytest.mark.parametrize("V", [1, 31, 1000, 40000])
 def test_argmax_small_vocab(gpu, V):
     rng = np.random.default_rng(V)
     logits = rng.integers(-3, 3, (4, V)).astype(F32)  # many ties
