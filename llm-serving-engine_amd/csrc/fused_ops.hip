@@ -9,6 +9,8 @@
 //    temperature 0) that also advances each sequence's context length by the new token.
 // The reference's sum-of-squares loops are OpenMP simd reductions (any order); here they are
 // trees over the wavefront / workgroup in a fixed order.
+#include <initializer_list>
+
 #include "common.h"
 #include "kv_quant.h"
 #include "rope.h"
@@ -62,11 +64,136 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(float* __restrict_
     if (MODE == kNormAdd) v += r[t * H + i];
     if (MODE == kNormGather && bad) v = __builtin_nanf("");
     if (MODE != kNormPlain) xr[i] = v;
-    ss += v * v;
+    ss = __builtin_fmaf(v, v, ss);
   }
   ss = block_sum(ss, red);
   const float inv = 1.f / sqrtf(ss / static_cast<float>(H) + eps);
   for (int64_t i = threadIdx.x; i < H; i += kRowThreads) orow[i] = w[i] * (xr[i] * inv);
+}
+
+// The norms above, vectorized (rows of H % 4 == 0 channels, 16-byte aligned, H <= 4 * 256 * NC):
+// thread i holds channels 4 (i + 256 j) .. + 4, j < NC, in registers from the loads to the
+// output, and every load of the row (x or the embedding row, the residual's PL planes, w and
+// act_inv) is issued before the first use, so the row costs one memory round trip instead of
+// one per channel group and plane. The arithmetic per channel is rmsnorm_kernel's (planes
+// added in order, then to x); the sum of squares runs over the thread's channels in index
+// order, then block_sum.
+constexpr int kNormChunk = 4 * kRowThreads;  // channels per round of the threads (1024)
+constexpr int kNormMaxH = 4 * kNormChunk;     // rows the vectorized norms take (NC <= 4)
+
+constexpr int kPlaneGroup = 4;  // residual planes loaded together
+
+template <int MODE, int NC>
+__device__ __forceinline__ float norm_vec_pass(float* xr, const float* src, const float* rrow,
+                                               int64_t pstride, int planes, bool bad,
+                                               const float* w, const float* act, int H,
+                                               float4 (&v)[NC], float4 (&wv)[NC],
+                                               float4 (&av)[NC], bool (&on)[NC]) {
+  const int n4 = H / 4;
+  int cc[NC];
+  float4 rp[NC][kPlaneGroup];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = static_cast<int>(threadIdx.x) + kRowThreads * j;
+    on[j] = c < n4;
+    cc[j] = on[j] ? c : n4 - 1;  // clamped: the loads stay unconditional
+    v[j] = reinterpret_cast<const float4*>(src)[cc[j]];
+    wv[j] = reinterpret_cast<const float4*>(w)[cc[j]];
+    av[j] = reinterpret_cast<const float4*>(act ? act : w)[cc[j]];  // act null: unused
+    if constexpr (MODE == kNormAdd) {
+#pragma unroll
+      for (int q = 0; q < kPlaneGroup; ++q)  // planes past the last repeat it (not added)
+        rp[j][q] = reinterpret_cast<const float4*>(
+            rrow + static_cast<int64_t>(q < planes ? q : planes - 1) * pstride)[cc[j]];
+    }
+  }
+  float4 rs[NC];
+  if constexpr (MODE == kNormAdd) {
+    auto add4 = [](float4& a, const float4& b) {
+      a.x += b.x;
+      a.y += b.y;
+      a.z += b.z;
+      a.w += b.w;
+    };
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      rs[j] = rp[j][0];
+#pragma unroll
+      for (int q = 1; q < kPlaneGroup; ++q)
+        if (q < planes) add4(rs[j], rp[j][q]);
+    }
+    for (int p0 = kPlaneGroup; p0 < planes; p0 += kPlaneGroup) {  // more than 4 planes
+#pragma unroll
+      for (int j = 0; j < NC; ++j)
+#pragma unroll
+        for (int q = 0; q < kPlaneGroup; ++q)
+          rp[j][q] = reinterpret_cast<const float4*>(
+              rrow + static_cast<int64_t>(p0 + q < planes ? p0 + q : planes - 1) * pstride)[cc[j]];
+#pragma unroll
+      for (int j = 0; j < NC; ++j)
+#pragma unroll
+        for (int q = 0; q < kPlaneGroup; ++q)
+          if (p0 + q < planes) add4(rs[j], rp[j][q]);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    float4 x = v[j];
+    if constexpr (MODE == kNormAdd) {
+      x.x += rs[j].x;
+      x.y += rs[j].y;
+      x.z += rs[j].z;
+      x.w += rs[j].w;
+    }
+    if (MODE == kNormGather && bad) {
+      const float nan = __builtin_nanf("");
+      x = make_float4(nan, nan, nan, nan);
+    }
+    v[j] = x;
+    if (on[j]) {
+      if constexpr (MODE != kNormPlain)
+        reinterpret_cast<float4*>(xr)[threadIdx.x + kRowThreads * j] = x;
+      ss = __builtin_fmaf(x.x, x.x, ss);  // explicit fmas: the order cannot be contracted
+      ss = __builtin_fmaf(x.y, x.y, ss);  // differently in the kernels that share this pass
+      ss = __builtin_fmaf(x.z, x.z, ss);
+      ss = __builtin_fmaf(x.w, x.w, ss);
+    }
+  }
+  return ss;
+}
+
+template <int MODE, int NC>
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_vec_kernel(float* __restrict__ x,
+                                                                  const float* __restrict__ r,
+                                                                  const int64_t* __restrict__ ids,
+                                                                  int64_t V,
+                                                                  const float* __restrict__ w,
+                                                                  float* __restrict__ out, int H,
+                                                                  float eps) {
+  __shared__ float red[kRowThreads / kWave];
+  const int64_t t = blockIdx.x;
+  float* xr = x + t * H;
+  const float* src = xr;
+  const float* rrow = r ? r + t * H : nullptr;
+  bool bad = false;
+  if (MODE == kNormGather) {
+    const int64_t id = ids[t];
+    bad = id < 0 || id >= V;
+    src = r + (bad ? 0 : id) * H;
+  }
+  float4 v[NC], wv[NC], av[NC];
+  bool on[NC];
+  float ss = norm_vec_pass<MODE, NC>(xr, src, rrow, 0, 1, bad, w, nullptr, H, v, wv, av, on);
+  ss = block_sum(ss, red);
+  const float inv = 1.f / sqrtf(ss / static_cast<float>(H) + eps);
+  float4* orow = reinterpret_cast<float4*>(out + t * H);
+#pragma unroll
+  for (int j = 0; j < NC; ++j)
+    if (on[j])
+      orow[threadIdx.x + kRowThreads * j] =
+          make_float4(wv[j].x * (v[j].x * inv), wv[j].y * (v[j].y * inv), wv[j].z * (v[j].z * inv),
+                      wv[j].w * (v[j].w * inv));
 }
 
 // out[t, i] = silu(gate) * up = gate / (1 + exp(-gate)) * up for a fused [T, 2I] gate|up row
@@ -83,16 +210,11 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_kernel(const float* __re
   }
 }
 
-// The norms above with the int4 linear's activation fragments as output (xfrag.h): the
-// first pass is rmsnorm_kernel's (same x update, same sum of squares, same inv); the second
-// computes h = w * (x * inv) as rmsnorm_kernel does, x' = h * act_inv (the next linear's AWQ
-// pre-scale, or h) and writes x' as bf16 hi / mid / lo fragments and block sums, with 4 consecutive
-// channels per thread (32 threads per 128-channel block). One workgroup per fragment row:
-// rows past T write zeros. H is a multiple of 128. The residual r may come as `planes` partial
-// sums [planes, T, H] (a K-split linear's output planes): they are added in plane order, then
-// to x.
+// rmsnorm_kernel's arithmetic with the fragments as output, one channel per thread and
+// round: the form for rows that rmsnorm_frag_kernel does not take (H above kNormMaxH or
+// unaligned rows). Same x update, same sum of squares and inv as rmsnorm_kernel.
 template <int MODE>
-__global__ __launch_bounds__(kRowThreads) void rmsnorm_frag_kernel(
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_frag_scalar_kernel(
     float* __restrict__ x, const float* __restrict__ r, const int64_t* __restrict__ ids, int64_t V,
     const float* __restrict__ w, const float* __restrict__ act_inv, __bf16* __restrict__ xf,
     float* __restrict__ xsum, int T, int H, int mp, float eps, int planes) {
@@ -126,7 +248,7 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_frag_kernel(
     }
     if (MODE == kNormGather && bad) v = __builtin_nanf("");
     if (MODE != kNormPlain) xr[i] = v;
-    ss += v * v;
+    ss = __builtin_fmaf(v, v, ss);
   }
   ss = block_sum(ss, red);  // its barriers also order the x writes above before the reads below
   const float inv = 1.f / sqrtf(ss / static_cast<float>(H) + eps);
@@ -139,6 +261,64 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_frag_kernel(
     }
     lsh::frag_store<4>(xf, t, c0, nblk, v);
     const float sblk = lsh::group_sum<32>(lsh::tree_sum<4>(v));
+    if (threadIdx.x % 32 == 0) xsum[static_cast<int64_t>(c0 / lsh::kFragBlk) * mp + t] = sblk;
+  }
+}
+
+// The norms above with the int4 linear's activation fragments as output (xfrag.h): the
+// first pass is rmsnorm_vec_kernel's (norm_vec_pass: same x update, same sum of squares, same
+// inv); the second computes h = w * (x * inv) as it does, x' = h * act_inv (the next linear's
+// AWQ pre-scale, or h) and writes x' as bf16 hi / mid / lo fragments and block sums, with 4
+// consecutive channels per thread (32 threads per 128-channel block). One workgroup per
+// fragment row: rows past T write zeros. H is a multiple of 128, at most 1024 NC. The residual
+// r may come as `planes` partial sums [planes, T, H] (a K-split linear's output planes): they
+// are added in plane order, then to x.
+template <int MODE, int NC>
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_frag_kernel(
+    float* __restrict__ x, const float* __restrict__ r, const int64_t* __restrict__ ids, int64_t V,
+    const float* __restrict__ w, const float* __restrict__ act_inv, __bf16* __restrict__ xf,
+    float* __restrict__ xsum, int T, int H, int mp, float eps, int planes) {
+  __shared__ float red[kRowThreads / kWave];
+  const int t = blockIdx.x;
+  const int nblk = H / lsh::kFragBlk;
+  if (t >= T) {  // padding row of the last 16-row tile
+    for (int c0 = 4 * threadIdx.x; c0 < H; c0 += 4 * kRowThreads) {
+      const float z[4] = {0.f, 0.f, 0.f, 0.f};
+      lsh::frag_store<4>(xf, t, c0, nblk, z);
+      if (threadIdx.x % 32 == 0) xsum[static_cast<int64_t>(c0 / lsh::kFragBlk) * mp + t] = 0.f;
+    }
+    return;
+  }
+  float* xr = x + static_cast<int64_t>(t) * H;
+  const float* src = xr;
+  const float* rrow = r ? r + static_cast<int64_t>(t) * H : nullptr;
+  bool bad = false;
+  if (MODE == kNormGather) {
+    const int64_t id = ids[t];
+    bad = id < 0 || id >= V;
+    src = r + (bad ? 0 : id) * H;
+  }
+  float4 v[NC], wv[NC], av[NC];
+  bool on[NC];
+  float ss = norm_vec_pass<MODE, NC>(xr, src, rrow, static_cast<int64_t>(T) * H, planes, bad, w,
+                                      act_inv, H, v, wv, av, on);
+  ss = block_sum(ss, red);
+  const float inv = 1.f / sqrtf(ss / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    if (!on[j]) continue;  // H % 128 == 0: whole 32-lane groups agree
+    const int c0 = 4 * (static_cast<int>(threadIdx.x) + kRowThreads * j);
+    const float hx[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    const float wx[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+    const float ax[4] = {av[j].x, av[j].y, av[j].z, av[j].w};
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float h = wx[e] * (hx[e] * inv);
+      o[e] = act_inv ? __fmul_rn(h, ax[e]) : h;
+    }
+    lsh::frag_store<4>(xf, t, c0, nblk, o);
+    const float sblk = lsh::group_sum<32>(lsh::tree_sum<4>(o));
     if (threadIdx.x % 32 == 0) xsum[static_cast<int64_t>(c0 / lsh::kFragBlk) * mp + t] = sblk;
   }
 }
@@ -348,6 +528,35 @@ int launch_rope(const RopeArgs& a, hipStream_t st) {
   return LLMSERVE_OK;
 }
 
+// The vectorized norms take rows of H % 4 == 0 channels up to kNormMaxH with 16-byte aligned
+// pointers (thread chunks of 4 channels); anything else runs the one-channel-per-thread form.
+// Both forms of a norm with fragments and without agree bit for bit for the same rows.
+bool norm_vec_ok(int64_t H, std::initializer_list<const void*> ptrs) {
+  if (H % 4 != 0 || H > kNormMaxH) return false;
+  for (const void* p : ptrs)
+    if (p != nullptr && !lsh::aligned16(p)) return false;
+  return true;
+}
+
+// the chunk count (template NC) of the vectorized norms for H <= kNormMaxH
+int norm_chunks(int64_t H) { return H <= kNormChunk ? 1 : (H <= 2 * kNormChunk ? 2 : 4); }
+
+template <int MODE>
+void launch_norm(float* x, const float* r, const int64_t* ids, int64_t V, const float* w,
+                 float* out, int64_t T, int64_t H, float eps, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(T)), block(kRowThreads);
+  if (!norm_vec_ok(H, {x, r, w, out})) {
+    lsh::launch(rmsnorm_kernel<MODE>, grid, block, 0, st, true, x, r, ids, V, w, out, H, eps);
+    return;
+  }
+  const int Hi = static_cast<int>(H);
+  switch (norm_chunks(H)) {
+    case 1: lsh::launch(rmsnorm_vec_kernel<MODE, 1>, grid, block, 0, st, true, x, r, ids, V, w, out, Hi, eps); break;
+    case 2: lsh::launch(rmsnorm_vec_kernel<MODE, 2>, grid, block, 0, st, true, x, r, ids, V, w, out, Hi, eps); break;
+    default: lsh::launch(rmsnorm_vec_kernel<MODE, 4>, grid, block, 0, st, true, x, r, ids, V, w, out, Hi, eps); break;
+  }
+}
+
 bool head_dim_ok(int64_t D) { return D == 16 || D == 32 || D == 64 || D == 128 || D == 256; }
 
 }  // namespace
@@ -358,9 +567,8 @@ extern "C" int llmserve_rmsnorm(const float* x, const float* w, float* out, int6
             (long long)H);
   if (T == 0) return LLMSERVE_OK;
   LSH_CHECK(x && w && out, "rmsnorm: null pointer");
-  lsh::launch(rmsnorm_kernel<kNormPlain>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
-              lsh::as_stream(stream), true, const_cast<float*>(x), nullptr, nullptr, int64_t{0},
-              w, out, H, eps);
+  launch_norm<kNormPlain>(const_cast<float*>(x), nullptr, nullptr, 0, w, out, T, H, eps,
+                          lsh::as_stream(stream));
   return lsh::launch_status("rmsnorm");
 }
 
@@ -370,8 +578,7 @@ extern "C" int llmserve_add_rmsnorm(float* x, const float* r, const float* w, fl
             (long long)T, (long long)H);
   if (T == 0) return LLMSERVE_OK;
   LSH_CHECK(x && r && w && out, "add_rmsnorm: null pointer");
-  lsh::launch(rmsnorm_kernel<kNormAdd>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
-              lsh::as_stream(stream), true, x, r, nullptr, int64_t{0}, w, out, H, eps);
+  launch_norm<kNormAdd>(x, r, nullptr, 0, w, out, T, H, eps, lsh::as_stream(stream));
   return lsh::launch_status("add_rmsnorm");
 }
 
@@ -383,8 +590,7 @@ extern "C" int llmserve_embed_rmsnorm(const int64_t* ids, const float* embed, in
             (long long)V);
   if (T == 0) return LLMSERVE_OK;
   LSH_CHECK(ids && embed && w && x && out, "embed_rmsnorm: null pointer");
-  lsh::launch(rmsnorm_kernel<kNormGather>, dim3(static_cast<unsigned>(T)), dim3(kRowThreads), 0,
-              lsh::as_stream(stream), true, x, embed, ids, V, w, out, H, eps);
+  launch_norm<kNormGather>(x, embed, ids, V, w, out, T, H, eps, lsh::as_stream(stream));
   return lsh::launch_status("embed_rmsnorm");
 }
 
@@ -514,20 +720,40 @@ int launch_norm_frag(int mode, float* x, const float* r, const int64_t* ids, int
   const dim3 grid(static_cast<unsigned>(mp)), block(kRowThreads);
   hipStream_t st = lsh::as_stream(stream);
   const int Ti = static_cast<int>(T), Hi = static_cast<int>(H);
-  switch (mode) {
-    case kNormAdd:
-      lsh::launch(rmsnorm_frag_kernel<kNormAdd>, grid, block, 0, st, true, x, r, ids, V, w, act_inv,
-                  xf, xsum, Ti, Hi, mp, eps, planes);
-      break;
-    case kNormGather:
-      lsh::launch(rmsnorm_frag_kernel<kNormGather>, grid, block, 0, st, true, x, r, ids, V, w,
-                  act_inv, xf, xsum, Ti, Hi, mp, eps, 1);
-      break;
-    default:
-      lsh::launch(rmsnorm_frag_kernel<kNormPlain>, grid, block, 0, st, true, x, r, ids, V, w,
-                  act_inv, xf, xsum, Ti, Hi, mp, eps, 1);
-      break;
+  const int pl = mode == kNormAdd ? planes : 1;
+  if (!norm_vec_ok(H, {x, r, w, act_inv})) {
+    switch (mode) {
+      case kNormAdd:
+        lsh::launch(rmsnorm_frag_scalar_kernel<kNormAdd>, grid, block, 0, st, true, x, r, ids, V, w,
+                    act_inv, xf, xsum, Ti, Hi, mp, eps, pl);
+        break;
+      case kNormGather:
+        lsh::launch(rmsnorm_frag_scalar_kernel<kNormGather>, grid, block, 0, st, true, x, r, ids, V,
+                    w, act_inv, xf, xsum, Ti, Hi, mp, eps, pl);
+        break;
+      default:
+        lsh::launch(rmsnorm_frag_scalar_kernel<kNormPlain>, grid, block, 0, st, true, x, r, ids, V,
+                    w, act_inv, xf, xsum, Ti, Hi, mp, eps, pl);
+        break;
+    }
+    return lsh::launch_status(what);
   }
+#define LSH_NF(m, nc)                                                                          \
+  lsh::launch(rmsnorm_frag_kernel<m, nc>, grid, block, 0, st, true, x, r, ids, V, w, act_inv, xf, \
+              xsum, Ti, Hi, mp, eps, pl)
+#define LSH_NF_MODE(m)                  \
+  switch (norm_chunks(H)) {             \
+    case 1: LSH_NF(m, 1); break;        \
+    case 2: LSH_NF(m, 2); break;        \
+    default: LSH_NF(m, 4); break;       \
+  }
+  switch (mode) {
+    case kNormAdd: LSH_NF_MODE(kNormAdd) break;
+    case kNormGather: LSH_NF_MODE(kNormGather) break;
+    default: LSH_NF_MODE(kNormPlain) break;
+  }
+#undef LSH_NF_MODE
+#undef LSH_NF
   return lsh::launch_status(what);
 }
 

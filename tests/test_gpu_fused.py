@@ -52,6 +52,42 @@ def test_norms(gpu, fg, T, H):
     assert _rel(o, fg[k + "_outadd"]) < 2 * TOL
 
 
+@pytest.mark.parametrize("H", [200, 203, 2048, 3000, 4096, 5000, 5120])
+def test_norm_forms_at_every_row_width(gpu, H):
+    """Each row width's kernel form: rows of H % 4 == 0 channels up to 4096 keep 1, 2 or 4
+    float4 chunks per thread in registers (200 and 3000 leave chunks partly or wholly past the
+    row), anything else (203, 5000, 5120) runs one channel per thread. All of them: x += r is
+    one fp32 add, the embedding row is copied exactly (an id outside the table gives a NaN row),
+    the norm is within TOL of the float64 mathematics, and the fragment-writing form gives the
+    bytes of the split pass over the plain form's output."""
+    f = fo()
+    T, V = 5, 40
+    rng = np.random.default_rng(H)
+    x = rng.standard_normal((T, H)).astype(F32)
+    r = rng.standard_normal((T, H)).astype(F32)
+    w = (1 + 0.1 * rng.standard_normal(H)).astype(F32)
+    assert _rel(f.rmsnorm(cu.dev(x), cu.dev(w), 1e-6), ofo.rmsnorm_f64(x, w, 1e-6)) < TOL
+    xd = cu.dev(x)
+    out = f.add_rmsnorm_(xd, cu.dev(r), cu.dev(w), 1e-6)
+    assert np.array_equal(xd.cpu().numpy(), x + r)
+    assert _rel(out, ofo.rmsnorm_f64(x + r, w, 1e-6)) < TOL
+    emb = rng.standard_normal((V, H)).astype(F32)
+    ids = np.array([3, 0, V - 1, V, 7], np.int64)  # V: outside the table
+    xe, he = f.embed_rmsnorm(cu.dev(ids), cu.dev(emb), cu.dev(w), 1e-6)
+    xe, he = xe.cpu().numpy(), he.cpu().numpy()
+    ok = ids < V
+    assert np.array_equal(xe[ok], emb[ids[ok]])
+    assert _rel(he[ok], ofo.rmsnorm_f64(emb[ids[ok]], w, 1e-6)) < TOL
+    assert np.isnan(xe[~ok]).all() and np.isnan(he[~ok]).all()
+    if H % 128 == 0:
+        inv = cu.dev((rng.random(H) + 0.5).astype(F32))
+        xa, xb = cu.dev(x), cu.dev(x)
+        h = f.add_rmsnorm_(xa, cu.dev(r), cu.dev(w), 1e-6)
+        xf = f.add_rmsnorm_xfrag_(xb, cu.dev(r), cu.dev(w), inv, 1e-6)
+        assert torch.equal(xa, xb)
+        assert torch.equal(xf, cu.split_fragments(h, inv))
+
+
 @pytest.mark.parametrize("T,I", [(2, 300), (4, 3072)])
 def test_silu_mul(gpu, fg, T, I):
     gu = fg[f"silu_T{T}_I{I}_gu"]
