@@ -840,6 +840,16 @@ def profile_only(torch, dev, what: str) -> int:
         gemv = load_int8_gemv()
         for i in range(16):
             gemv.int8_linear_prefill(x, *qs[i % 2])
+    elif what == "prefill3":  # config 3's three GEMMs (qkv, gate_up, down), M = 2048, 16 each
+        g = torch.Generator(device=dev).manual_seed(4)
+        gemv = load_int8_gemv()
+        for N, K in ((6144, 2048), (16384, 2048), (2048, 8192)):
+            x = torch.randn(2048, K, device=dev, generator=g)
+            qs = [load_quant().int8_quantize(torch.randn(N, K, device=dev, generator=g) * 0.02)
+                  for _ in range(2)]
+            for i in range(16):
+                gemv.int8_linear_prefill(x, *qs[i % 2])
+            del x, qs
     elif what == "gemm4":  # config 5's batched int4 linear: qkv 1024->4096 at 64 rows, packed
         N, K = SHAPES["qkv"]
         g = torch.Generator(device=dev).manual_seed(5)
@@ -911,7 +921,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
     ap.add_argument("--only", choices=["gemv", "gemv4", "gemm4", "gemm16", "attention", "prefill",
-                                       "lmhead", "copy",
+                                       "prefill3", "lmhead", "copy",
                                        "c5step", "c5step1"],
                     help="profiling run: only launch that kernel (64 times) and exit")
     args = ap.parse_args()
