@@ -414,8 +414,10 @@ print("binding ok")
 
 @pytest.mark.parametrize("case", ["rocm", "no-device", "no-package"])
 def test_reference_binding_from_integration_doc(tmp_path, case):
-    """INTEGRATION.md's binding block, appended verbatim to a stub package named ``llmserve``
-    (laid out as the reference's kernels/__init__.py, kernels/__init__.py:19-72), loads this
+    """The documented reference-side binding block (the one ``python`` block of the
+    repository's integration guide that defines ``_mi355x``), appended verbatim to a stub
+    package named ``llmserve`` (laid out as the reference's kernels/__init__.py,
+    kernels/__init__.py:19-72), loads this
     build under its alias and returns its namespaces on a ROCm host with no recursion; with no
     device, or no package at the configured path, the reference's own loaders answer."""
     import re
