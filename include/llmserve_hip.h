@@ -152,9 +152,14 @@ int llmserve_int4_gemm_pack(const uint8_t* nibbles, const float* g_scale, const 
  * arithmetic up to summation order, with the decode-batch kernel, whose wavefronts issue all loads of their 1-3 K blocks before the first product.
  * Any M, N >= 1; K and group_size multiples of 128. x, inv_act_scale and the packed weight
  * 16-byte aligned; `workspace` (16-byte aligned) holds
- * llmserve_int4_linear_gemm_packed_workspace_bytes(M, K) bytes.
+ * llmserve_int4_linear_gemm_packed_workspace_bytes(M, K) bytes. Up to 16 rows, a narrow output
+ * (whose tiles alone leave most CUs idle) splits its K blocks across workgroups into
+ * llmserve_int4_packed_splits(M, N, K) planes (the first in y, the others in the workspace),
+ * added in plane order by a second launch: the planes, and so the result, are those of
+ * llmserve_int4_linear_gemm_xfrag_split with that split count on the same x', bit for bit.
  */
 int64_t llmserve_int4_linear_gemm_packed_workspace_bytes(int64_t M, int64_t K);
+int64_t llmserve_int4_packed_splits(int64_t M, int64_t N, int64_t K);
 int llmserve_int4_linear_gemm_packed(const float* x, const float* inv_act_scale /* nullable */,
                                      const void* packed, float* y, int64_t M, int64_t N,
                                      int64_t K, int64_t group_size, void* workspace,
@@ -165,8 +170,8 @@ int llmserve_int4_linear_gemm_packed(const float* x, const float* inv_act_scale 
  * lo pieces in wavefront order, then fp32 sums of x' over every 128-channel block; rows up to M
  * rounded to 16, the extra rows zero). llmserve_int4_xfrag_bytes(M, K) bytes, 16-byte aligned.
  * Written by llmserve_int4_xfrag_split (the split pass of llmserve_int4_linear_gemm_packed
- * above 16 rows; up to 16 rows that entry point builds the same values inside its one launch
- * and leaves its workspace unused) or by the fused producers below (bit-identical for the same
+ * above 16 rows; up to 16 rows that entry point builds the same values inside its GEMM launch,
+ * using its workspace only for K planes) or by the fused producers below (bit-identical for the same
  * x'); read by llmserve_int4_linear_gemm_xfrag, which is llmserve_int4_linear_gemm_packed on
  * given fragments. No counterpart in the reference: they fuse Int4Linear's
  * `x * inv_act_scale` (quant.py:141) into the producing kernel.

@@ -549,7 +549,10 @@ void int4_gemm_wide(Int4GemmArgs a, int mtiles, int groups) {
 // four lane shuffles). The products and their accumulation are int4_gemm_lat's.
 // Work: S wavefronts split the K blocks of NT 16-column tiles (one block per wavefront and
 // round); NT = 1 gives each workgroup one tile of a slab, so a narrow output (N = 1024:
-// 16 slabs) spreads over 64 workgroups instead of 16.
+// 16 slabs) spreads over 64 workgroups instead of 16. With bpp < K / 128 the K blocks are
+// split across workgroups as well: plane p (blocks [p bpp, (p + 1) bpp)) goes to y (p = 0)
+// or ys + (p - 1) M N, with int4_gemm_lat's per-plane order (the fragment path's K-split
+// planes, bit for bit), and plane_sum_kernel adds the planes in order.
 // v_permlane32_swap: the upper 32 lanes of a trade places with the lower 32 of b.
 __device__ __forceinline__ void swap_halves32(float& a, float& b) {
   const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a),
@@ -571,8 +574,10 @@ struct Int4GemmXArgs {
   const float* inv;  // [K] AWQ pre-scale (INV only)
   const uint8_t* w;  // packed nibbles
   const float* s;    // packed scales
-  float* y;          // [M, N]
+  float* y;          // [M, N]: the output, or plane 0 when bpp < K / 128
+  float* ys;         // planes 1, 2, ... [planes - 1, M, N] (bpp < K / 128)
   int M, N, K, bpg;
+  int bpp;           // K blocks per plane
 };
 
 template <int S, int NT, bool INV, bool CO>
@@ -580,12 +585,16 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
   extern __shared__ f32x4 red[];  // S > 1: [S][NT][64]
   constexpr int kUnits = kNT / NT;  // workgroups per slab
   const int lane = threadIdx.x % kWave, ks = threadIdx.x / kWave;
-  const int slab = blockIdx.x / kUnits, u0 = (blockIdx.x % kUnits) * NT;
+  const int slabs = (a.N + kCols - 1) / kCols;
+  const int per_plane = slabs * kUnits;
+  const int plane = blockIdx.x / per_plane, wg = blockIdx.x % per_plane;
+  const int slab = wg / kUnits, u0 = (wg % kUnits) * NT;
   const int n0 = slab * kCols + 16 * u0;
   if (n0 >= a.N) return;  // whole workgroup: no barrier is reached
   const int fr = lane % 16, fc = lane / 16;
   const int nblk = a.K / kBlk;
-  const int slabs = (a.N + kCols - 1) / kCols;
+  const int b0 = plane * a.bpp, b1 = min(b0 + a.bpp, nblk);  // this plane's blocks
+  float* y = plane == 0 ? a.y : a.ys + static_cast<int64_t>(plane - 1) * a.M * a.N;
   // rows past M repeat row M - 1 (in bounds): each output row depends on its own x row
   // only, and theirs are not stored
   const float* xrow =
@@ -594,8 +603,8 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
   f32x4 acc[NT];
 #pragma unroll
   for (int u = 0; u < NT; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int base = 0; base < nblk; base += S) {
-    const int b = min(base + ks, nblk - 1);  // clamped: loads stay unconditional
+  for (int base = b0; base < b1; base += S) {
+    const int b = min(base + ks, b1 - 1);  // clamped: loads stay unconditional
     const int g = b / a.bpg;
     u32x4 w[NT];
     const uint8_t* wt = a.w + ((static_cast<int64_t>(slab) * nblk + b) * kNT + u0) * kPkTile + 16 * lane;
@@ -665,7 +674,7 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
     f32x4 xs;
 #pragma unroll
     for (int r = 0; r < 4; ++r) xs[r] = __shfl(rs, 4 * fc + r, kWave);  // rows 4 fc + r
-    const float on = base + ks < nblk ? 1.f : 0.f;
+    const float on = base + ks < b1 ? 1.f : 0.f;
 #pragma unroll
     for (int u = 0; u < NT; ++u) {
       f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -703,9 +712,28 @@ __global__ __launch_bounds__(S * kWave) void int4_gemm_x(Int4GemmXArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = 4 * fc + r;
-      if (m < a.M) a.y[static_cast<int64_t>(m) * a.N + n] = v[r];
+      if (m < a.M) y[static_cast<int64_t>(m) * a.N + n] = v[r];
     }
   }
+}
+
+// y = y + ys[0] + ... + ys[P - 2] over n elements (plane 0 is y itself), added in plane
+// order (the fragment path's plane consumers add them in the same order); the planes' loads
+// go out together (P <= 4).
+__global__ __launch_bounds__(256) void plane_sum_kernel(float* __restrict__ y,
+                                                        const float* __restrict__ ys, int64_t n,
+                                                        int P) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  float t[4];
+  t[0] = y[i];
+#pragma unroll
+  for (int p = 1; p < 4; ++p) t[p] = p < P ? ys[(p - 1) * n + i] : 0.f;
+  float v = t[0];
+#pragma unroll
+  for (int p = 1; p < 4; ++p)
+    if (p < P) v += t[p];
+  y[i] = v;
 }
 
 // Wavefronts of a workgroup whose wavefronts take one K block per round: the fewest rounds of
@@ -720,8 +748,8 @@ int one_block_waves(int nb) {
 }
 
 template <int S, int NT, bool CO>
-void launch_x(const Int4GemmXArgs& a, int64_t slabs, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(slabs * (kNT / NT))), block(S * kWave);
+void launch_x(const Int4GemmXArgs& a, int64_t slabs, int planes, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(slabs * (kNT / NT) * planes)), block(S * kWave);
   const size_t lds = S > 1 ? static_cast<size_t>(S) * NT * kWave * sizeof(f32x4) : 0;
   if (a.inv)
     lsh::launch(int4_gemm_x<S, NT, true, CO>, grid, block, lds, st, true, a);
@@ -738,14 +766,16 @@ void launch_x(const Int4GemmXArgs& a, int64_t slabs, hipStream_t st) {
 // against 319).
 // S = one_block_waves(nb) (idle wavefronts of a last round would still convert x): K = 3072
 // (24 blocks) takes two rounds of 12, 16 rows 292 -> 302 GB/s.
+// planes > 1: the K blocks split across workgroups (a.bpp blocks each), S from a.bpp.
 // Returns false (nothing launched) for a configuration without an instance.
-bool launch_x_tile(const Int4GemmXArgs& a, int64_t slabs, int nb, hipStream_t st) {
-  const int S = one_block_waves(nb);
+bool launch_x_tile(const Int4GemmXArgs& a, int64_t slabs, int planes, hipStream_t st) {
+  const int S = one_block_waves(a.bpp);
   const int NT = slabs * kNT <= 512 ? 1 : 2;
   const bool co = a.M > 8;
 #define LSH_X(s, nt)                                                                        \
   if (S == s && NT == nt) {                                                                 \
-    co ? launch_x<s, nt, true>(a, slabs, st) : launch_x<s, nt, false>(a, slabs, st);        \
+    co ? launch_x<s, nt, true>(a, slabs, planes, st)                                        \
+       : launch_x<s, nt, false>(a, slabs, planes, st);                                      \
     return true;                                                                            \
   }
   LSH_X(4, 1) LSH_X(4, 2) LSH_X(8, 1) LSH_X(8, 2) LSH_X(12, 1) LSH_X(12, 2) LSH_X(16, 1)
@@ -755,6 +785,36 @@ bool launch_x_tile(const Int4GemmXArgs& a, int64_t slabs, int nb, hipStream_t st
 }
 
 int64_t xsum_rows(int64_t M) { return (M + kRows - 1) / kRows * kRows; }
+
+int device_cus() {
+  int cus = 256, dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
+      cus = c;
+  }
+  return cus;
+}
+
+// K planes of the one-launch GEMM (one 16-row tile): a narrow output, whose tiles alone leave
+// most CUs idle and whose every workgroup converts x for all its K blocks, splits the blocks
+// across workgroups: the largest P <= 4 with tiles x P <= CUs, at least 4 blocks in every
+// plane, and planes 1 .. P - 1 (M x N floats each; plane 0 is the output) inside the fragment
+// workspace the call takes anyway. Config 2's o_proj (16 K blocks) and down_proj (24) at 16
+// rows: 4 planes each.
+int packed_planes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > kRows || K % kBlk != 0) return 1;
+  const int64_t nb = K / kBlk, slabs = pk_slabs(N);
+  const int64_t tiles = slabs * (slabs * kNT <= 512 ? kNT : kNT / 2);
+  const int64_t cus = device_cus(), room = lsh::frag_bytes(M, K);
+  for (int P = 4; P >= 2; --P) {  // plane_sum_kernel adds at most 4
+    const int64_t bpp = (nb + P - 1) / P;
+    if (tiles * P <= cus && bpp >= 4 && (nb + bpp - 1) / bpp == P &&
+        (P - 1) * M * N * static_cast<int64_t>(sizeof(float)) <= room)
+      return P;
+  }
+  return 1;
+}
 
 template <int KB, int S>
 void launch_lat_ks(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int planes, int bpp,
@@ -921,6 +981,10 @@ extern "C" int64_t llmserve_int4_linear_gemm_packed_workspace_bytes(int64_t M, i
   return lsh::frag_bytes(M, K);
 }
 
+extern "C" int64_t llmserve_int4_packed_splits(int64_t M, int64_t N, int64_t K) {
+  return packed_planes(M, N, K);
+}
+
 extern "C" int64_t llmserve_int4_xfrag_bytes(int64_t M, int64_t K) {
   if (M <= 0 || K <= 0 || K % kBlk) return 0;
   return lsh::frag_bytes(M, K);
@@ -953,13 +1017,19 @@ extern "C" int llmserve_int4_linear_gemm_packed(const float* x, const float* inv
   const int64_t mtiles = (M + kRows - 1) / kRows;
   const int mp = static_cast<int>(xsum_rows(M));
   const uint8_t* wpk0 = static_cast<const uint8_t*>(packed);
-  if (mtiles == 1) {  // one row tile: fragments built inside the GEMM, one launch
+  if (mtiles == 1) {  // one row tile: fragments built inside the GEMM
+    // narrow outputs: K planes in the workspace (unused by this path otherwise), then their sum
+    const int planes = packed_planes(M, N, K);
+    float* ys = static_cast<float*>(workspace);  // planes 1 ..
     Int4GemmXArgs xa{x, inv_act_scale, wpk0,
                      reinterpret_cast<const float*>(wpk0 + (pk_weight_bytes(N, K) + 255) / 256 * 256),
-                     y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
-                     static_cast<int>(group_size / kBlk)};
-    LSH_CHECK(launch_x_tile(xa, pk_slabs(N), nb, st),
+                     y, ys, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
+                     static_cast<int>(group_size / kBlk), (nb + planes - 1) / planes};
+    LSH_CHECK(launch_x_tile(xa, pk_slabs(N), planes, st),
               "int4_linear_gemm_packed: no kernel instance for K=%lld", (long long)K);
+    if (planes > 1)
+      lsh::launch(plane_sum_kernel, dim3(static_cast<unsigned>((M * N + 255) / 256)), dim3(256),
+                  0, st, true, y, static_cast<const float*>(ys), M * N, planes);
     return lsh::launch_status("int4_linear_gemm_packed");
   }
   __bf16* xf = static_cast<__bf16*>(workspace);

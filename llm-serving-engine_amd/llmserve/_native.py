@@ -61,6 +61,7 @@ C_SIGNATURES: dict[str, tuple[object, list]] = {
     "llmserve_int4_xfrag_split": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "llmserve_int4_linear_gemm_xfrag": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "llmserve_int4_xfrag_splits": (_I64, [_I64, _I64, _I64]),
+    "llmserve_int4_packed_splits": (_I64, [_I64, _I64, _I64]),
     "llmserve_int4_linear_gemm_xfrag_split": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "llmserve_rmsnorm_xfrag": (_I32, [_P, _P, _P, _P, _I64, _I64, _F32, _P]),
     "llmserve_add_rmsnorm_xfrag": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _F32, _P]),

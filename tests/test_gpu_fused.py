@@ -288,10 +288,12 @@ def test_xfrag_rejects_bad_shapes(gpu):
 @pytest.mark.parametrize("T", [1, 5, 16])
 @pytest.mark.parametrize("awq", [True, False])
 def test_one_tile_packed_gemm_equals_fragment_path(gpu, T, awq):
-    """Up to 16 rows int4_linear_gemm_packed builds the fragments inside its one launch; they
+    """Up to 16 rows int4_linear_gemm_packed builds the fragments inside its GEMM launch; they
     and the products are the split pass's, so the result equals the fragment consumer on the
     fragments a norm or silu * up kernel writes, bit for bit (same per-wavefront blocks and
-    the same fixed-order sum of the wavefronts at these shapes)."""
+    the same fixed-order sum of the wavefronts at these shapes). A narrow output (down_proj
+    here) splits its K blocks into planes: it equals the K-split fragment consumer's planes
+    added in order."""
     from llmserve.kernels import load_int8_gemv
 
     f, lin = fo(), load_int8_gemv()
@@ -310,5 +312,10 @@ def test_one_tile_packed_gemm_equals_fragment_path(gpu, T, awq):
     pkd, invd = _int4_packed(1024, I, 4, awq)
     gu = cu.dev(rng.standard_normal((T, 2 * I)).astype(F32))
     ref = lin.int4_linear_gemm_packed(f.silu_mul(gu), pkd, 1024, 128, invd)
-    got = f.int4_linear_gemm_xfrag(f.silu_mul_xfrag(gu, invd), pkd, T, 1024, I, 128)
+    P = int(cu.capi().llmserve_int4_packed_splits(T, 1024, I))
+    assert P == 4
+    planes = f.int4_linear_gemm_xfrag_split(f.silu_mul_xfrag(gu, invd), pkd, T, 1024, I, 128, P)
+    got = planes[0].clone()
+    for p in range(1, P):
+        got = got + planes[p]
     assert torch.equal(got, ref)

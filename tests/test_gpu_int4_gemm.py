@@ -220,6 +220,31 @@ def test_packed_gemm_split_planes(gpu, M, N, K):
         _gemm_xfrag_split(xf, packed, M, N, K, 128, 9)
 
 
+@pytest.mark.parametrize("M,N,K,g", [(16, 1024, 2048, 128), (16, 1024, 3072, 128),
+                                     (5, 1024, 2048, 128), (1, 1024, 3072, 128),
+                                     (9, 200, 1536, 256), (16, 64, 3200, 640)])
+def test_one_tile_k_planes(gpu, M, N, K, g):
+    """Up to 16 rows a narrow output splits its K blocks over workgroups (config 2's o_proj
+    and down_proj at 16 rows: 4 planes each; planes past the first must fit the workspace the
+    call takes anyway): the result is within TOL of float64 and equals, bit for bit, the
+    K-split fragment consumer's planes on the same x' added in order. The wide shapes keep one
+    plane."""
+    L = cu.capi()
+    assert [L.llmserve_int4_packed_splits(16, n, k) for n, k in QWEN] == \
+        [1 if n > 1024 else 4 for n, k in QWEN]
+    P = int(L.llmserve_int4_packed_splits(M, N, K))
+    assert P > 1
+    x, nib, gs, gz, inv = _case(M, N, K, g, 5 * M + N + K)
+    packed = cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), g)
+    y = cu.int4_linear_gemm_packed(cu.dev(x), packed, N, g, cu.dev(inv))
+    cu.assert_rel_close(y, mr.int4_linear_f64(x, nib, gs, gz, g, inv), TOL, f"M={M} {N}x{K}")
+    planes = _gemm_xfrag_split(cu.split_fragments(cu.dev(x), cu.dev(inv)), packed, M, N, K, g, P)
+    s = planes[0].clone()
+    for p in range(1, P):
+        s = s + planes[p]
+    assert torch.equal(y, s), f"M={M} {N}x{K}: one-launch planes != fragment planes"
+
+
 def test_packed_gemm_rejects_bad_shapes(gpu):
     x, nib, gs, gz, _ = _case(20, 48, 256, 64, 3, awq=False)
     with pytest.raises(RuntimeError, match="multiples of 128"):
