@@ -1097,16 +1097,19 @@ extern "C" int llmserve_int4_linear_gemm_xfrag(const void* xfrag, const void* pa
   return lsh::launch_status("int4_linear_gemm_xfrag");
 }
 
-// K planes for a decode-batch linear on fragments: enough that the slab tiles of all planes
-// give half the CUs a workgroup, with at least 4 blocks of K per plane; 1 when the slabs alone
-// do (qkv, gate_up at Qwen3-0.6B shapes). o_proj and down_proj at 64 rows (N = 1024: 64 slab
-// tiles) take 2: the residual norm that adds the planes reads each of them, and the config-5
-// step is faster with 2 than with 4 (17.99 k against 17.6 k tok/s) or 1 (17.4 k).
+// K planes for a decode-batch linear on fragments: P doubles while the slab tiles of all
+// planes still fit the CUs and every plane keeps at least 4 blocks of K; 1 when the slabs
+// alone fill the GPU (qkv, gate_up at Qwen3-0.6B shapes). o_proj and down_proj at 64 rows
+// (N = 1024: 64 slab tiles) take 4. The residual norm that adds the planes loads them all in
+// one round: the config-5 step runs 18.84 k tok/s with 4 planes against 18.64 k with 2 and
+// 18.72 k with 3 (with a norm that read the planes one after another, 2 beat 4: 17.99 k
+// against 17.6 k).
 extern "C" int64_t llmserve_int4_xfrag_splits(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K < kBlk) return 1;
   const int64_t tiles = pk_slabs(N) * ((M + kRows - 1) / kRows), nb = K / kBlk;
+  const int64_t cus = device_cus();
   int64_t P = 1;
-  while (P < kMaxPlanes && tiles * P < 128 && nb >= 4 * 2 * P) P *= 2;
+  while (P < kMaxPlanes && tiles * 2 * P <= cus && nb >= 4 * 2 * P) P *= 2;
   return P;
 }
 

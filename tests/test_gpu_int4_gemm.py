@@ -193,10 +193,10 @@ def test_packed_gemm_split_planes(gpu, M, N, K):
     xf = cu.split_fragments(cu.dev(x), cu.dev(inv))
     nb = K // 128
     step_p = cu.capi().llmserve_int4_xfrag_splits(M, N, K)
-    # the rule: double P while the slab tiles of all planes give fewer than half the CUs (128)
-    # a workgroup and each plane keeps >= 4 blocks
+    # the rule: double P while the slab tiles of all planes still fit the CUs (256) and each
+    # plane keeps >= 4 blocks
     tiles, want = (N // 64) * -(-M // 16), 1
-    while want < 8 and tiles * want < 128 and nb >= 8 * want:
+    while want < 8 and tiles * 2 * want <= 256 and nb >= 8 * want:
         want *= 2
     assert step_p == want
     full = mr.int4_linear_f64(x, nib, gs, gz, 128, inv)
