@@ -786,14 +786,19 @@ bool launch_x_tile(const Int4GemmXArgs& a, int64_t slabs, int planes, hipStream_
 
 int64_t xsum_rows(int64_t M) { return (M + kRows - 1) / kRows * kRows; }
 
+// CUs of the current device (cached per device: the linears ask on every call).
 int device_cus() {
-  int cus = 256, dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess) {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
     int c = 0;
-    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
-      cus = c;
+    cached[dev] = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) ==
+                              hipSuccess && c > 0
+                      ? c
+                      : 256;
   }
-  return cus;
+  return cached[dev];
 }
 
 // K planes of the one-launch GEMM (one 16-row tile): a narrow output, whose tiles alone leave
@@ -838,12 +843,7 @@ bool launch_lat(const Int4GemmArgs& a, int64_t slabs, int64_t mtiles, int nb_all
   // very wide outputs (at least 256 slabs) with K = 512 or 1024: int4_gemm_wide, about two
   // workgroups per CU
   if (planes == 1 && (nb_all == 4 || nb_all == 8) && slabs >= 256 && slabs * mtiles >= kWideTiles) {
-    int cus = 256, dev = 0;
-    if (hipGetDevice(&dev) == hipSuccess) {
-      int c = 0;
-      if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
-        cus = c;
-    }
+    const int cus = device_cus();
     int64_t groups = (2 * cus + mtiles - 1) / mtiles;
     groups = std::min<int64_t>(groups, slabs / 2);
     groups = std::max<int64_t>(8, (groups + 7) / 8 * 8);
