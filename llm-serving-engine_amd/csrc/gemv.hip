@@ -61,20 +61,18 @@ __device__ __forceinline__ u32x4 load16(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
-// Channels 2b (low nibble) and 2b+1 (high nibble) of byte b, for the 4 bytes of u.
 // Eight nibbles (channels 2b: low nibble of byte b, 2b + 1: high nibble) to fp32: the two
-// masked words, then one byte-select conversion per value (left to itself the compiler
-// extracts each nibble with a bit-field extract first: one more instruction per value).
+// masked words, then one byte-select conversion (v_cvt_f32_ubyteN) per value. The empty asm
+// hides the masks from the compiler, which would otherwise extract each nibble with a
+// bit-field extract first (one more instruction per value); it emits nothing.
 __device__ __forceinline__ void unpack_nibbles(uint32_t u, float* q) {
-  const uint32_t lo = u & 0x0f0f0f0fu, hi = (u >> 4) & 0x0f0f0f0fu;
-  asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(q[0]) : "v"(lo));
-  asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(q[1]) : "v"(hi));
-  asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(q[2]) : "v"(lo));
-  asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(q[3]) : "v"(hi));
-  asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(q[4]) : "v"(lo));
-  asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(q[5]) : "v"(hi));
-  asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(q[6]) : "v"(lo));
-  asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(q[7]) : "v"(hi));
+  uint32_t lo = u & 0x0f0f0f0fu, hi = (u >> 4) & 0x0f0f0f0fu;
+  asm("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    q[2 * b] = static_cast<float>((lo >> (8 * b)) & 0xffu);
+    q[2 * b + 1] = static_cast<float>((hi >> (8 * b)) & 0xffu);
+  }
 }
 
 __device__ __forceinline__ void unpack_int8(uint32_t u, float* q) {
