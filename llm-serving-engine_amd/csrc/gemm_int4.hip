@@ -88,9 +88,13 @@ struct Int4GemmArgs {
   int M, N, K, G, bpg, mp;  // bpg: 128-channel blocks per quantization group
 };
 
-// 8 nibbles (channels 2e low, 2e + 1 high of byte e) -> 8 bf16, exact.
+// 8 nibbles (channels 2e low, 2e + 1 high of byte e) -> 8 bf16, exact: each value one
+// byte-select conversion (v_cvt_f32_ubyteN) of the two masked words, then two per packed
+// conversion. The empty asm hides the masks from the compiler, which would otherwise
+// extract each nibble with a bit-field extract first; it emits nothing.
 __device__ __forceinline__ bf16x8 nibbles_bf16(uint32_t wd) {
-  const uint32_t lo = wd & 0x0f0f0f0fu, hi = (wd >> 4) & 0x0f0f0f0fu;
+  uint32_t lo = wd & 0x0f0f0f0fu, hi = (wd >> 4) & 0x0f0f0f0fu;
+  asm("" : "+v"(lo), "+v"(hi));
   bf16x8 r;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
