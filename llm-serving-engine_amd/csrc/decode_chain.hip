@@ -266,7 +266,10 @@ __device__ __forceinline__ void chunk_terms(const Chunk& f, int c, const float* 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t u = f.w[i];
-    const uint32_t lo = u & 0x0f0f0f0fu, hi = (u >> 4) & 0x0f0f0f0fu;
+    uint32_t lo = u & 0x0f0f0f0fu, hi = (u >> 4) & 0x0f0f0f0fu;
+    // hides the masks: each value is then one byte-select conversion (v_cvt_f32_ubyteN)
+    // instead of a bit-field extract and a conversion; the asm emits nothing
+    asm("" : "+v"(lo), "+v"(hi));
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       q[8 * i + 2 * b] = static_cast<float>((lo >> (8 * b)) & 0xffu);
