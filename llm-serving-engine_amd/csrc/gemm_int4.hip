@@ -761,10 +761,19 @@ void launch_x(const Int4GemmXArgs& a, int64_t slabs, int planes, hipStream_t st)
     lsh::launch(int4_gemm_x<S, NT, false, CO>, grid, block, lds, st, true, a);
 }
 
+int device_cus();
+
+// Tiles per workgroup of the one-tile GEMM: one while the output's 16-column tiles fit the
+// CUs, two beyond (a workgroup converts its x blocks once for both tiles; with one tile per
+// workgroup config 2's gate_up, 384 tiles, puts two workgroups on half the CUs).
+int x_tile_nt(int64_t slabs) { return slabs * kNT > device_cus() ? 2 : 1; }
+
 // S: wavefronts to cover the K blocks in one round (up to 16: K = 2048; K = 3072 takes two
-// rounds); NT: tiles per workgroup. More workgroups beat less redundant conversion: config 2
-// at 16 rows (the four Qwen3-0.6B shapes, 112 launches) 273 GB/s with one tile per
-// workgroup, 276 with two, 219 with a whole slab (four); 5 rows 324 / 307 / 221.
+// rounds); NT: tiles per workgroup (x_tile_nt). More workgroups beat less redundant conversion
+// while they fit the CUs: config 2 at 16 rows (the four Qwen3-0.6B shapes, 112 launches) 273
+// GB/s with one tile per workgroup for all shapes, 276 with two, 219 with a whole slab (four);
+// 5 rows 324 / 307 / 221. Two tiles only where one would put two workgroups on some CUs
+// (gate_up, 384 tiles: 8.88 -> 6.52 us per call, 348 -> 375 GB/s).
 // CO (coalesced x loads and the lane transpose) above 8 rows: 16 rows 279 -> 292 GB/s;
 // at 1-8 rows the direct loads touch no more lines and skip the transpose (8 rows 330
 // against 319).
@@ -774,7 +783,7 @@ void launch_x(const Int4GemmXArgs& a, int64_t slabs, int planes, hipStream_t st)
 // Returns false (nothing launched) for a configuration without an instance.
 bool launch_x_tile(const Int4GemmXArgs& a, int64_t slabs, int planes, hipStream_t st) {
   const int S = one_block_waves(a.bpp);
-  const int NT = slabs * kNT <= 512 ? 1 : 2;
+  const int NT = x_tile_nt(slabs);
   const bool co = a.M > 8;
 #define LSH_X(s, nt)                                                                        \
   if (S == s && NT == nt) {                                                                 \
@@ -814,7 +823,7 @@ int device_cus() {
 int packed_planes(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || M > kRows || K % kBlk != 0) return 1;
   const int64_t nb = K / kBlk, slabs = pk_slabs(N);
-  const int64_t tiles = slabs * (slabs * kNT <= 512 ? kNT : kNT / 2);
+  const int64_t tiles = slabs * (kNT / x_tile_nt(slabs));
   const int64_t cus = device_cus(), room = lsh::frag_bytes(M, K);
   for (int P = 4; P >= 2; --P) {  // plane_sum_kernel adds at most 4
     const int64_t bpp = (nb + P - 1) / P;
