@@ -144,10 +144,13 @@ def test_packed_gemm_qwen_shapes(gpu, M, N, K):
 
 @pytest.mark.parametrize("M,N,K,g", [(1, 32, 512, 128), (5, 77, 256, 128), (64, 1000, 1536, 256),
                                      (33, 16, 128, 128), (100, 160, 4096, 128), (300, 72, 640, 128),
-                                     (64, 151936 // 8, 1024, 128), (48, 64, 3200, 640)])
+                                     (64, 151936 // 8, 1024, 128), (48, 64, 3200, 640),
+                                     (16, 4200, 1024, 128), (7, 4213, 512, 256)])
 def test_packed_gemm_tails(gpu, M, N, K, g):
     """Any N (packed slabs pad to 64 rows), K past one round of 24 blocks (4096, 3200),
-    groups of several blocks, row tails, a wide output, no AWQ scale on odd M."""
+    groups of several blocks, row tails, a wide output, no AWQ scale on odd M. Up to 16 rows,
+    more 16-column tiles than CUs (N = 4200: 264 tiles) run two tiles per workgroup, with a
+    last workgroup whose second tile is past N."""
     x, nib, gs, gz, inv = _case(M, N, K, g, M + N + K + g, awq=(M % 2 == 0))
     packed = cu.int4_gemm_pack(cu.dev(nib), cu.dev(gs), cu.dev(gz), g)
     y = cu.int4_linear_gemm_packed(cu.dev(x), packed, N, g, None if inv is None else cu.dev(inv))
