@@ -553,7 +553,8 @@ void int4_gemm_wide(Int4GemmArgs a, int mtiles, int groups) {
 // four lane shuffles). The products and their accumulation are int4_gemm_lat's.
 // Work: S wavefronts split the K blocks of NT 16-column tiles (one block per wavefront and
 // round); NT = 1 gives each workgroup one tile of a slab, so a narrow output (N = 1024:
-// 16 slabs) spreads over 64 workgroups instead of 16. With bpp < K / 128 the K blocks are
+// 16 slabs) spreads over 64 workgroups instead of 16; NT = 2 where the tiles outnumber the
+// CUs (one x conversion per block serves both tiles). With bpp < K / 128 the K blocks are
 // split across workgroups as well: plane p (blocks [p bpp, (p + 1) bpp)) goes to y (p = 0)
 // or ys + (p - 1) M N, with int4_gemm_lat's per-plane order (the fragment path's K-split
 // planes, bit for bit), and plane_sum_kernel adds the planes in order.
