@@ -55,12 +55,14 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
 // Ranges never straddle two (sequence b, head group hg) units: unit (b, hg) gets
 // n_b = ceil(ctx_b / Q) ranges, numbered unit by unit in (b, hg) order. With a caller's fixed
 // partition size P (the reference's partitions) Q = P and the ranges hold P tokens, the last
-// one the rest. The balanced default equalises the ranges of a unit (ceil(ctx_b / n_b) tokens
-// each) and takes Q between max(ceil(T / W), kMinRange, ceil(max ctx / kcap)), T = NHG *
-// sum_b ctx_b, kcap the partial slots per unit, and ceil(T / (W - units)) (which always fits:
-// each unit rounds up by less than one range) so
-// that the R = NHG * sum_b n_b ranges fit the W resident workgroups: the lower end if it fits,
-// else the feasible end of kPlanSteps bisections. Every workgroup derives the same plan from
+// one the rest. The balanced default chooses Q, a multiple of kMinRange, between
+// max(ceil(T / W), kMinRange, ceil(max ctx / kcap)), T = NHG * sum_b ctx_b, kcap the partial
+// slots per unit, and ceil(T / (W - units)) (which always fits: each unit rounds up by less
+// than one range) so that the R = NHG * sum_b n_b ranges fit the W resident workgroups: the
+// lower end if it fits, else the feasible end of kPlanSteps bisections; its ranges then hold Q
+// tokens as a fixed partition's do. (Ranges equalised within each unit, ceil(ctx_b / n_b)
+// tokens, with Q to the token, measured slower: config 4 57.3-58.9 against 55.7-56.0 us per
+// decode + merge; 64 rows of U[1024, 4096] 73.9-74.7 against 72.1.) Every workgroup derives the same plan from
 // the contexts, with DPP / readlane reductions (no LDS crossbar round trips: the plan is on
 // every range's critical path). A range that started a second unit would pay that unit's
 // start-up (its context, then q and block ids, then the first K/V loads) as dependent round
@@ -164,11 +166,15 @@ __device__ Plan make_plan(const DecodeArgs& a) {
     const int64_t f = (T + (a.W - units) - 1) / (a.W - units);
     uint32_t hi = f < mx ? static_cast<uint32_t>(f) : mx;  // fits
     if (hi < lo) hi = lo;
+    // Q in whole multiples of kMinRange (rounding up keeps a bound feasible: the range count
+    // only falls as Q grows)
+    lo = (lo + kMinRange - 1) / kMinRange * kMinRange;
+    hi = (hi + kMinRange - 1) / kMinRange * kMinRange;
     if (count_ranges(a, lo, p.c0) <= a.W) {
       hi = lo;
     } else {
-      for (int it = 0; it < kPlanSteps && lo + 1 < hi; ++it) {  // (lo infeasible, hi feasible)
-        const uint32_t mid = lo + (hi - lo) / 2;
+      for (int it = 0; it < kPlanSteps && lo + kMinRange < hi; ++it) {  // (lo infeasible, hi feasible)
+        const uint32_t mid = lo + (hi - lo) / kMinRange / 2 * kMinRange;
         if (count_ranges(a, mid, p.c0) <= a.W)
           hi = mid;
         else
@@ -218,7 +224,7 @@ __device__ RangePos find_range(const DecodeArgs& a, const Plan& p, int64_t j) {
       if (rel < 0 || rel >= static_cast<int64_t>(r.n) * a.NHG) break;  // unreachable
       r.hg = static_cast<int>(rel / r.n);
       const uint32_t k = static_cast<uint32_t>(rel - static_cast<int64_t>(r.hg) * r.n);
-      const uint32_t L = p.fixed ? p.Q : (cb - 1) / r.n + 1;
+      const uint32_t L = p.Q;  // ranges of Q tokens, the unit's last one the rest
       const uint32_t t0 = k * L, t1 = t0 + L < cb ? t0 + L : cb;
       r.t0 = static_cast<int>(t0);
       r.t1 = static_cast<int>(t1);
