@@ -350,9 +350,10 @@ int llmserve_lm_head_f32(const float* x, const float* w, float* y, int64_t M, in
  * q fp32 [B,Hq,D]; k/v_cache int8 [num_slots,Hk,D]; k/v_scale fp32 [num_slots,Hk];
  * block_tables int64 [B,max_blocks]; context_lens int64 [B] -> out fp32 [B,Hq,D].
  * The context is split, as the reference's partitions are, into work ranges whose partial
- * (max, sum, acc) are merged: partition_size = tokens per range; 0 cuts each (sequence, kv
- * head group) into equal ranges, sized so that the whole batch's ranges fill the GPU's
- * resident workgroups once (ranges never straddle two sequences; a sequence more than a few
+ * (max, sum, acc) are merged: partition_size = tokens per range; 0 picks the range size
+ * itself, the smallest multiple of 64 tokens whose ranges fit the GPU's resident workgroups
+ * once, and cuts each (sequence, kv head group) into ranges of that size, the last one the
+ * rest (ranges never straddle two sequences; a sequence more than a few
  * times the batch's mean context gets wider ranges, so that its partials fit a workspace
  * bounded by the grid rather than by max_blocks). Block ids outside [0, num_slots/block_size) contribute nothing;
  * context lengths are clamped to max_blocks*block_size. A zero context yields NaN, as the
