@@ -114,6 +114,26 @@ def test_baseline_config4_size(gpu):
     assert torch.equal(out3, out)
 
 
+@pytest.mark.parametrize("B,lo,hi", [(32, 512, 8192), (64, 1024, 4096), (7, 1, 3000)])
+def test_balanced_plan_is_a_64_token_partition(gpu, B, lo, hi):
+    """The default split (partition_size 0) cuts every (sequence, kv head group) into ranges
+    of Q tokens, the last one the rest, with Q a multiple of 64 chosen from the contexts: its
+    output equals, bit for bit, that of a fixed partition size of some multiple of 64 (same
+    ranges, same per-range arithmetic, the partials merged in the same order)."""
+    c = make_case(B + lo, B, 16, 8, 128, 16, lo, hi)
+    args = [cu.dev(c[k]) for k in ("q", "kq", "vq", "ks", "vs", "bt", "cl")]
+    qm = cu.dev(c["q_mult"])
+    sc = 128 ** -0.5
+    out = cu.paged_decode_int8(*args, 16, sc, 0, qm)
+    ref = ocpu.paged_decode_int8(c["q"], c["kq"], c["vq"], c["ks"], c["vs"], c["bt"], c["cl"], 16,
+                                 sc, 0, c["q_mult"])
+    cu.assert_rel_close(out, ref, 2 * TOL, f"B={B}: balanced plan vs C restatement")
+    top = -(-int(c["cl"].max()) // 64) * 64
+    same = [P for P in range(64, top + 65, 64)
+            if torch.equal(cu.paged_decode_int8(*args, 16, sc, P, qm), out)]
+    assert same, f"B={B}: no 64-token multiple reproduces the balanced plan"
+
+
 def test_skewed_batch_within_unit_slots(gpu):
     """One long sequence among 255 short ones: the workspace holds a few times each unit's
     fair share of ranges, so the plan widens the ranges until the long unit fits; the result
